@@ -1,0 +1,898 @@
+// trie_attn.hip — trie-scoped attention (forward, softmax, backward) for
+// MI355X / gfx950, behind the C ABI of include/agpt_attn.h.
+//
+// Data layout in HBM (all row-major, rows in DFS preorder so every subtree is
+// a contiguous row range):
+//   Q, K, V, O, dO : [T, D] fp32 or bf16     lse : [T, H] fp32
+//   dQ, dK, dV     : [T, D] fp32
+//   plan tables    : parent, depth, subtree_end [T] int32;
+//                    tile_pref_off [n_tiles+1], tile_prefix [Σ A_t] int32
+//   workspace      : Pk, Pv [Σ A_t, D] fp32 (per-tile partial dK/dV of the
+//                    tile's out-of-tile ancestors), Ck, Cv [n_chunks, maxD, D]
+//
+// A tile is kTileQ consecutive rows [s, e). Every ancestor of a row in the
+// tile that lies outside the tile is an ancestor of s (preorder), so a tile
+// needs only its own rows plus the A_t = depth(s)-1 "prefix" rows on the path
+// of s (tile_prefix, ordered by depth). Forward and the dQ half of backward
+// walk each query's path through LDS tables (in-tile parent links, then the
+// prefix list). dK/dV are key-centric: key a collects over the contiguous
+// query range [max(a,s), min(end(a),e)) of the tile; keys whose subtree ends
+// inside their own tile are final after one kernel, the others ("open" keys)
+// are finished by a fixed-order segmented reduction over the later tiles'
+// prefix partials (trie_bwd_chunk_kernel + trie_bwd_reduce_kernel). No
+// floating-point atomics: results are bitwise reproducible.
+
+#include "common.h"
+#include "../../include/agpt_attn.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace agpt;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+  do {                                                                                     \
+    hipError_t _e = (expr);                                                                \
+    if (_e != hipSuccess)                                                                  \
+      return set_error(AGPT_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(_e));   \
+  } while (0)
+
+struct PlanDev {
+  const int32_t* parent;
+  const int32_t* depth;
+  const int32_t* end;
+  const int32_t* pref_off;  // [n_tiles + 1]
+  const int32_t* prefix;    // [pref_off[n_tiles]]
+  int64_t T;
+  int32_t n_tiles;
+  int32_t max_depth;
+};
+
+// ---------------------------------------------------------------------------
+// Shared tile set-up: in-tile parent links, depths, subtree ends and the
+// prefix path of the tile's first row.
+// ---------------------------------------------------------------------------
+struct TileShared {
+  int32_t parent[kTileQ];
+  int32_t depth[kTileQ];
+  int32_t end[kTileQ];
+  int32_t prefix[kMaxDepth];
+  int32_t prefix_end[kMaxDepth];
+};
+
+__device__ __forceinline__ void load_tile(const PlanDev& pl, int t, int64_t s, int ntile, int A,
+                                          TileShared& sh, bool need_ends) {
+  for (int i = threadIdx.x; i < ntile; i += blockDim.x) {
+    sh.parent[i] = pl.parent[s + i];
+    sh.depth[i] = pl.depth[s + i];
+    if (need_ends) sh.end[i] = pl.end[s + i];
+  }
+  const int32_t off = pl.pref_off[t];
+  for (int i = threadIdx.x; i < A; i += blockDim.x) {
+    const int32_t a = pl.prefix[off + i];
+    sh.prefix[i] = a;
+    if (need_ends) sh.prefix_end[i] = pl.end[a];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward: o_n = Σ_j softmax(q_n·k_j·scale) v_j over n's path; lse saved.
+// One workgroup per tile; item = (query row, head); online softmax in the
+// log2 domain.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin>
+__global__ __launch_bounds__(256) void trie_fwd_kernel(PlanDev pl, const Tin* __restrict__ Q,
+                                                       const Tin* __restrict__ K,
+                                                       const Tin* __restrict__ V,
+                                                       Tin* __restrict__ O,
+                                                       float* __restrict__ lse, int H,
+                                                       float scale) {
+  __shared__ TileShared sh;
+  const int t = blockIdx.x;
+  const int64_t s = static_cast<int64_t>(t) * kTileQ;
+  const int ntile = static_cast<int>(min<int64_t>(kTileQ, pl.T - s));
+  const int A = pl.pref_off[t + 1] - pl.pref_off[t];
+  load_tile(pl, t, s, ntile, A, sh, false);
+  __syncthreads();
+
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  for (int item = threadIdx.x; item < ntile * H; item += blockDim.x) {
+    const int ql = item / H;
+    const int h = item - ql * H;
+    const int64_t n = s + ql;
+    float q[HD];
+    load_vec<HD>(Q + n * D + h * HD, q);
+#pragma unroll
+    for (int i = 0; i < HD; ++i) q[i] *= qscale;
+    float m = -INFINITY, l = 0.0f;
+    float acc[HD];
+#pragma unroll
+    for (int i = 0; i < HD; ++i) acc[i] = 0.0f;
+
+    auto visit = [&](int64_t a) {
+      float k[HD], v[HD];
+      load_vec<HD>(K + a * D + h * HD, k);
+      load_vec<HD>(V + a * D + h * HD, v);
+      float sc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) sc += q[i] * k[i];
+      const float m_new = fmaxf(m, sc);
+      const float alpha = fast_exp2(m - m_new);
+      const float p = fast_exp2(sc - m_new);
+      l = l * alpha + p;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) acc[i] = acc[i] * alpha + p * v[i];
+      m = m_new;
+    };
+
+    int cur = ql;
+    int rem;
+    for (;;) {
+      visit(s + cur);
+      const int32_t par = sh.parent[cur];
+      if (par < s) {
+        rem = sh.depth[cur] - 1;  // ancestors left, all on the prefix path
+        break;
+      }
+      cur = static_cast<int>(par - s);
+    }
+    for (int d = rem - 1; d >= 0; --d) visit(sh.prefix[d]);
+
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < HD; ++i) acc[i] *= inv;
+    store_vec<HD>(O + n * D + h * HD, acc);
+    lse[n * H + h] = (m + fast_log2(l)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, per tile.
+//   phase 0: lse and (fp32 inputs) δ = dO·O per (query, head) into LDS
+//   phase 1: (bf16 inputs: δ = Σ_j w_j dO·v_j over the path, then)
+//            dQ = Σ_j ds_j k_j over each query's path (+ inverse RoPE)
+//   phase 2: per key of the tile's key set (prefix rows + tile rows):
+//            dK_a = Σ_n ds_{n,a} q_n, dV_a = Σ_n w_{n,a} dO_n over the
+//            tile's queries in subtree(a); finished keys are written in
+//            final form, open keys leave partials (own tile: in dK/dV rows;
+//            prefix keys: in Pk/Pv).
+// ---------------------------------------------------------------------------
+struct BwdShared {
+  TileShared tile;
+  float lse2[kTileQ * kMaxHeads];
+  float delta[kTileQ * kMaxHeads];
+};
+
+struct RopeArgs {
+  const float* cos_t;
+  const float* sin_t;
+  int seq_len;
+};
+
+__device__ __forceinline__ int rope_pos(int depth, int seq_len) {
+  const int p = depth - 1;
+  return p < seq_len - 1 ? p : seq_len - 1;
+}
+
+template <int HD, typename Tin>
+__global__ __launch_bounds__(256) void trie_bwd_kernel(
+    PlanDev pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV,
+    float* __restrict__ Pk, float* __restrict__ Pv, const float* __restrict__ acc_dk,
+    const float* __restrict__ acc_dv, RopeArgs rope, int H, float scale) {
+  __shared__ BwdShared sh;
+  const int t = blockIdx.x;
+  const int64_t s = static_cast<int64_t>(t) * kTileQ;
+  const int ntile = static_cast<int>(min<int64_t>(kTileQ, pl.T - s));
+  const int64_t e = s + ntile;
+  const int32_t poff = pl.pref_off[t];
+  const int A = pl.pref_off[t + 1] - poff;
+  load_tile(pl, t, s, ntile, A, sh.tile, true);
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+
+  // phase 0: lse (log2 units) and, for fp32 inputs, δ = dO·O. With bf16
+  // inputs O is a rounded output, so δ is recomputed in phase 1 as
+  // Σ_j w_j (dO·v_j) in fp32 (batched_depth_backward.cr:637-646).
+  constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
+  for (int item = threadIdx.x; item < ntile * H; item += blockDim.x) {
+    const int ql = item / H;
+    const int h = item - ql * H;
+    const int64_t n = s + ql;
+    if constexpr (kDeltaFromO) {
+      float o[HD], g[HD];
+      load_vec<HD>(O + n * D + h * HD, o);
+      load_vec<HD>(dO + n * D + h * HD, g);
+      float d = 0.0f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) d += o[i] * g[i];
+      sh.delta[item] = d;
+    }
+    sh.lse2[item] = lse[n * H + h] * kLog2e;
+  }
+  __syncthreads();
+
+  // phase 1: dQ
+  for (int item = threadIdx.x; item < ntile * H; item += blockDim.x) {
+    const int ql = item / H;
+    const int h = item - ql * H;
+    const int64_t n = s + ql;
+    float q[HD], g[HD], dq[HD];
+    load_vec<HD>(Q + n * D + h * HD, q);
+    load_vec<HD>(dO + n * D + h * HD, g);
+#pragma unroll
+    for (int i = 0; i < HD; ++i) {
+      q[i] *= qscale;
+      dq[i] = 0.0f;
+    }
+    const float l2 = sh.lse2[item];
+    // Walks n's path: in-tile parent links, then the tile's prefix list.
+    auto walk = [&](auto&& visit) {
+      int cur = ql;
+      int rem;
+      for (;;) {
+        visit(s + cur);
+        const int32_t par = sh.tile.parent[cur];
+        if (par < s) {
+          rem = sh.tile.depth[cur] - 1;
+          break;
+        }
+        cur = static_cast<int>(par - s);
+      }
+      for (int d = rem - 1; d >= 0; --d) visit(sh.tile.prefix[d]);
+    };
+    float dl;
+    if constexpr (kDeltaFromO) {
+      dl = sh.delta[item];
+    } else {
+      dl = 0.0f;
+      walk([&](int64_t a) {
+        float k[HD], v[HD];
+        load_vec<HD>(K + a * D + h * HD, k);
+        load_vec<HD>(V + a * D + h * HD, v);
+        float sc = 0.0f, dw = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD; ++i) {
+          sc += q[i] * k[i];
+          dw += g[i] * v[i];
+        }
+        dl += fast_exp2(sc - l2) * dw;
+      });
+      sh.delta[item] = dl;
+    }
+    walk([&](int64_t a) {
+      float k[HD], v[HD];
+      load_vec<HD>(K + a * D + h * HD, k);
+      load_vec<HD>(V + a * D + h * HD, v);
+      float sc = 0.0f, dw = 0.0f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) {
+        sc += q[i] * k[i];
+        dw += g[i] * v[i];
+      }
+      const float w = fast_exp2(sc - l2);
+      const float ds = w * (dw - dl) * scale;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) dq[i] += ds * k[i];
+    });
+    if (rope.cos_t) rope_inverse<HD>(dq, rope.cos_t, rope.sin_t, rope_pos(sh.tile.depth[ql], rope.seq_len));
+    store_vec<HD>(dQ + n * D + h * HD, dq);
+  }
+  if constexpr (!kDeltaFromO) __syncthreads();  // phase 2 reads every query's δ
+
+  // phase 2: dK / dV for the key set
+  const int nk = A + ntile;
+  for (int item = threadIdx.x; item < nk * H; item += blockDim.x) {
+    const int ki = item / H;
+    const int h = item - ki * H;
+    int64_t a, end_a;
+    int depth_a;
+    if (ki < A) {
+      a = sh.tile.prefix[ki];
+      end_a = sh.tile.prefix_end[ki];
+      depth_a = ki + 1;
+    } else {
+      a = s + (ki - A);
+      end_a = sh.tile.end[ki - A];
+      depth_a = sh.tile.depth[ki - A];
+    }
+    const int64_t q_lo = a > s ? a : s;
+    const int64_t q_hi = end_a < e ? end_a : e;
+    float k[HD], v[HD], dk[HD], dv[HD];
+    load_vec<HD>(K + a * D + h * HD, k);
+    load_vec<HD>(V + a * D + h * HD, v);
+#pragma unroll
+    for (int i = 0; i < HD; ++i) {
+      k[i] *= qscale;
+      dk[i] = 0.0f;
+      dv[i] = 0.0f;
+    }
+    for (int64_t n = q_lo; n < q_hi; ++n) {
+      const int qi = static_cast<int>(n - s) * H + h;
+      float q[HD], g[HD];
+      load_vec<HD>(Q + n * D + h * HD, q);
+      load_vec<HD>(dO + n * D + h * HD, g);
+      float sc = 0.0f, dw = 0.0f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) {
+        sc += q[i] * k[i];
+        dw += g[i] * v[i];
+      }
+      const float w = fast_exp2(sc - sh.lse2[qi]);
+      const float ds = w * (dw - sh.delta[qi]) * scale;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) {
+        dk[i] += ds * q[i];
+        dv[i] += w * g[i];
+      }
+    }
+    if (ki < A) {
+      const int64_t row = static_cast<int64_t>(poff) + ki;
+      store_vec<HD>(Pk + row * D + h * HD, dk);
+      store_vec<HD>(Pv + row * D + h * HD, dv);
+    } else if (end_a <= e) {
+      if (acc_dk) {
+        float x[HD];
+        load_vec<HD>(acc_dk + a * D + h * HD, x);
+#pragma unroll
+        for (int i = 0; i < HD; ++i) dk[i] += x[i];
+      }
+      if (acc_dv) {
+        float x[HD];
+        load_vec<HD>(acc_dv + a * D + h * HD, x);
+#pragma unroll
+        for (int i = 0; i < HD; ++i) dv[i] += x[i];
+      }
+      if (rope.cos_t) rope_inverse<HD>(dk, rope.cos_t, rope.sin_t, rope_pos(depth_a, rope.seq_len));
+      store_vec<HD>(dK + a * D + h * HD, dk);
+      store_vec<HD>(dV + a * D + h * HD, dv);
+    } else {
+      store_vec<HD>(dK + a * D + h * HD, dk);
+      store_vec<HD>(dV + a * D + h * HD, dv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reduction level 1: chunk c (kChunkTiles consecutive tiles) sums the prefix
+// partials of slot k over its tiles, for the slots every tile of the chunk
+// has (k < min A). Such a sum is used only when the whole chunk lies inside
+// one key's span, where slot k names the same key in every tile.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void trie_bwd_chunk_kernel(PlanDev pl, const float* __restrict__ Pk,
+                                                             const float* __restrict__ Pv,
+                                                             float* __restrict__ Ck,
+                                                             float* __restrict__ Cv, int D) {
+  const int c = blockIdx.x;
+  const int u0 = c * kChunkTiles;
+  const int u1 = min(pl.n_tiles, u0 + kChunkTiles);
+  __shared__ int min_a;
+  if (threadIdx.x == 0) {
+    int m = kMaxDepth;
+    for (int u = u0; u < u1; ++u) m = min(m, pl.pref_off[u + 1] - pl.pref_off[u]);
+    min_a = m;
+  }
+  __syncthreads();
+  const int total = min_a * D;
+  for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const int k = idx / D;
+    const int col = idx - k * D;
+    float sk = 0.0f, sv = 0.0f;
+    for (int u = u0; u < u1; ++u) {
+      const int64_t row = static_cast<int64_t>(pl.pref_off[u]) + k;
+      sk += Pk[row * D + col];
+      sv += Pv[row * D + col];
+    }
+    const int64_t o = (static_cast<int64_t>(c) * pl.max_depth + k) * D + col;
+    Ck[o] = sk;
+    Cv[o] = sv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reduction level 2: one wave per open key a of tile t (the rows of tile t on
+// the prefix path of tile t+1). dK_a = own-tile partial (already in dK) +
+// Σ over tiles u in (t, tile(end_a - 1)] of slot depth(a)-1, in tile order,
+// using chunk sums for whole chunks. Then seeds, inverse RoPE, final write.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
+    PlanDev pl, float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ Pk,
+    const float* __restrict__ Pv, const float* __restrict__ Ck, const float* __restrict__ Cv,
+    const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeArgs rope, int H) {
+  const int t = blockIdx.x;  // tiles 0 .. n_tiles-2
+  const int64_t s = static_cast<int64_t>(t) * kTileQ;
+  const int32_t noff = pl.pref_off[t + 1];
+  const int An = pl.pref_off[t + 2] - noff;
+  const int D = H * HD;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nwaves = blockDim.x >> 6;
+  for (int k = An - 1 - wave; k >= 0; k -= nwaves) {
+    const int64_t a = pl.prefix[noff + k];
+    if (a < s) break;  // deeper-first scan: everything above is outside tile t
+    const int u_last = static_cast<int>((pl.end[a] - 1) / kTileQ);
+    const int pos = rope.cos_t ? rope_pos(k + 1, rope.seq_len) : 0;
+    for (int col0 = lane * 2; col0 < D; col0 += 128) {
+      float2 sk = *reinterpret_cast<const float2*>(dK + a * D + col0);
+      float2 sv = *reinterpret_cast<const float2*>(dV + a * D + col0);
+      int u = t + 1;
+      while (u <= u_last) {
+        const int c = u / kChunkTiles;
+        if (u == c * kChunkTiles && u + kChunkTiles - 1 <= u_last) {
+          const int64_t o = (static_cast<int64_t>(c) * pl.max_depth + k) * D + col0;
+          const float2 ck = *reinterpret_cast<const float2*>(Ck + o);
+          const float2 cv = *reinterpret_cast<const float2*>(Cv + o);
+          sk.x += ck.x;
+          sk.y += ck.y;
+          sv.x += cv.x;
+          sv.y += cv.y;
+          u += kChunkTiles;
+        } else {
+          const int64_t o = (static_cast<int64_t>(pl.pref_off[u]) + k) * D + col0;
+          const float2 pk = *reinterpret_cast<const float2*>(Pk + o);
+          const float2 pv = *reinterpret_cast<const float2*>(Pv + o);
+          sk.x += pk.x;
+          sk.y += pk.y;
+          sv.x += pv.x;
+          sv.y += pv.y;
+          ++u;
+        }
+      }
+      if (acc_dk) {
+        const float2 x = *reinterpret_cast<const float2*>(acc_dk + a * D + col0);
+        sk.x += x.x;
+        sk.y += x.y;
+      }
+      if (acc_dv) {
+        const float2 x = *reinterpret_cast<const float2*>(acc_dv + a * D + col0);
+        sv.x += x.x;
+        sv.y += x.y;
+      }
+      if (rope.cos_t) {
+        const int j = col0 % HD;  // even: pair (j, j+1) of the head
+        const float c = rope.cos_t[pos * HD + j];
+        const float sn = rope.sin_t[pos * HD + j];
+        const float x0 = sk.x, x1 = sk.y;
+        sk.x = x0 * c + x1 * sn;
+        sk.y = -x0 * sn + x1 * c;
+      }
+      *reinterpret_cast<float2*>(dK + a * D + col0) = sk;
+      *reinterpret_cast<float2*>(dV + a * D + col0) = sv;
+    }
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// Host side: handle, plan, launches.
+// ===========================================================================
+struct agpt_attn_s {
+  agpt_attn_config cfg{};
+  int device = 0;
+  // plan (host copies used for launch geometry)
+  int64_t T = 0;
+  int32_t n_tiles = 0;
+  int32_t n_chunks = 0;
+  int32_t max_depth = 0;
+  int64_t sum_depth = 0;
+  int64_t n_prefix_rows = 0;
+  bool planned = false;
+  // device tables
+  int32_t* d_parent = nullptr;
+  int32_t* d_depth = nullptr;
+  int32_t* d_end = nullptr;
+  int32_t* d_pref_off = nullptr;
+  int32_t* d_prefix = nullptr;
+  float* d_Pk = nullptr;
+  float* d_Pv = nullptr;
+  float* d_Ck = nullptr;
+  float* d_Cv = nullptr;
+};
+
+namespace {
+
+void free_plan(agpt_attn_s* h) {
+  int32_t** ip[] = {&h->d_parent, &h->d_depth, &h->d_end, &h->d_pref_off, &h->d_prefix};
+  for (auto p : ip)
+    if (*p) {
+      (void)hipFree(*p);
+      *p = nullptr;
+    }
+  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv};
+  for (auto p : fp)
+    if (*p) {
+      (void)hipFree(*p);
+      *p = nullptr;
+    }
+  h->planned = false;
+}
+
+bool head_dim_supported(int hd) { return hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64; }
+
+PlanDev plan_dev(const agpt_attn_s* h) {
+  PlanDev p;
+  p.parent = h->d_parent;
+  p.depth = h->d_depth;
+  p.end = h->d_end;
+  p.pref_off = h->d_pref_off;
+  p.prefix = h->d_prefix;
+  p.T = h->T;
+  p.n_tiles = h->n_tiles;
+  p.max_depth = h->max_depth;
+  return p;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+int agpt_internal_set_error(int code, const char* msg) { return set_error(code, "%s", msg); }
+
+extern "C" const char* agpt_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char* agpt_version(void) {
+  return "agpt_attn gfx950 tile-walk v1 (tile=64, fp32/bf16, hd 4..64)";
+}
+
+extern "C" int agpt_attn_check_tree(const int32_t* parent, int64_t n, int32_t* depth,
+                                    int32_t* subtree_end) {
+  if (n < 0 || (n > 0 && !parent)) return set_error(AGPT_ERR_INVALID_ARG, "null parent table");
+  if (n >= (int64_t{1} << 31) - kTileQ)
+    return set_error(AGPT_ERR_INVALID_ARG, "n_nodes %lld exceeds int32 row indexing", (long long)n);
+  std::vector<int32_t> dep(static_cast<size_t>(n)), en(static_cast<size_t>(n));
+  // Preorder check with a stack of open subtrees: the parent of row i must be
+  // the node on top of the stack after popping every subtree that i cannot
+  // belong to; that makes every subtree a contiguous row range.
+  std::vector<int32_t> stack;
+  stack.reserve(kMaxDepth);
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t p = parent[i];
+    if (p < -1 || p >= i)
+      return set_error(AGPT_ERR_NOT_DFS, "parent[%lld] = %d is not an earlier row or -1",
+                       (long long)i, p);
+    while (!stack.empty() && stack.back() != p) {
+      en[stack.back()] = static_cast<int32_t>(i);
+      stack.pop_back();
+    }
+    if (p >= 0 && stack.empty())
+      return set_error(AGPT_ERR_NOT_DFS,
+                       "row %lld follows a closed subtree of its parent %d: not DFS preorder",
+                       (long long)i, p);
+    dep[i] = p < 0 ? 1 : dep[p] + 1;
+    stack.push_back(static_cast<int32_t>(i));
+  }
+  while (!stack.empty()) {
+    en[stack.back()] = static_cast<int32_t>(n);
+    stack.pop_back();
+  }
+  if (depth) std::memcpy(depth, dep.data(), sizeof(int32_t) * n);
+  if (subtree_end) std::memcpy(subtree_end, en.data(), sizeof(int32_t) * n);
+  g_last_error.clear();
+  return AGPT_OK;
+}
+
+extern "C" int agpt_attn_dfs_order(const int32_t* parent, int64_t n, int32_t* perm) {
+  if (n < 0 || (n > 0 && (!parent || !perm))) return set_error(AGPT_ERR_INVALID_ARG, "null argument");
+  std::vector<int64_t> cnt(static_cast<size_t>(n) + 1, 0);
+  int64_t n_roots = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t p = parent[i];
+    if (p < -1 || p >= n || p == i) return set_error(AGPT_ERR_INVALID_ARG, "bad parent[%lld]=%d", (long long)i, p);
+    if (p >= 0) cnt[p + 1]++;
+    else n_roots++;
+  }
+  // CSR children lists, children in original order
+  std::vector<int64_t> off(static_cast<size_t>(n) + 1, 0);
+  for (int64_t i = 0; i < n; ++i) off[i + 1] = off[i] + cnt[i + 1];
+  std::vector<int32_t> kids(static_cast<size_t>(off[n]));
+  std::vector<int64_t> fill(off.begin(), off.end() - 1);
+  std::vector<int32_t> roots;
+  roots.reserve(static_cast<size_t>(n_roots));
+  for (int64_t i = 0; i < n; ++i) {
+    if (parent[i] >= 0) kids[fill[parent[i]]++] = static_cast<int32_t>(i);
+    else roots.push_back(static_cast<int32_t>(i));
+  }
+  int64_t k = 0;
+  std::vector<int32_t> stack;
+  for (auto it = roots.rbegin(); it != roots.rend(); ++it) stack.push_back(*it);
+  while (!stack.empty()) {
+    const int32_t v = stack.back();
+    stack.pop_back();
+    if (k >= n) return set_error(AGPT_ERR_INVALID_ARG, "parent table has a cycle");
+    perm[k++] = v;
+    for (int64_t j = off[v + 1] - 1; j >= off[v]; --j) stack.push_back(kids[j]);
+  }
+  if (k != n) return set_error(AGPT_ERR_INVALID_ARG, "parent table has a cycle");
+  return AGPT_OK;
+}
+
+extern "C" int agpt_attn_create(const agpt_attn_config* cfg, agpt_attn_handle* out) {
+  if (!cfg || !out) return set_error(AGPT_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  if (cfg->n_heads < 1 || cfg->n_heads > kMaxHeads)
+    return set_error(AGPT_ERR_UNSUPPORTED, "n_heads %d outside 1..%d", cfg->n_heads, kMaxHeads);
+  if (!head_dim_supported(cfg->head_dim))
+    return set_error(AGPT_ERR_UNSUPPORTED, "head_dim %d not built (4, 8, 16, 32, 64)", cfg->head_dim);
+  if (cfg->max_depth < 1 || cfg->max_depth > kMaxDepth)
+    return set_error(AGPT_ERR_UNSUPPORTED, "max_depth %d outside 1..%d", cfg->max_depth, kMaxDepth);
+  if (cfg->dtype != AGPT_DTYPE_F32 && cfg->dtype != AGPT_DTYPE_BF16)
+    return set_error(AGPT_ERR_UNSUPPORTED, "dtype %d", cfg->dtype);
+  auto* h = new agpt_attn_s();
+  h->cfg = *cfg;
+  if (hipGetDevice(&h->device) != hipSuccess) {
+    delete h;
+    return set_error(AGPT_ERR_DEVICE, "no HIP device");
+  }
+  *out = h;
+  return AGPT_OK;
+}
+
+extern "C" int agpt_attn_destroy(agpt_attn_handle h) {
+  if (!h) return AGPT_OK;
+  free_plan(h);
+  delete h;
+  return AGPT_OK;
+}
+
+namespace {
+
+template <typename T>
+int upload(T** dst, const std::vector<T>& src) {
+  const size_t bytes = std::max<size_t>(src.size(), 1) * sizeof(T);
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(dst), bytes));
+  if (!src.empty()) HIP_TRY(hipMemcpy(*dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice));
+  return AGPT_OK;
+}
+
+int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
+  free_plan(h);
+  std::vector<int32_t> depth(static_cast<size_t>(n)), end(static_cast<size_t>(n));
+  int rc = agpt_attn_check_tree(parent, n, depth.data(), end.data());
+  if (rc != AGPT_OK) return rc;
+  int32_t maxd = 1;
+  int64_t sumd = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    maxd = std::max(maxd, depth[i]);
+    sumd += depth[i];
+  }
+  if (maxd > h->cfg.max_depth)
+    return set_error(AGPT_ERR_TOO_DEEP, "tree depth %d exceeds config max_depth %d", maxd, h->cfg.max_depth);
+  const int32_t n_tiles = static_cast<int32_t>((n + kTileQ - 1) / kTileQ);
+  std::vector<int32_t> pref_off(static_cast<size_t>(n_tiles) + 2, 0);
+  for (int32_t t = 0; t < n_tiles; ++t) pref_off[t + 1] = pref_off[t] + depth[static_cast<int64_t>(t) * kTileQ] - 1;
+  pref_off[n_tiles + 1] = pref_off[n_tiles];  // sentinel read by the reducer
+  std::vector<int32_t> prefix(static_cast<size_t>(pref_off[n_tiles]));
+  for (int32_t t = 0; t < n_tiles; ++t) {
+    const int64_t s = static_cast<int64_t>(t) * kTileQ;
+    int32_t a = parent[s];
+    for (int d = depth[s] - 2; d >= 0; --d) {
+      prefix[pref_off[t] + d] = a;
+      a = parent[a];
+    }
+  }
+  const int D = h->cfg.n_heads * h->cfg.head_dim;
+  h->T = n;
+  h->n_tiles = n_tiles;
+  h->n_chunks = (n_tiles + kChunkTiles - 1) / kChunkTiles;
+  h->max_depth = maxd;
+  h->sum_depth = sumd;
+  h->n_prefix_rows = pref_off[n_tiles];
+  std::vector<int32_t> par(parent, parent + n);
+  if ((rc = upload(&h->d_parent, par)) != AGPT_OK) return rc;
+  if ((rc = upload(&h->d_depth, depth)) != AGPT_OK) return rc;
+  if ((rc = upload(&h->d_end, end)) != AGPT_OK) return rc;
+  if ((rc = upload(&h->d_pref_off, pref_off)) != AGPT_OK) return rc;
+  if ((rc = upload(&h->d_prefix, prefix)) != AGPT_OK) return rc;
+  const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pk), pbytes));
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pv), pbytes));
+  const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Ck), cbytes));
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
+  h->planned = true;
+  g_last_error.clear();
+  return AGPT_OK;
+}
+
+}  // namespace
+
+extern "C" int agpt_attn_plan(agpt_attn_handle h, const int32_t* parent, int64_t n) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (n < 1 || !parent) return set_error(AGPT_ERR_INVALID_ARG, "empty tree or null parent table");
+  HIP_TRY(hipSetDevice(h->device));
+  const int rc = plan_impl(h, parent, n);
+  if (rc != AGPT_OK) free_plan(h);
+  return rc;
+}
+
+extern "C" int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_parent,
+                                    const int32_t* edge_len, int64_t n_radix) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (n_radix < 1 || !radix_parent || !edge_len)
+    return set_error(AGPT_ERR_INVALID_ARG, "empty radix tree or null table");
+  std::vector<int64_t> last_row(static_cast<size_t>(n_radix));
+  std::vector<int32_t> parent;
+  for (int64_t r = 0; r < n_radix; ++r) {
+    const int32_t rp = radix_parent[r];
+    if (rp < -1 || rp >= r)
+      return set_error(AGPT_ERR_NOT_DFS, "radix_parent[%lld] = %d is not an earlier node or -1",
+                       (long long)r, rp);
+    if (edge_len[r] < 1) return set_error(AGPT_ERR_INVALID_ARG, "edge_len[%lld] = %d", (long long)r, edge_len[r]);
+    int64_t prev = rp < 0 ? -1 : last_row[rp];
+    for (int j = 0; j < edge_len[r]; ++j) {
+      parent.push_back(static_cast<int32_t>(prev));
+      prev = static_cast<int64_t>(parent.size()) - 1;
+      if (prev >= (int64_t{1} << 31) - kTileQ) return set_error(AGPT_ERR_INVALID_ARG, "too many rows");
+    }
+    last_row[r] = prev;
+  }
+  return agpt_attn_plan(h, parent.data(), static_cast<int64_t>(parent.size()));
+}
+
+extern "C" int agpt_attn_plan_info(agpt_attn_handle h, int64_t* n_nodes, int64_t* n_tiles,
+                                   int64_t* sum_depth, int32_t* max_depth) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (!h->planned) return set_error(AGPT_ERR_NO_PLAN, "no plan");
+  if (n_nodes) *n_nodes = h->T;
+  if (n_tiles) *n_tiles = h->n_tiles;
+  if (sum_depth) *sum_depth = h->sum_depth;
+  if (max_depth) *max_depth = h->max_depth;
+  return AGPT_OK;
+}
+
+namespace {
+
+int check_opts(const agpt_attn_s* h, const agpt_attn_opts* o) {
+  if (o && o->rope_cos) {
+    if (!o->rope_sin || o->rope_seq_len < 1)
+      return set_error(AGPT_ERR_INVALID_ARG, "RoPE needs both tables and rope_seq_len >= 1");
+  }
+  (void)h;
+  return AGPT_OK;
+}
+
+float scale_of(const agpt_attn_s* h, const agpt_attn_opts* o) {
+  if (o && o->scale != 0.0f) return o->scale;
+  return static_cast<float>(1.0 / std::sqrt(static_cast<double>(h->cfg.head_dim)));
+}
+
+// Records the caller's profiling event `i` (see agpt_attn_opts.prof_events).
+struct ProfMarks {
+  void** ev = nullptr;
+  int n = 0;
+  hipStream_t st = nullptr;
+  void mark(int i) const {
+    if (ev && i < n && ev[i]) (void)hipEventRecord(static_cast<hipEvent_t>(ev[i]), st);
+  }
+};
+
+template <int HD, typename Tin>
+void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, void* o,
+                float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
+  pm.mark(0);
+  hipLaunchKernelGGL((trie_fwd_kernel<HD, Tin>), dim3(h->n_tiles), dim3(256), 0, st, plan_dev(h),
+                     static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v),
+                     static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+  pm.mark(1);
+}
+
+template <int HD, typename Tin>
+void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, const void* o,
+                const float* lse, const void* dO, float* dq, float* dk, float* dv,
+                const float* acc_dk, const float* acc_dv, RopeArgs rope, float scale,
+                hipStream_t st, const ProfMarks& pm) {
+  const int D = h->cfg.n_heads * HD;
+  pm.mark(0);
+  hipLaunchKernelGGL((trie_bwd_kernel<HD, Tin>), dim3(h->n_tiles), dim3(256), 0, st, plan_dev(h),
+                     static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v),
+                     static_cast<const Tin*>(o), lse, static_cast<const Tin*>(dO), dq, dk, dv, h->d_Pk,
+                     h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+  pm.mark(1);
+  if (h->n_tiles > 1) {
+    hipLaunchKernelGGL(trie_bwd_chunk_kernel, dim3(h->n_chunks), dim3(256), 0, st, plan_dev(h), h->d_Pk,
+                       h->d_Pv, h->d_Ck, h->d_Cv, D);
+    pm.mark(2);
+    hipLaunchKernelGGL((trie_bwd_reduce_kernel<HD>), dim3(h->n_tiles - 1), dim3(256), 0, st, plan_dev(h),
+                       dk, dv, h->d_Pk, h->d_Pv, h->d_Ck, h->d_Cv, acc_dk, acc_dv, rope,
+                       h->cfg.n_heads);
+  }
+  pm.mark(3);
+}
+
+template <typename Fn>
+int dispatch_hd(int hd, Fn&& fn) {
+  switch (hd) {
+    case 4: fn(std::integral_constant<int, 4>{}); return AGPT_OK;
+    case 8: fn(std::integral_constant<int, 8>{}); return AGPT_OK;
+    case 16: fn(std::integral_constant<int, 16>{}); return AGPT_OK;
+    case 32: fn(std::integral_constant<int, 32>{}); return AGPT_OK;
+    case 64: fn(std::integral_constant<int, 64>{}); return AGPT_OK;
+    default: return set_error(AGPT_ERR_UNSUPPORTED, "head_dim %d", hd);
+  }
+}
+
+}  // namespace
+
+extern "C" int agpt_attn_fwd(agpt_attn_handle h, const void* q, const void* k, const void* v,
+                             void* o, float* lse, const agpt_attn_opts* opts) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (!h->planned) return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_fwd before agpt_attn_plan");
+  if (!q || !k || !v || !o || !lse) return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse))
+    return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
+  int rc = check_opts(h, opts);
+  if (rc != AGPT_OK) return rc;
+  HIP_TRY(hipSetDevice(h->device));
+  const float scale = scale_of(h, opts);
+  hipStream_t st = opts ? static_cast<hipStream_t>(opts->stream) : nullptr;
+  ProfMarks pm;
+  if (opts) pm = ProfMarks{opts->prof_events, opts->n_prof_events, st};
+  rc = dispatch_hd(h->cfg.head_dim, [&](auto hdc) {
+    constexpr int HD = decltype(hdc)::value;
+    if (h->cfg.dtype == AGPT_DTYPE_F32) launch_fwd<HD, float>(h, q, k, v, o, lse, scale, st, pm);
+    else launch_fwd<HD, bf16_t>(h, q, k, v, o, lse, scale, st, pm);
+  });
+  if (rc != AGPT_OK) return rc;
+  HIP_TRY(hipGetLastError());
+  return AGPT_OK;
+}
+
+extern "C" int agpt_attn_bwd(agpt_attn_handle h, const void* q, const void* k, const void* v,
+                             const void* o, const float* lse, const void* d_o, float* dq,
+                             float* dk, float* dv, const float* acc_dk, const float* acc_dv,
+                             const agpt_attn_opts* opts) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (!h->planned) return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_bwd before agpt_attn_plan");
+  if (!q || !k || !v || !o || !lse || !d_o || !dq || !dk || !dv)
+    return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
+  const void* ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv};
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
+  int rc = check_opts(h, opts);
+  if (rc != AGPT_OK) return rc;
+  HIP_TRY(hipSetDevice(h->device));
+  const float scale = scale_of(h, opts);
+  hipStream_t st = opts ? static_cast<hipStream_t>(opts->stream) : nullptr;
+  RopeArgs rope{nullptr, nullptr, 1};
+  if (opts && opts->rope_cos) rope = RopeArgs{opts->rope_cos, opts->rope_sin, opts->rope_seq_len};
+  ProfMarks pm;
+  if (opts) pm = ProfMarks{opts->prof_events, opts->n_prof_events, st};
+  rc = dispatch_hd(h->cfg.head_dim, [&](auto hdc) {
+    constexpr int HD = decltype(hdc)::value;
+    if (h->cfg.dtype == AGPT_DTYPE_F32)
+      launch_bwd<HD, float>(h, q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv, rope, scale, st, pm);
+    else
+      launch_bwd<HD, bf16_t>(h, q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv, rope, scale, st, pm);
+  });
+  if (rc != AGPT_OK) return rc;
+  HIP_TRY(hipGetLastError());
+  return AGPT_OK;
+}
+
+extern "C" int agpt_sync(void) {
+  HIP_TRY(hipDeviceSynchronize());
+  return AGPT_OK;
+}

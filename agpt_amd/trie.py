@@ -1,0 +1,125 @@
+"""Synthetic corpora and tries (the inputs of the trie-attention path).
+
+Thin numpy wrappers over libagpt_trie.so (include/agpt_trie.h).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._native import trie_lib
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+def markov_corpus(n: int, order: int, vocab: int, zipf_s: float, seed: int,
+                  sigma: float = 2.0) -> np.ndarray:
+    """Order-k Markov tokens with Zipf marginal ranks (see include/agpt_trie.h)."""
+    out = np.empty(n, dtype=np.int32)
+    rc = trie_lib().agpt_markov_corpus(seed, order, vocab, zipf_s, sigma, n, _ptr(out))
+    if rc:
+        raise ValueError("agpt_markov_corpus: bad arguments")
+    return out
+
+
+def uniform_tokens(n: int, vocab: int, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    if trie_lib().agpt_uniform_tokens(seed, vocab, n, _ptr(out)):
+        raise ValueError("agpt_uniform_tokens: bad arguments")
+    return out
+
+
+@dataclass
+class Trie:
+    """Node-token tables in DFS preorder (one row = one query position)."""
+    parent: np.ndarray       # int32 [T], -1 for depth-1 nodes
+    depth: np.ndarray        # int32 [T], 1-based = keys attended
+    token: np.ndarray        # int32 [T]
+    subtree_end: np.ndarray  # int32 [T], exclusive
+    radix_head: np.ndarray   # int32 [T]
+    partition: np.ndarray    # int32 [T], bigram key
+    n_radix: int
+    n_root_children: int
+    n_bigram_parts: int
+
+    @property
+    def n_nodes(self) -> int:
+        return int(self.parent.shape[0])
+
+    @property
+    def sum_depth(self) -> int:
+        return int(self.depth.astype(np.int64).sum())
+
+    @property
+    def max_depth(self) -> int:
+        return int(self.depth.max()) if self.n_nodes else 0
+
+    def radix(self) -> tuple[np.ndarray, np.ndarray]:
+        """(radix_parent, edge_len) of the radix view, DFS preorder."""
+        heads = np.flatnonzero(self.radix_head)
+        edge_len = np.diff(np.append(heads, self.n_nodes)).astype(np.int32)
+        radix_of = np.cumsum(self.radix_head) - 1
+        par = self.parent[heads]
+        radix_parent = np.where(par < 0, -1, radix_of[np.maximum(par, 0)]).astype(np.int32)
+        return radix_parent, edge_len
+
+
+def _export(h) -> Trie:
+    lib = trie_lib()
+    n = C.c_int64()
+    nr = C.c_int64()
+    sd = C.c_int64()
+    md = C.c_int32()
+    nrc = C.c_int64()
+    nbp = C.c_int64()
+    lib.agpt_trie_stats(h, C.byref(n), C.byref(nr), C.byref(sd), C.byref(md), C.byref(nrc),
+                        C.byref(nbp))
+    T = n.value
+    arrs = [np.empty(T, dtype=np.int32) for _ in range(6)]
+    lib.agpt_trie_export(h, *[_ptr(a) for a in arrs])
+    lib.agpt_trie_free(h)
+    return Trie(*arrs, n_radix=nr.value, n_root_children=nrc.value, n_bigram_parts=nbp.value)
+
+
+def build_trie(tokens: np.ndarray, max_depth: int, max_starts: int = 0) -> Trie:
+    """Leveled trie with TrieCorpus#ingest semantics (trie_corpus.cr:200-228)."""
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    h = C.c_void_p()
+    if trie_lib().agpt_trie_build(_ptr(tok), tok.shape[0], max_depth, max_starts, C.byref(h)):
+        raise ValueError("agpt_trie_build: bad arguments")
+    return _export(h)
+
+
+def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    assert tok.shape[0] >= n_chains * chain_len
+    h = C.c_void_p()
+    if trie_lib().agpt_trie_build_chains(_ptr(tok), n_chains, chain_len, C.byref(h)):
+        raise ValueError("agpt_trie_build_chains: bad arguments")
+    return _export(h)
+
+
+# BASELINE.json configs (synthetic tries). Seeds are fixed and recorded.
+CONFIGS = {
+    "C1": dict(n=200_000, order=3, vocab=65, zipf=1.1, depth=32, seed=1, H=4, hd=16, dtype="f32"),
+    "C2": dict(n=1_100_000, order=5, vocab=65, zipf=1.1, depth=32, seed=2, H=8, hd=16, dtype="f32"),
+    "C4": dict(n=5_000_000, order=8, vocab=256, zipf=1.2, depth=128, seed=4, H=8, hd=64,
+               dtype="bf16"),
+    "C5": dict(chains=512, chain_len=256, vocab=65, seed=5, H=4, hd=64, dtype="bf16"),
+}
+
+
+def config_trie(name: str, scale: float = 1.0) -> Trie:
+    """The synthetic trie of a BASELINE config; scale < 1 shrinks the corpus."""
+    c = CONFIGS[name]
+    if "chains" in c:
+        n_chains = max(1, int(c["chains"] * scale))
+        tok = uniform_tokens(n_chains * c["chain_len"], c["vocab"], c["seed"])
+        return build_chains(tok, n_chains, c["chain_len"])
+    n = max(2, int(c["n"] * scale))
+    tok = markov_corpus(n, c["order"], c["vocab"], c["zipf"], c["seed"])
+    return build_trie(tok, c["depth"])

@@ -1,0 +1,74 @@
+/*
+ * agpt_trie.h — host-only C ABI of libagpt_trie.so: the seeded synthetic
+ * corpus generator and the trie builder that produce the inputs of the
+ * trie-attention path (node-token parent tables in DFS preorder).
+ *
+ * The reference builds its tries offline with Crystal tools
+ * (src/agpt/trie_corpus.cr:200-228 ingest, src/agpt/streaming_radix_builder.cr
+ * radix compression and subtree keys); these functions restate only the parts
+ * that define the attention inputs: which prefixes become nodes, their
+ * parent/child structure and depth, radix-chain heads, and the unigram /
+ * bigram partition key. No device code; safe to call without a GPU.
+ */
+#ifndef AGPT_TRIE_H
+#define AGPT_TRIE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct agpt_trie_s* agpt_trie_handle;
+
+/* Seeded order-k Markov corpus over `vocab` symbols. Symbol r has marginal
+ * rank r with Zipf weight (r+1)^-zipf_s; the conditional law given the last
+ * `order` symbols is p(x|ctx) ∝ (x+1)^-zipf_s * exp(sigma * xi(ctx, x)),
+ * xi ~ N(0,1) drawn from a counter-based generator keyed by (seed, ctx, x).
+ * Writes n tokens. Returns 0 on success. */
+int agpt_markov_corpus(uint64_t seed, int order, int vocab, double zipf_s,
+                       double sigma, int64_t n, int32_t* out_tokens);
+
+/* Uniform i.i.d. tokens in [0, vocab) from seed (the chain-control corpus). */
+int agpt_uniform_tokens(uint64_t seed, int vocab, int64_t n, int32_t* out_tokens);
+
+/* Leveled trie of a token stream with TrieCorpus#ingest semantics
+ * (trie_corpus.cr:200-228): starts are 0..n-2 (or max_starts of them spread
+ * evenly, trie_corpus.cr:897-913, when max_starts > 0); each start inserts the
+ * path tokens[start .. start+len) with len = min(max_depth, n-1-start).
+ * Nodes come out in DFS preorder with children in ascending token order. */
+int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
+                    int64_t max_starts, agpt_trie_handle* out);
+
+/* `n_chains` independent unary chains of `chain_len` nodes each (never
+ * merged); chain c takes tokens[c*chain_len ...]. The dense-causal control. */
+int agpt_trie_build_chains(const int32_t* tokens, int64_t n_chains, int chain_len,
+                           agpt_trie_handle* out);
+
+/* Node-token count T, radix-node count (chain heads, streaming_radix_builder.cr:149-175),
+ * Σ depth, max depth, number of root children, number of bigram partitions. */
+int agpt_trie_stats(agpt_trie_handle t, int64_t* n_nodes, int64_t* n_radix,
+                    int64_t* sum_depth, int32_t* max_depth, int64_t* n_root_children,
+                    int64_t* n_bigram_parts);
+
+/* Copies the per-node tables (any pointer may be NULL), each of T entries:
+ * parent (-1 for depth 1), depth (1-based), token, subtree_end (exclusive),
+ * radix_head (1 if the node starts a radix edge), partition (bigram subtree
+ * key (first_token << 8) | second_token, second_token = 255 for depth-1
+ * nodes, the sentinel of streaming_radix_builder.cr:219-224). */
+int agpt_trie_export(agpt_trie_handle t, int32_t* parent, int32_t* depth,
+                     int32_t* token, int32_t* subtree_end, int32_t* radix_head,
+                     int32_t* partition);
+
+/* Radix view: number of radix nodes R, then per radix node (DFS preorder)
+ * its radix parent (-1 for root children) and edge length. */
+int agpt_trie_export_radix(agpt_trie_handle t, int32_t* radix_parent,
+                           int32_t* edge_len);
+
+void agpt_trie_free(agpt_trie_handle t);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AGPT_TRIE_H */

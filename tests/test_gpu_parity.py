@@ -1,0 +1,270 @@
+"""HIP trie attention vs the CPU oracle (the restated Crystal loops), through
+the C ABI (libagpt_attn.so via ctypes), on seeded tries.
+
+Bar: fp32 within 1e-4 relative / 1e-5 absolute; bf16-input variants within
+2e-2 relative.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import (ATOL_BF16, ATOL_F32, RTOL_BF16, RTOL_F32, assert_close, round_bf16,
+                     scale_of, small_trie, tensors)
+from oracle import oracle as ORC
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=None, acc=None, max_depth=None):
+    import torch
+
+    from agpt_amd.attention import TrieAttention, rope_tables
+
+    dev = torch.device("cuda:0")
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    md = max_depth or max(1, int(ORC.depths(tr_parent).max()))
+    att = TrieAttention(H, hd, max_depth=md, dtype=tdt)
+    att.plan(tr_parent)
+    q, k, v, g = (torch.from_numpy(x).to(dev).to(tdt).contiguous() for x in (Q, K, V, G))
+    o, lse = att.forward(q, k, v)
+    rt = None
+    if rope is not None:
+        rt = tuple(torch.from_numpy(x).to(dev).contiguous() for x in rope)
+    acc_t = [None, None]
+    if acc is not None:
+        acc_t = [torch.from_numpy(x).to(dev).contiguous() for x in acc]
+    dq, dk, dv = att.backward(q, k, v, o, lse, g, acc_dk=acc_t[0], acc_dv=acc_t[1], rope=rt)
+    torch.cuda.synchronize()
+    res = [x.float().cpu().numpy() for x in (o, lse, dq, dk, dv)]
+    att.close()
+    return res
+
+
+def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0):
+    T = tr_parent.shape[0]
+    D = H * hd
+    Q, K, V, G = tensors(T, D, seed, sharp=sharp)
+    if dtype == "bf16":
+        Q, K, V, G = (round_bf16(x) for x in (Q, K, V, G))
+    scale = scale_of(hd)
+    rope_t = ORC.rope_table(64, hd) if rope else None
+    accs = None
+    if acc:
+        rng = np.random.default_rng(seed + 99)
+        accs = [rng.standard_normal((T, D)).astype(np.float32) * np.float32(0.1) for _ in range(2)]
+    o, lse, dq, dk, dv = _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=rope_t, acc=accs)
+    Oo, W, lse_o = ORC.fwd(tr_parent, Q, K, V, H, hd, scale)
+    if dtype == "bf16":
+        rtol, atol = RTOL_BF16, ATOL_BF16
+    else:
+        rtol, atol = RTOL_F32, ATOL_F32
+    # Sharp softmax (large scores) makes dK/dV sums of terms far larger than
+    # the result; there the relative bound is taken normwise per (row, head).
+    rs = hd if (sharp > 1.0 or dtype == "bf16") else None
+    assert_close(o, Oo, rtol, atol, "O", row_scale=rs)
+    assert_close(lse, lse_o, rtol, atol, "lse")
+    dQ, dK, dV = ORC.bwd(tr_parent, Q, K, V, W, G, H, hd, scale,
+                         acc_dk=None if accs is None else accs[0],
+                         acc_dv=None if accs is None else accs[1], rope=rope_t)
+    assert_close(dq, dQ, rtol, atol, "dQ", row_scale=rs)
+    assert_close(dk, dK, rtol, atol, "dK", row_scale=rs)
+    assert_close(dv, dV, rtol, atol, "dV", row_scale=rs)
+
+
+@pytest.mark.parametrize("hd,H", [(4, 2), (8, 3), (16, 4), (16, 8), (32, 2), (64, 2)])
+def test_parity_f32(gpu, hd, H):
+    tr = small_trie(n_tokens=600, depth=12, seed=hd + H)
+    _check(tr.parent, H, hd, seed=hd * 10 + H)
+
+
+@pytest.mark.parametrize("rope,acc,sharp", [(True, False, 1.0), (False, True, 1.0),
+                                            (True, True, 8.0)])
+def test_parity_rope_acc_sharp(gpu, rope, acc, sharp):
+    tr = small_trie(n_tokens=900, depth=16, seed=11)
+    _check(tr.parent, 4, 16, seed=5, rope=rope, acc=acc, sharp=sharp)
+
+
+@pytest.mark.parametrize("hd", [16, 64])
+def test_parity_bf16(gpu, hd):
+    tr = small_trie(n_tokens=700, depth=14, seed=21)
+    _check(tr.parent, 4, hd, seed=hd, dtype="bf16", rope=True)
+
+
+def test_parity_c1_sample(gpu):
+    """C1 shape (d_model 64, 4x16, depth 32) on a reduced corpus."""
+    from agpt_amd import trie
+    tr = trie.config_trie("C1", scale=0.004)  # 800 chars -> a few thousand node-tokens
+    _check(tr.parent, 4, 16, seed=1, rope=True)
+
+
+@pytest.mark.parametrize("kind", ["single", "roots", "chain256", "tile_edge", "tile_edge1"])
+def test_edge_shapes(gpu, kind):
+    if kind == "single":
+        parent = np.array([-1], np.int32)
+    elif kind == "roots":
+        parent = np.full(130, -1, np.int32)
+    elif kind == "chain256":
+        parent = np.arange(-1, 255, dtype=np.int32)
+    elif kind == "tile_edge":
+        parent = np.concatenate([np.arange(-1, 63), np.arange(63, 127)]).astype(np.int32)
+    else:  # a chain of 65: the tile boundary cuts the deepest row
+        parent = np.arange(-1, 64, dtype=np.int32)
+    _check(parent, 2, 8, seed=len(parent), rope=True, acc=True)
+
+
+def test_deterministic(gpu):
+    import torch
+
+    from agpt_amd.attention import TrieAttention
+    tr = small_trie(n_tokens=3000, depth=24, seed=4)
+    T, H, hd = tr.n_nodes, 8, 16
+    Q, K, V, G = (torch.from_numpy(x).cuda() for x in tensors(T, H * hd, 8))
+    att = TrieAttention(H, hd, max_depth=24)
+    att.plan(tr.parent)
+    outs = []
+    for _ in range(2):
+        o, lse = att.forward(Q, K, V)
+        outs.append([x.clone() for x in (o, lse, *att.backward(Q, K, V, o, lse, G))])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_errors(gpu):
+    import torch
+
+    from agpt_amd._native import AGPT_ERR_NOT_DFS, AGPT_ERR_TOO_DEEP, AgptError
+    from agpt_amd.attention import TrieAttention
+    att = TrieAttention(2, 8, max_depth=4)
+    with pytest.raises(AgptError) as e:
+        att.plan(np.array([-1, 0, -1, 1], np.int32))  # row 3's parent subtree already closed
+    assert e.value.code == AGPT_ERR_NOT_DFS
+    with pytest.raises(AgptError) as e:
+        att.plan(np.arange(-1, 5, dtype=np.int32))  # depth 6 > 4
+    assert e.value.code == AGPT_ERR_TOO_DEEP
+    q = torch.zeros(3, 16, device="cuda")
+    with pytest.raises(ValueError):
+        att.forward(q, q, q)  # no plan: row-count check
+    att.plan(np.array([-1, 0, 1], np.int32))
+    o, lse = att.forward(q, q, q)
+    torch.cuda.synchronize()
+    assert torch.all(o == 0)
+
+
+# ---- packed varlen drop-ins ----------------------------------------------
+
+def _pack_nodes(parent, Q, K, V, H, hd):
+    """Reference packing (batched_depth_forward.cr:668-742): node i's packed
+    prefix = its ancestors' rows then its own, duplicated per node."""
+    depth = ORC.depths(parent)
+    T = parent.shape[0]
+    offs = np.zeros(T, np.int32)
+    lens = depth.astype(np.int32)
+    offs[1:] = np.cumsum(lens)[:-1]
+    rows = []
+    for n in range(T):
+        path = []
+        a = n
+        while a >= 0:
+            path.append(a)
+            a = parent[a]
+        rows.extend(path[::-1])
+    rows = np.array(rows, np.int64)
+    return offs, lens, rows, K[rows], V[rows]
+
+
+def test_varlen_matches_trie(gpu):
+    import torch
+
+    from agpt_amd import attention as A
+    tr = small_trie(n_tokens=300, depth=9, seed=31)
+    T, H, hd = tr.n_nodes, 4, 8
+    D = H * hd
+    Q, K, V, G = tensors(T, D, 13)
+    scale = scale_of(hd)
+    offs, lens, rows, Kp, Vp = _pack_nodes(tr.parent, Q, K, V, H, hd)
+    max_len = int(lens.max())
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    out = torch.zeros(T * D, device="cuda")
+    w = torch.zeros(T * H * max_len, device="cuda")
+    A.batched_varlen_attention(cu(Q), cu(Kp), cu(Vp), cu(offs), cu(lens), out, w, T, H, hd,
+                               max_len, scale)
+    o_ref, w_ref = ORC.varlen_fwd(Q, Kp, Vp, offs, lens, T, H, hd, max_len, scale)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), o_ref, what="varlen O")
+    assert_close(w.cpu().numpy(), w_ref, what="varlen W")
+    unp = torch.empty(T, D, device="cuda")
+    A.unpack_batched_attn_output(out, unp, T, H, hd)
+    dq = torch.zeros(T * D, device="cuda")
+    dk = torch.full((rows.size * D,), 7.0, device="cuda")  # overwritten, not accumulated
+    dv = torch.full((rows.size * D,), 7.0, device="cuda")
+    A.batched_varlen_attention_backward(cu(Q), cu(Kp), cu(Vp), w, cu(G), cu(offs), cu(lens), dq,
+                                        dk, dv, T, H, hd, max_len, scale)
+    dq_r, dk_r, dv_r = ORC.varlen_bwd(Q, Kp, Vp, w_ref, G, offs, lens, T, H, hd, max_len, scale,
+                                      rows.size)
+    torch.cuda.synchronize()
+    assert_close(unp.cpu().numpy().ravel(), o_ref, what="unpack")
+    assert_close(dq.cpu().numpy(), dq_r, what="varlen dQ")
+    assert_close(dk.cpu().numpy(), dk_r, what="varlen dK")
+    assert_close(dv.cpu().numpy(), dv_r, what="varlen dV")
+
+
+def test_varlen_L_queries(gpu):
+    import torch
+
+    from agpt_amd import attention as A
+    from agpt_amd import trie
+    tr = small_trie(n_tokens=500, depth=12, seed=41)
+    rpar, elen = tr.radix()
+    R = rpar.shape[0]
+    H, hd = 2, 16
+    D = H * hd
+    T = tr.n_nodes
+    Q, K, V, G = tensors(T, D, 17)
+    scale = scale_of(hd)
+    # chunk-packer layout (agpt_train.cu:4456-4479): queries of radix node i
+    # are its edge rows; its packed prefix = ancestor rows then edge rows.
+    heads = np.flatnonzero(tr.radix_head)
+    qoff = np.append(heads, T).astype(np.int32)
+    q2n = np.repeat(np.arange(R, dtype=np.int32), elen)
+    kv_rows = []
+    kv_off = np.zeros(R, np.int32)
+    kv_len = np.zeros(R, np.int32)
+    for r in range(R):
+        last = qoff[r + 1] - 1
+        path = []
+        a = last
+        while a >= 0:
+            path.append(a)
+            a = tr.parent[a]
+        kv_off[r] = len(kv_rows)
+        kv_len[r] = len(path)
+        kv_rows.extend(path[::-1])
+    kv_rows = np.array(kv_rows, np.int64)
+    Kp, Vp = K[kv_rows], V[kv_rows]
+    max_kv = int(kv_len.max())
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    out = torch.zeros(T * D, device="cuda")
+    w = torch.zeros(T * H * max_kv, device="cuda")
+    A.batched_varlen_attention_L_queries(cu(Q), cu(Kp), cu(Vp), cu(q2n), cu(qoff), cu(kv_off),
+                                         cu(kv_len), out, w, T, H, hd, max_kv, scale)
+    o_ref, w_ref = ORC.varlen_L_fwd(Q, Kp, Vp, q2n, qoff, kv_off, kv_len, T, H, hd, max_kv, scale)
+    # the radix layout is the trie semantics: same outputs as the trie oracle
+    O_trie, _, _ = ORC.fwd(tr.parent, Q, K, V, H, hd, scale)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), o_ref, what="L O")
+    assert_close(o_ref.reshape(T, D), O_trie, what="L oracle vs trie oracle")
+    dq = torch.zeros(T * D, device="cuda")
+    seed_k = np.random.default_rng(3).standard_normal(kv_rows.size * D).astype(np.float32)
+    dk = cu(seed_k.copy())
+    dv = cu(seed_k.copy())
+    A.batched_varlen_attention_L_queries_backward(cu(Q), cu(Kp), cu(Vp), w, cu(G), cu(q2n),
+                                                  cu(qoff), cu(kv_off), cu(kv_len), dq, dk, dv, T,
+                                                  H, hd, max_kv, scale)
+    dq_r, dk_r, dv_r = ORC.varlen_L_bwd(Q, Kp, Vp, w_ref, G, q2n, qoff, kv_off, kv_len, T, H, hd,
+                                        max_kv, scale, kv_rows.size, dk=seed_k, dv=seed_k)
+    torch.cuda.synchronize()
+    assert_close(dq.cpu().numpy(), dq_r, what="L dQ")
+    assert_close(dk.cpu().numpy(), dk_r, what="L dK")
+    assert_close(dv.cpu().numpy(), dv_r, what="L dV")

@@ -1,0 +1,169 @@
+"""Host logic (CPU only): trie construction, tree validation, DFS ordering,
+and the C ABI of both libraries (loads, exports every declared symbol; no
+device calls)."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from agpt_amd import _native, trie
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared(header: str) -> list[str]:
+    text = (ROOT / "include" / header).read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(agpt_[A-Za-z0-9_]+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header,loader", [("agpt_attn.h", _native.attn_lib),
+                                           ("agpt_trie.h", _native.trie_lib)])
+def test_abi_exports_every_declared_symbol(header, loader):
+    lib = loader()
+    names = _declared(header)
+    assert len(names) >= 8
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    table = _native.ATTN_SYMBOLS if header == "agpt_attn.h" else _native.TRIE_SYMBOLS
+    assert set(table) == set(names)  # the ctypes table binds exactly the header
+
+
+def _brute_prefixes(tokens, max_depth, starts):
+    nodes = set()
+    n = len(tokens)
+    for s in starts:
+        L = min(max_depth, n - 1 - s)
+        for d in range(1, L + 1):
+            nodes.add(tuple(tokens[s:s + d]))
+    return nodes
+
+
+@pytest.mark.parametrize("n,order,vocab,depth,max_starts", [(300, 2, 5, 8, 0), (500, 3, 9, 12, 0),
+                                                            (400, 1, 4, 6, 37)])
+def test_trie_matches_ingest_semantics(n, order, vocab, depth, max_starts):
+    tok = trie.markov_corpus(n, order, vocab, 1.1, seed=n)
+    tr = trie.build_trie(tok, depth, max_starts=max_starts)
+    total = n - 1
+    if max_starts:
+        starts = [(i * total // max_starts) % total for i in range(max_starts)]
+    else:
+        starts = range(total)
+    want = _brute_prefixes(list(tok), depth, starts)
+    # reconstruct each node's path string from the parent links
+    paths = []
+    for i in range(tr.n_nodes):
+        p = tr.parent[i]
+        paths.append((paths[p] if p >= 0 else ()) + (int(tr.token[i]),))
+        assert tr.depth[i] == len(paths[i])
+    assert len(set(paths)) == tr.n_nodes  # no duplicate nodes
+    assert set(paths) == want
+    # DFS preorder with ascending child tokens = lexicographic order of paths
+    assert paths == sorted(paths)
+    # subtree ranges contiguous and exact
+    for i in range(0, tr.n_nodes, max(1, tr.n_nodes // 50)):
+        e = tr.subtree_end[i]
+        assert all(paths[j][:len(paths[i])] == paths[i] for j in range(i, e))
+        assert e == tr.n_nodes or paths[e][:len(paths[i])] != paths[i]
+
+
+def test_trie_stats_radix_and_partitions():
+    tok = trie.markov_corpus(2000, 3, 7, 1.1, seed=4)
+    tr = trie.build_trie(tok, 16)
+    nchild = np.bincount(tr.parent[tr.parent >= 0], minlength=tr.n_nodes)
+    heads = (tr.parent < 0) | (nchild[np.maximum(tr.parent, 0)] != 1)
+    assert tr.n_radix == int(heads.sum()) == int(tr.radix_head.sum())
+    rpar, elen = tr.radix()
+    assert elen.sum() == tr.n_nodes and rpar.shape[0] == tr.n_radix
+    assert np.all(rpar < np.arange(tr.n_radix))
+    # bigram key: (first token << 8) | second token (255 at depth 1)
+    for i in range(0, tr.n_nodes, 97):
+        a, path = i, []
+        while a >= 0:
+            path.append(int(tr.token[a]))
+            a = tr.parent[a]
+        path = path[::-1]
+        second = path[1] if len(path) > 1 else 255
+        assert tr.partition[i] == (path[0] << 8) | second
+
+
+def test_markov_corpus_is_seeded_and_zipf_like():
+    a = trie.markov_corpus(50_000, 3, 65, 1.1, seed=7)
+    b = trie.markov_corpus(50_000, 3, 65, 1.1, seed=7)
+    c = trie.markov_corpus(50_000, 3, 65, 1.1, seed=8)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert a.min() >= 0 and a.max() < 65
+    counts = np.bincount(a, minlength=65)
+    assert counts[:5].sum() > counts[-20:].sum()  # low ranks dominate
+
+
+def test_chain_trie():
+    tok = trie.uniform_tokens(5 * 7, 65, seed=1)
+    tr = trie.build_chains(tok, 5, 7)
+    assert tr.n_nodes == 35 and tr.max_depth == 7 and tr.n_radix == 5
+    assert np.array_equal(tr.parent[:8], [-1, 0, 1, 2, 3, 4, 5, -1])
+
+
+def _check_tree(parent):
+    lib = _native.attn_lib()
+    par = np.ascontiguousarray(parent, np.int32)
+    d = np.zeros(par.shape[0], np.int32)
+    e = np.zeros(par.shape[0], np.int32)
+    rc = lib.agpt_attn_check_tree(par.ctypes.data_as(C.POINTER(C.c_int32)), par.shape[0],
+                                  d.ctypes.data_as(C.POINTER(C.c_int32)),
+                                  e.ctypes.data_as(C.POINTER(C.c_int32)))
+    return rc, d, e
+
+
+def test_check_tree():
+    tok = trie.markov_corpus(300, 2, 5, 1.1, seed=3)
+    tr = trie.build_trie(tok, 9)
+    rc, d, e = _check_tree(tr.parent)
+    assert rc == _native.AGPT_OK
+    assert np.array_equal(d, tr.depth) and np.array_equal(e, tr.subtree_end)
+    assert _check_tree([-1, 0, -1, 1])[0] == _native.AGPT_ERR_NOT_DFS  # closed subtree
+    assert _check_tree([0])[0] == _native.AGPT_ERR_NOT_DFS             # self parent
+    assert _check_tree([-1, 2, 0])[0] == _native.AGPT_ERR_NOT_DFS      # forward parent
+    assert _check_tree([-2])[0] == _native.AGPT_ERR_NOT_DFS
+    rc, d, e = _check_tree([-1, -1, 1, 2, 1])
+    assert rc == 0 and list(d) == [1, 1, 2, 3, 2] and list(e) == [1, 5, 4, 4, 5]
+    msg = _native.attn_lib().agpt_last_error()
+    assert isinstance(msg, bytes)
+
+
+def test_dfs_order_of_arbitrary_forest():
+    rng = np.random.default_rng(0)
+    n = 500
+    # random forest in BFS-like order, then shuffled labels
+    parent = np.array([-1 if i < 5 or rng.random() < 0.05 else int(rng.integers(0, i))
+                       for i in range(n)], np.int32)
+    lab = rng.permutation(n)
+    inv = np.argsort(lab)
+    shuffled = np.array([-1 if parent[inv[j]] < 0 else lab[parent[inv[j]]] for j in range(n)],
+                        np.int32)
+    perm = np.empty(n, np.int32)
+    lib = _native.attn_lib()
+    assert lib.agpt_attn_dfs_order(shuffled.ctypes.data_as(C.POINTER(C.c_int32)), n,
+                                   perm.ctypes.data_as(C.POINTER(C.c_int32))) == 0
+    assert sorted(perm) == list(range(n))
+    pos = np.empty(n, np.int64)
+    pos[perm] = np.arange(n)
+    new_parent = np.array([-1 if shuffled[r] < 0 else pos[shuffled[r]] for r in perm], np.int32)
+    assert _check_tree(new_parent)[0] == 0
+    cyc = np.array([1, 0], np.int32)
+    assert lib.agpt_attn_dfs_order(cyc.ctypes.data_as(C.POINTER(C.c_int32)), 2,
+                                   perm.ctypes.data_as(C.POINTER(C.c_int32))) != 0
+
+
+def test_create_fails_loudly_without_device():
+    """No silent CPU path: without a GPU the handle cannot be created."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from agpt_amd.attention import TrieAttention
+    with pytest.raises(_native.AgptError):
+        TrieAttention(2, 8)
