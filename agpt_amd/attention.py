@@ -104,6 +104,9 @@ class TrieAttention:
                                               C.byref(md)))
         return dict(n_nodes=n.value, n_tiles=nt.value, sum_depth=sd.value, max_depth=md.value)
 
+    def describe(self) -> str:
+        return self._lib.agpt_attn_describe(self._h).decode()
+
     # -- compute ------------------------------------------------------------
     def _opts(self, scale, rope, stream, events=None) -> N.AttnOpts:
         o = N.AttnOpts()

@@ -21,7 +21,8 @@ ARCH = os.environ.get("AGPT_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# Packed-FP32 instructions are disabled for every HIP object.
+# Packed-FP32 instructions are disabled for every HIP object: some of their
+# forms have given silently wrong results on the MI355X pool this targets.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

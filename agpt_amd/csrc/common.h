@@ -10,8 +10,8 @@ int agpt_internal_set_error(int code, const char* msg);
 
 namespace agpt {
 
-// Rows of one tile: a contiguous DFS-preorder range of node-tokens.
-constexpr int kTileQ = 64;
+// Largest tile: a tile is a contiguous DFS-preorder range of node-tokens.
+constexpr int kMaxTileRows = 256;
 // Deepest supported node (keys per query).
 constexpr int kMaxDepth = 256;
 // Widest supported head count (LDS tables are sized for it).

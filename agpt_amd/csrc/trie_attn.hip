@@ -10,7 +10,7 @@
 //   workspace      : Pk, Pv [Σ A_t, D] fp32 (per-tile partial dK/dV of the
 //                    tile's out-of-tile ancestors), Ck, Cv [n_chunks, maxD, D]
 //
-// A tile is kTileQ consecutive rows [s, e). Every ancestor of a row in the
+// A tile is pl.tile consecutive rows [s, e) (64, 128 or 256). Every ancestor of a row in the
 // tile that lies outside the tile is an ancestor of s (preorder), so a tile
 // needs only its own rows plus the A_t = depth(s)-1 "prefix" rows on the path
 // of s (tile_prefix, ordered by depth). Forward and the dQ half of backward
@@ -29,8 +29,10 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 using namespace agpt;
@@ -65,6 +67,12 @@ struct PlanDev {
   int64_t T;
   int32_t n_tiles;
   int32_t max_depth;
+  int32_t tile;  // rows per tile (<= kMaxTileRows)
+  // Fast-kernel work items per tile (agpt_fast::make_item), longest first:
+  const int16_t* q_items;     // query chain groups, by walk length
+  const int32_t* q_item_off;  // [n_tiles + 1]
+  const int16_t* k_items;     // key-set chain groups, by query-range length
+  const int32_t* k_item_off;  // [n_tiles + 1]
 };
 
 // ---------------------------------------------------------------------------
@@ -72,9 +80,9 @@ struct PlanDev {
 // prefix path of the tile's first row.
 // ---------------------------------------------------------------------------
 struct TileShared {
-  int32_t parent[kTileQ];
-  int32_t depth[kTileQ];
-  int32_t end[kTileQ];
+  int32_t parent[kMaxTileRows];
+  int32_t depth[kMaxTileRows];
+  int32_t end[kMaxTileRows];
   int32_t prefix[kMaxDepth];
   int32_t prefix_end[kMaxDepth];
 };
@@ -108,8 +116,8 @@ __global__ __launch_bounds__(256) void trie_fwd_kernel(PlanDev pl, const Tin* __
                                                        float scale) {
   __shared__ TileShared sh;
   const int t = blockIdx.x;
-  const int64_t s = static_cast<int64_t>(t) * kTileQ;
-  const int ntile = static_cast<int>(min<int64_t>(kTileQ, pl.T - s));
+  const int64_t s = static_cast<int64_t>(t) * pl.tile;
+  const int ntile = static_cast<int>(min<int64_t>(pl.tile, pl.T - s));
   const int A = pl.pref_off[t + 1] - pl.pref_off[t];
   load_tile(pl, t, s, ntile, A, sh, false);
   __syncthreads();
@@ -179,8 +187,8 @@ __global__ __launch_bounds__(256) void trie_fwd_kernel(PlanDev pl, const Tin* __
 // ---------------------------------------------------------------------------
 struct BwdShared {
   TileShared tile;
-  float lse2[kTileQ * kMaxHeads];
-  float delta[kTileQ * kMaxHeads];
+  float lse2[kMaxTileRows * kMaxHeads];
+  float delta[kMaxTileRows * kMaxHeads];
 };
 
 struct RopeArgs {
@@ -203,8 +211,8 @@ __global__ __launch_bounds__(256) void trie_bwd_kernel(
     const float* __restrict__ acc_dv, RopeArgs rope, int H, float scale) {
   __shared__ BwdShared sh;
   const int t = blockIdx.x;
-  const int64_t s = static_cast<int64_t>(t) * kTileQ;
-  const int ntile = static_cast<int>(min<int64_t>(kTileQ, pl.T - s));
+  const int64_t s = static_cast<int64_t>(t) * pl.tile;
+  const int ntile = static_cast<int>(min<int64_t>(pl.tile, pl.T - s));
   const int64_t e = s + ntile;
   const int32_t poff = pl.pref_off[t];
   const int A = pl.pref_off[t + 1] - poff;
@@ -422,7 +430,7 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
     const float* __restrict__ Pv, const float* __restrict__ Ck, const float* __restrict__ Cv,
     const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeArgs rope, int H) {
   const int t = blockIdx.x;  // tiles 0 .. n_tiles-2
-  const int64_t s = static_cast<int64_t>(t) * kTileQ;
+  const int64_t s = static_cast<int64_t>(t) * pl.tile;
   const int32_t noff = pl.pref_off[t + 1];
   const int An = pl.pref_off[t + 2] - noff;
   const int D = H * HD;
@@ -432,7 +440,7 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
   for (int k = An - 1 - wave; k >= 0; k -= nwaves) {
     const int64_t a = pl.prefix[noff + k];
     if (a < s) break;  // deeper-first scan: everything above is outside tile t
-    const int u_last = static_cast<int>((pl.end[a] - 1) / kTileQ);
+    const int u_last = static_cast<int>((pl.end[a] - 1) / pl.tile);
     const int pos = rope.cos_t ? rope_pos(k + 1, rope.seq_len) : 0;
     for (int col0 = lane * 2; col0 < D; col0 += 128) {
       float2 sk = *reinterpret_cast<const float2*>(dK + a * D + col0);
@@ -486,6 +494,8 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
 
 }  // namespace
 
+#include "trie_fast.h"
+
 // ===========================================================================
 // Host side: handle, plan, launches.
 // ===========================================================================
@@ -494,6 +504,7 @@ struct agpt_attn_s {
   int device = 0;
   // plan (host copies used for launch geometry)
   int64_t T = 0;
+  int32_t tile = 0;
   int32_t n_tiles = 0;
   int32_t n_chunks = 0;
   int32_t max_depth = 0;
@@ -506,23 +517,43 @@ struct agpt_attn_s {
   int32_t* d_end = nullptr;
   int32_t* d_pref_off = nullptr;
   int32_t* d_prefix = nullptr;
+  // workspace: prefix partials, chunk sums, δ
   float* d_Pk = nullptr;
   float* d_Pv = nullptr;
   float* d_Ck = nullptr;
   float* d_Cv = nullptr;
+  float* d_Dl = nullptr;
+  int16_t* d_q_items = nullptr;
+  int16_t* d_k_items = nullptr;
+  int32_t* d_q_item_off = nullptr;
+  int32_t* d_k_item_off = nullptr;
+  // kernel family chosen at plan time: 0 = global-memory walk (any shape),
+  // 5 = LDS-staged, cost-ordered workgroups per (tile, head group) (trie_fast.h)
+  int variant = 0;
+  int hg = 1, nw = 2, qb = 1, kb = 1;
+  size_t fwd_lds = 0, kv_lds = 0;
+  int max_lds = 65536;
+  std::string desc;
 };
 
 namespace {
 
 void free_plan(agpt_attn_s* h) {
-  int32_t** ip[] = {&h->d_parent, &h->d_depth, &h->d_end, &h->d_pref_off, &h->d_prefix};
+  int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
+                    &h->d_prefix,   &h->d_q_item_off,  &h->d_k_item_off};
   for (auto p : ip)
     if (*p) {
       (void)hipFree(*p);
       *p = nullptr;
     }
-  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv};
+  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv, &h->d_Dl};
   for (auto p : fp)
+    if (*p) {
+      (void)hipFree(*p);
+      *p = nullptr;
+    }
+  int16_t** op[] = {&h->d_q_items, &h->d_k_items};
+  for (auto p : op)
     if (*p) {
       (void)hipFree(*p);
       *p = nullptr;
@@ -542,10 +573,20 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.T = h->T;
   p.n_tiles = h->n_tiles;
   p.max_depth = h->max_depth;
+  p.tile = h->tile;
+  p.q_items = h->d_q_items;
+  p.q_item_off = h->d_q_item_off;
+  p.k_items = h->d_k_items;
+  p.k_item_off = h->d_k_item_off;
   return p;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? std::atoi(v) : dflt;
+}
 
 }  // namespace
 
@@ -554,13 +595,13 @@ int agpt_internal_set_error(int code, const char* msg) { return set_error(code, 
 extern "C" const char* agpt_last_error(void) { return g_last_error.c_str(); }
 
 extern "C" const char* agpt_version(void) {
-  return "agpt_attn gfx950 tile-walk v1 (tile=64, fp32/bf16, hd 4..64)";
+  return "agpt_attn gfx950: wave-per-tile LDS-staged cost-balanced trie attention (fp32/bf16, hd 4..64)";
 }
 
 extern "C" int agpt_attn_check_tree(const int32_t* parent, int64_t n, int32_t* depth,
                                     int32_t* subtree_end) {
   if (n < 0 || (n > 0 && !parent)) return set_error(AGPT_ERR_INVALID_ARG, "null parent table");
-  if (n >= (int64_t{1} << 31) - kTileQ)
+  if (n >= (int64_t{1} << 31) - kMaxTileRows)
     return set_error(AGPT_ERR_INVALID_ARG, "n_nodes %lld exceeds int32 row indexing", (long long)n);
   std::vector<int32_t> dep(static_cast<size_t>(n)), en(static_cast<size_t>(n));
   // Preorder check with a stack of open subtrees: the parent of row i must be
@@ -659,6 +700,50 @@ extern "C" int agpt_attn_destroy(agpt_attn_handle h) {
 
 namespace {
 
+// Picks the kernel family and its shape for the planned batch: the fast
+// kernels (trie_fast.h) when the head slice fits whole 16-byte chunks, the
+// head dim splits into four lane slices of at least four elements, and the
+// staged key set fits the workgroup LDS; otherwise the global-memory walk.
+// Heads per workgroup are chosen so that one row slice is a 128-byte line;
+// chain groups hold up to QB queries / KB keys (at most four).
+// AGPT_ATTN_VARIANT / _HG / _NW / _TILE / _QB / _KB override (tuning).
+void choose_variant(agpt_attn_s* h, int& tile) {
+  const int hd = h->cfg.head_dim, H = h->cfg.n_heads;
+  const int elem = h->cfg.dtype == AGPT_DTYPE_F32 ? 4 : 2;
+  int lim = 65536;
+  (void)hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device);
+  h->max_lds = lim;
+  const int budget = lim - static_cast<int>(sizeof(agpt_fast::Tables)) -
+                     2 * agpt_fast::kMaxTile * 4 * static_cast<int>(sizeof(float));
+  h->variant = env_int("AGPT_ATTN_VARIANT", 5) == 5 ? 5 : 0;
+  if (h->variant != 5) {
+    const int t = env_int("AGPT_ATTN_TILE", 64);
+    tile = (t == 64 || t == 128 || t == 256) ? t : 64;
+    return;
+  }
+  int hg = env_int("AGPT_ATTN_HG", 0);
+  if (hg == 0) {
+    hg = 1;
+    while (hg * 2 <= 4 && H % (hg * 2) == 0 && hg * 2 * hd * elem <= 128) hg *= 2;
+  }
+  h->hg = hg;
+  h->nw = env_int("AGPT_ATTN_NW", 4);
+  h->qb = env_int("AGPT_ATTN_QB", agpt_fast::kGroup);
+  h->kb = env_int("AGPT_ATTN_KB", agpt_fast::kGroup);
+  tile = env_int("AGPT_ATTN_TILE", 64);
+  h->fwd_lds = agpt_fast::query_lds_bytes(h->max_depth, tile, hg, hd, elem);
+  h->kv_lds = agpt_fast::kv_lds_bytes(tile, hg, hd, elem);
+  const bool ok = hd >= 16 && hd <= 64 && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
+                  (h->nw == 1 || h->nw == 2 || h->nw == 4) && (tile == 64 || tile == 128) &&
+                  h->qb >= 1 && h->qb <= agpt_fast::kGroup && h->kb >= 1 && h->kb <= agpt_fast::kGroup &&
+                  (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(budget) &&
+                  h->kv_lds <= static_cast<size_t>(budget);
+  if (!ok) {
+    h->variant = 0;
+    tile = 64;
+  }
+}
+
 template <typename T>
 int upload(T** dst, const std::vector<T>& src) {
   const size_t bytes = std::max<size_t>(src.size(), 1) * sizeof(T);
@@ -680,24 +765,77 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
   }
   if (maxd > h->cfg.max_depth)
     return set_error(AGPT_ERR_TOO_DEEP, "tree depth %d exceeds config max_depth %d", maxd, h->cfg.max_depth);
-  const int32_t n_tiles = static_cast<int32_t>((n + kTileQ - 1) / kTileQ);
+  h->max_depth = maxd;
+  int tile = 64;
+  choose_variant(h, tile);
+  const int32_t n_tiles = static_cast<int32_t>((n + tile - 1) / tile);
   std::vector<int32_t> pref_off(static_cast<size_t>(n_tiles) + 2, 0);
-  for (int32_t t = 0; t < n_tiles; ++t) pref_off[t + 1] = pref_off[t] + depth[static_cast<int64_t>(t) * kTileQ] - 1;
+  for (int32_t t = 0; t < n_tiles; ++t) pref_off[t + 1] = pref_off[t] + depth[static_cast<int64_t>(t) * tile] - 1;
   pref_off[n_tiles + 1] = pref_off[n_tiles];  // sentinel read by the reducer
   std::vector<int32_t> prefix(static_cast<size_t>(pref_off[n_tiles]));
   for (int32_t t = 0; t < n_tiles; ++t) {
-    const int64_t s = static_cast<int64_t>(t) * kTileQ;
+    const int64_t s = static_cast<int64_t>(t) * tile;
     int32_t a = parent[s];
     for (int d = depth[s] - 2; d >= 0; --d) {
       prefix[pref_off[t] + d] = a;
       a = parent[a];
     }
   }
+  // Work items of the fast kernels: chain groups (each row the previous
+  // row's child) of up to qb queries / kb key-set entries, per tile sorted
+  // by cost, longest first (stable).
+  std::vector<int16_t> q_items, k_items;
+  std::vector<int32_t> q_off(static_cast<size_t>(n_tiles) + 1, 0), k_off(static_cast<size_t>(n_tiles) + 1, 0);
+  if (h->variant == 5) {
+    std::vector<std::pair<int, int16_t>> items;
+    auto flush = [&](std::vector<int16_t>& out) {
+      std::stable_sort(items.begin(), items.end(),
+                       [](const std::pair<int, int16_t>& a, const std::pair<int, int16_t>& b) {
+                         return a.first > b.first;
+                       });
+      for (const auto& it : items) out.push_back(it.second);
+      items.clear();
+    };
+    for (int32_t t = 0; t < n_tiles; ++t) {
+      const int64_t s = static_cast<int64_t>(t) * tile;
+      const int nt = static_cast<int>(std::min<int64_t>(tile, n - s));
+      const int A = pref_off[t + 1] - pref_off[t];
+      for (int r = 0; r < nt;) {
+        int c = 1;
+        while (c < h->qb && r + c < nt && parent[s + r + c] == s + r + c - 1) ++c;
+        items.emplace_back(depth[s + r + c - 1], static_cast<int16_t>(agpt_fast::make_item(r, c)));
+        r += c;
+      }
+      flush(q_items);
+      q_off[t + 1] = static_cast<int32_t>(q_items.size());
+      // Key-set entry k: prefix[k] for k < A (entry k-1 is its parent), else
+      // tile row k - A (chained when its parent is the previous entry).
+      auto chained = [&](int k) {
+        if (k < A) return true;
+        const int c = k - A;
+        return c == 0 ? A > 0 : parent[s + c] == s + c - 1;
+      };
+      auto range_len = [&](int k) {
+        if (k < A) return static_cast<int>(std::min<int64_t>(end[prefix[pref_off[t] + k]] - s, nt));
+        const int c = k - A;
+        return static_cast<int>(std::min<int64_t>(end[s + c] - s, nt)) - c;
+      };
+      const int nk = A + nt;
+      for (int k = 0; k < nk;) {
+        int c = 1;
+        while (c < h->kb && k + c < nk && chained(k + c)) ++c;
+        items.emplace_back(range_len(k), static_cast<int16_t>(agpt_fast::make_item(k, c)));
+        k += c;
+      }
+      flush(k_items);
+      k_off[t + 1] = static_cast<int32_t>(k_items.size());
+    }
+  }
   const int D = h->cfg.n_heads * h->cfg.head_dim;
   h->T = n;
+  h->tile = tile;
   h->n_tiles = n_tiles;
   h->n_chunks = (n_tiles + kChunkTiles - 1) / kChunkTiles;
-  h->max_depth = maxd;
   h->sum_depth = sumd;
   h->n_prefix_rows = pref_off[n_tiles];
   std::vector<int32_t> par(parent, parent + n);
@@ -706,12 +844,20 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
   if ((rc = upload(&h->d_end, end)) != AGPT_OK) return rc;
   if ((rc = upload(&h->d_pref_off, pref_off)) != AGPT_OK) return rc;
   if ((rc = upload(&h->d_prefix, prefix)) != AGPT_OK) return rc;
+  if (h->variant == 5) {
+    if ((rc = upload(&h->d_q_items, q_items)) != AGPT_OK) return rc;
+    if ((rc = upload(&h->d_k_items, k_items)) != AGPT_OK) return rc;
+    if ((rc = upload(&h->d_q_item_off, q_off)) != AGPT_OK) return rc;
+    if ((rc = upload(&h->d_k_item_off, k_off)) != AGPT_OK) return rc;
+  }
   const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pk), pbytes));
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pv), pbytes));
   const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Ck), cbytes));
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
+  if (h->variant == 5)
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
   h->planned = true;
   g_last_error.clear();
   return AGPT_OK;
@@ -745,11 +891,26 @@ extern "C" int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_par
     for (int j = 0; j < edge_len[r]; ++j) {
       parent.push_back(static_cast<int32_t>(prev));
       prev = static_cast<int64_t>(parent.size()) - 1;
-      if (prev >= (int64_t{1} << 31) - kTileQ) return set_error(AGPT_ERR_INVALID_ARG, "too many rows");
+      if (prev >= (int64_t{1} << 31) - kMaxTileRows) return set_error(AGPT_ERR_INVALID_ARG, "too many rows");
     }
     last_row[r] = prev;
   }
   return agpt_attn_plan(h, parent.data(), static_cast<int64_t>(parent.size()));
+}
+
+extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
+  if (!h) return "null handle";
+  if (!h->planned) return "no plan";
+  char buf[320];
+  if (h->variant == 5)
+    snprintf(buf, sizeof(buf),
+             "lds-staged chain-grouped: tile_rows=%d tiles=%d heads_per_wg=%d waves_per_wg=%d "
+             "query_group=%d key_group=%d query_lds=%zu kv_lds=%zu lds_limit=%d",
+             h->tile, h->n_tiles, h->hg, h->nw, h->qb, h->kb, h->fwd_lds, h->kv_lds, h->max_lds);
+  else
+    snprintf(buf, sizeof(buf), "global-memory walk: tile_rows=%d tiles=%d", h->tile, h->n_tiles);
+  h->desc = buf;
+  return h->desc.c_str();
 }
 
 extern "C" int agpt_attn_plan_info(agpt_attn_handle h, int64_t* n_nodes, int64_t* n_tiles,
@@ -765,12 +926,11 @@ extern "C" int agpt_attn_plan_info(agpt_attn_handle h, int64_t* n_nodes, int64_t
 
 namespace {
 
-int check_opts(const agpt_attn_s* h, const agpt_attn_opts* o) {
+int check_opts(const agpt_attn_opts* o) {
   if (o && o->rope_cos) {
     if (!o->rope_sin || o->rope_seq_len < 1)
       return set_error(AGPT_ERR_INVALID_ARG, "RoPE needs both tables and rope_seq_len >= 1");
   }
-  (void)h;
   return AGPT_OK;
 }
 
@@ -789,13 +949,46 @@ struct ProfMarks {
   }
 };
 
+int fast_grid(const agpt_attn_s* h) {
+  const int nb = h->n_tiles * (h->cfg.n_heads / h->hg);
+  return ((nb + agpt_fast::kXcds - 1) / agpt_fast::kXcds) * agpt_fast::kXcds;
+}
+
+template <typename Fn>
+void set_lds(Fn fn, size_t bytes) {
+  if (bytes > 65536)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+template <typename Fn>
+void with_124(int v, Fn&& fn) {  // v in {1, 2, 4}
+  if (v == 4) fn(std::integral_constant<int, 4>{});
+  else if (v == 2) fn(std::integral_constant<int, 2>{});
+  else fn(std::integral_constant<int, 1>{});
+}
+
 template <int HD, typename Tin>
 void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, void* o,
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
-  hipLaunchKernelGGL((trie_fwd_kernel<HD, Tin>), dim3(h->n_tiles), dim3(256), 0, st, plan_dev(h),
-                     static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v),
-                     static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+  if (h->variant == 5) {
+    if constexpr (HD >= 16) {
+      with_124(h->hg, [&](auto hgc) {
+        constexpr int HG = decltype(hgc)::value;
+        auto fn = agpt_fast::fwd_kernel<HD, Tin, HG, PlanDev>;
+        set_lds(fn, h->fwd_lds);
+        hipLaunchKernelGGL(fn, dim3(fast_grid(h)), dim3(64 * h->nw), h->fwd_lds, st, plan_dev(h),
+                           static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads,
+                           scale);
+      });
+    }
+  } else {
+    hipLaunchKernelGGL((trie_fwd_kernel<HD, Tin>), dim3(h->n_tiles), dim3(256), 0, st, plan_dev(h),
+                       static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                       static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+  }
   pm.mark(1);
 }
 
@@ -806,20 +999,44 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                 hipStream_t st, const ProfMarks& pm) {
   const int D = h->cfg.n_heads * HD;
   pm.mark(0);
-  hipLaunchKernelGGL((trie_bwd_kernel<HD, Tin>), dim3(h->n_tiles), dim3(256), 0, st, plan_dev(h),
-                     static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v),
-                     static_cast<const Tin*>(o), lse, static_cast<const Tin*>(dO), dq, dk, dv, h->d_Pk,
-                     h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
-  pm.mark(1);
+  if (h->variant == 5) {
+    if constexpr (HD >= 16) {
+      with_124(h->hg, [&](auto hgc) {
+        constexpr int HG = decltype(hgc)::value;
+        auto fq = agpt_fast::bwd_q_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+        set_lds(fq, h->fwd_lds);
+        hipLaunchKernelGGL(fq, dim3(fast_grid(h)), dim3(64 * h->nw), h->fwd_lds, st, plan_dev(h),
+                           static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
+                           static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
+        pm.mark(1);
+        auto fk = agpt_fast::bwd_kv_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+        set_lds(fk, h->kv_lds);
+        hipLaunchKernelGGL(fk, dim3(fast_grid(h)), dim3(64 * h->nw), h->kv_lds, st, plan_dev(h),
+                           static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk,
+                           dv, h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+      });
+    }
+  } else {
+    hipLaunchKernelGGL((trie_bwd_kernel<HD, Tin>), dim3(h->n_tiles), dim3(256), 0, st, plan_dev(h),
+                       static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v),
+                       static_cast<const Tin*>(o), lse, static_cast<const Tin*>(dO), dq, dk, dv, h->d_Pk,
+                       h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+    pm.mark(1);
+  }
+  pm.mark(2);
   if (h->n_tiles > 1) {
     hipLaunchKernelGGL(trie_bwd_chunk_kernel, dim3(h->n_chunks), dim3(256), 0, st, plan_dev(h), h->d_Pk,
                        h->d_Pv, h->d_Ck, h->d_Cv, D);
-    pm.mark(2);
+    pm.mark(3);
     hipLaunchKernelGGL((trie_bwd_reduce_kernel<HD>), dim3(h->n_tiles - 1), dim3(256), 0, st, plan_dev(h),
                        dk, dv, h->d_Pk, h->d_Pv, h->d_Ck, h->d_Cv, acc_dk, acc_dv, rope,
                        h->cfg.n_heads);
+  } else {
+    pm.mark(3);
   }
-  pm.mark(3);
+  pm.mark(4);
 }
 
 template <typename Fn>
@@ -843,7 +1060,7 @@ extern "C" int agpt_attn_fwd(agpt_attn_handle h, const void* q, const void* k, c
   if (!q || !k || !v || !o || !lse) return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse))
     return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
-  int rc = check_opts(h, opts);
+  int rc = check_opts(opts);
   if (rc != AGPT_OK) return rc;
   HIP_TRY(hipSetDevice(h->device));
   const float scale = scale_of(h, opts);
@@ -871,7 +1088,7 @@ extern "C" int agpt_attn_bwd(agpt_attn_handle h, const void* q, const void* k, c
   const void* ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv};
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
-  int rc = check_opts(h, opts);
+  int rc = check_opts(opts);
   if (rc != AGPT_OK) return rc;
   HIP_TRY(hipSetDevice(h->device));
   const float scale = scale_of(h, opts);

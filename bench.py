@@ -62,12 +62,16 @@ class HipEvents:
 
 
 def bytes_per_token(D: int, H: int, b_in: int) -> dict:
-    """Compulsory HBM bytes per node-token, one layer (flash-standard):
-    fwd reads Q,K,V and writes O, lse; bwd reads Q,K,V,O,dO,lse and writes
-    dQ,dK,dV (fp32)."""
+    """HBM bytes per node-token, one layer. "step" is the compulsory
+    (flash-standard) total: fwd reads Q,K,V and writes O, lse; bwd reads
+    Q,K,V,O,dO,lse and writes dQ,dK,dV (fp32). The per-kernel figures are
+    each kernel's own minimal I/O (the backward's query and key halves each
+    read what they need)."""
     fwd = 4 * D * b_in + 4 * H
     bwd = 5 * D * b_in + 4 * H + 3 * D * 4
-    return {"fwd": fwd, "bwd": bwd, "step": fwd + bwd}
+    return {"step": fwd + bwd, "trie_fwd": fwd, "trie_bwd": bwd,
+            "trie_bwd_q": 5 * D * b_in + 4 * H + D * 4 + 4 * H,
+            "trie_bwd_kv": 4 * D * b_in + 8 * H + 2 * D * 4}
 
 
 def make_inputs(tr, D, H, hd, dtype, seed, dev):
@@ -143,10 +147,25 @@ def main() -> int:
     ap.add_argument("--scale", type=float, default=1.0, help="corpus scale (1 = BASELINE size)")
     ap.add_argument("--cpu-rows", type=int, default=300_000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (PMC byte-counter "
+                         "calibration) and exit")
     args = ap.parse_args()
+    if args.copy_probe_mib:
+        import torch
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 copies of {args.copy_probe_mib} MiB "
+            f"(read {args.copy_probe_mib} MiB + write {args.copy_probe_mib} MiB each)")
+        return 0
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one GPU "
-              "(the trie-attention path shards by subtree with no exchange; see DESIGN.md)",
+              "(sharding the trie by subtree needs no exchange beyond the shared top "
+              "rows, but multi-GPU runs are not part of this build)",
               file=sys.stderr)
         return 2
 
@@ -169,7 +188,7 @@ def main() -> int:
     att = TrieAttention(H, hd, max_depth=max(tr.max_depth, 1), dtype=dtype)
     att.plan(tr.parent)
     info = att.plan_info()
-    log(f"plan: {info}")
+    log(f"plan: {info}; kernel: {att.describe()}")
     q, k, v, d_o = make_inputs(tr, D, H, hd, dtype, seed=1234, dev=dev)
     o = torch.empty(T, D, device=dev, dtype=dtype)
     lse = torch.empty(T, H, device=dev, dtype=torch.float32)
@@ -187,7 +206,7 @@ def main() -> int:
         log(f"warmup step {i + 1}/{args.warmup} done")
 
     hev = HipEvents()
-    evs = [(hev.create(2), hev.create(4)) for _ in range(args.steps)]
+    evs = [(hev.create(2), hev.create(5)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -195,18 +214,24 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
-    k_ms = {"trie_fwd": [], "trie_bwd": [], "trie_bwd_chunk": [], "trie_bwd_reduce": []}
+    split = "global-memory" not in att.describe()
+    names = (["trie_fwd", "trie_bwd_q", "trie_bwd_kv"] if split else ["trie_fwd", "trie_bwd"])
+    k_ms = {n: [] for n in names + ["trie_bwd_chunk", "trie_bwd_reduce"]}
     for fe, be in evs:
         k_ms["trie_fwd"].append(hev.ms(fe[0], fe[1]))
-        k_ms["trie_bwd"].append(hev.ms(be[0], be[1]))
-        k_ms["trie_bwd_chunk"].append(hev.ms(be[1], be[2]))
-        k_ms["trie_bwd_reduce"].append(hev.ms(be[2], be[3]))
+        if split:
+            k_ms["trie_bwd_q"].append(hev.ms(be[0], be[1]))
+            k_ms["trie_bwd_kv"].append(hev.ms(be[1], be[2]))
+        else:
+            k_ms["trie_bwd"].append(hev.ms(be[0], be[2]))
+        k_ms["trie_bwd_chunk"].append(hev.ms(be[2], be[3]))
+        k_ms["trie_bwd_reduce"].append(hev.ms(be[3], be[4]))
         hev.destroy(fe + be)
     avg = {n: float(np.mean(x)) for n, x in k_ms.items()}
     log("kernel avg ms: " + ", ".join(f"{n} {m:.3f}" for n, m in avg.items()))
 
     bpt = bytes_per_token(D, H, b_in)
-    kern_bytes = {"trie_fwd": bpt["fwd"] * T, "trie_bwd": bpt["bwd"] * T}
+    kern_bytes = {n: bpt[n] * T for n in names}
     dominant = max(kern_bytes, key=lambda n: avg[n])
     achieved = kern_bytes[dominant] / (avg[dominant] * 1e-3) / 1e9
     ms_step = elapsed / args.steps * 1e3
@@ -237,7 +262,7 @@ def main() -> int:
             "workload": f"{args.workload}: single-layer trie attention fwd+bwd",
             "node_tokens": T, "radix_nodes": tr.n_radix, "sum_depth": tr.sum_depth,
             "max_depth": tr.max_depth, "d_model": D, "heads": H, "head_dim": hd,
-            "corpus_scale": args.scale, "tiles": info["n_tiles"],
+            "corpus_scale": args.scale, "tiles": info["n_tiles"], "kernel": att.describe(),
         },
         "roofline": {
             "bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS,

@@ -117,6 +117,10 @@ int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_parent,
 int agpt_attn_plan_info(agpt_attn_handle h, int64_t* n_nodes, int64_t* n_tiles,
                         int64_t* sum_depth, int32_t* max_depth);
 
+/* Describes the kernel variant chosen for the planned batch (e.g. LDS-staged,
+ * heads per workgroup, LDS bytes); valid until the next plan or destroy. */
+const char* agpt_attn_describe(agpt_attn_handle h);
+
 /* Forward. Q (post-RoPE), K (post-RoPE), V: [T, D] of cfg.dtype.
  * Writes O [T, D] (cfg.dtype) and lse [T, H] fp32, the natural-log
  * log-sum-exp of each query's scaled scores (it replaces the saved weights

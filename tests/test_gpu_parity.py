@@ -15,6 +15,28 @@ from oracle import oracle as ORC
 
 pytestmark = pytest.mark.gpu
 
+# Kernel families selectable at plan time (AGPT_ATTN_* tuning overrides):
+# every parity test below runs against each of them.
+VARIANTS = {
+    "default": {},
+    "fast_hg1_nw1_qb1_kb1": {"AGPT_ATTN_HG": "1", "AGPT_ATTN_NW": "1", "AGPT_ATTN_QB": "1",
+                             "AGPT_ATTN_KB": "1"},
+    "fast_hg4_nw4_t128_qb2_kb4": {"AGPT_ATTN_HG": "4", "AGPT_ATTN_NW": "4", "AGPT_ATTN_TILE": "128",
+                                  "AGPT_ATTN_QB": "2", "AGPT_ATTN_KB": "4"},
+    "global_walk": {"AGPT_ATTN_VARIANT": "0"},
+    "global_walk_t256": {"AGPT_ATTN_VARIANT": "0", "AGPT_ATTN_TILE": "256"},
+}
+
+
+@pytest.fixture(params=list(VARIANTS), autouse=True)
+def variant(request, monkeypatch):
+    for k in ("AGPT_ATTN_VARIANT", "AGPT_ATTN_HG", "AGPT_ATTN_TILE", "AGPT_ATTN_NW",
+              "AGPT_ATTN_QB", "AGPT_ATTN_KB"):
+        monkeypatch.delenv(k, raising=False)
+    for k, v in VARIANTS[request.param].items():
+        monkeypatch.setenv(k, v)
+    return request.param
+
 
 def _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=None, acc=None, max_depth=None):
     import torch
@@ -26,6 +48,7 @@ def _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=None, acc=None, max_depth
     md = max_depth or max(1, int(ORC.depths(tr_parent).max()))
     att = TrieAttention(H, hd, max_depth=md, dtype=tdt)
     att.plan(tr_parent)
+    print("kernel:", att.describe())
     q, k, v, g = (torch.from_numpy(x).to(dev).to(tdt).contiguous() for x in (Q, K, V, G))
     o, lse = att.forward(q, k, v)
     rt = None
