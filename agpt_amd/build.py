@@ -29,6 +29,9 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Matrix-instruction accumulators in ordinary VGPRs: the kernels rescale
+    # and read them between steps, which the AGPR form turns into copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
 ]

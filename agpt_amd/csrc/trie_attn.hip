@@ -26,6 +26,7 @@
 #include "../../include/agpt_attn.h"
 
 #include <algorithm>
+#include <numeric>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -531,7 +532,8 @@ struct agpt_attn_s {
   // 5 = LDS-staged, cost-ordered workgroups per (tile, head group) (trie_fast.h)
   int variant = 0;
   int hg = 1, nw = 2, qb = 1, kb = 1;
-  size_t fwd_lds = 0, kv_lds = 0;
+  bool split = true;  // split long key groups (see agpt_fast::kSplitLen)
+  size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0;
   int max_lds = 65536;
   std::string desc;
 };
@@ -700,21 +702,21 @@ extern "C" int agpt_attn_destroy(agpt_attn_handle h) {
 
 namespace {
 
-// Picks the kernel family and its shape for the planned batch: the fast
-// kernels (trie_fast.h) when the head slice fits whole 16-byte chunks, the
-// head dim splits into four lane slices of at least four elements, and the
-// staged key set fits the workgroup LDS; otherwise the global-memory walk.
+// Picks the kernel family and its shape for the planned batch: the
+// streaming kernels (trie_fast.h, 64-row tiles) when the head slice fits
+// whole 16-byte chunks, the head dim is 16 or 32 (four lane slices of 4 or 8
+// elements; the per-lane registers stay in budget), and the tile context fits
+// the workgroup LDS; otherwise the global-memory walk.
 // Heads per workgroup are chosen so that one row slice is a 128-byte line;
 // chain groups hold up to QB queries / KB keys (at most four).
-// AGPT_ATTN_VARIANT / _HG / _NW / _TILE / _QB / _KB override (tuning).
+// AGPT_ATTN_VARIANT / _HG / _TILE / _QB / _KB override (tuning).
 void choose_variant(agpt_attn_s* h, int& tile) {
   const int hd = h->cfg.head_dim, H = h->cfg.n_heads;
   const int elem = h->cfg.dtype == AGPT_DTYPE_F32 ? 4 : 2;
   int lim = 65536;
   (void)hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device);
   h->max_lds = lim;
-  const int budget = lim - static_cast<int>(sizeof(agpt_fast::Tables)) -
-                     2 * agpt_fast::kMaxTile * 4 * static_cast<int>(sizeof(float));
+  const int budget = lim - static_cast<int>(sizeof(agpt_fast::StreamTables<4>));
   h->variant = env_int("AGPT_ATTN_VARIANT", 5) == 5 ? 5 : 0;
   if (h->variant != 5) {
     const int t = env_int("AGPT_ATTN_TILE", 64);
@@ -727,17 +729,18 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     while (hg * 2 <= 4 && H % (hg * 2) == 0 && hg * 2 * hd * elem <= 128) hg *= 2;
   }
   h->hg = hg;
-  h->nw = env_int("AGPT_ATTN_NW", 4);
   h->qb = env_int("AGPT_ATTN_QB", agpt_fast::kGroup);
   h->kb = env_int("AGPT_ATTN_KB", agpt_fast::kGroup);
-  tile = env_int("AGPT_ATTN_TILE", 64);
-  h->fwd_lds = agpt_fast::query_lds_bytes(h->max_depth, tile, hg, hd, elem);
-  h->kv_lds = agpt_fast::kv_lds_bytes(tile, hg, hd, elem);
-  const bool ok = hd >= 16 && hd <= 64 && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
-                  (h->nw == 1 || h->nw == 2 || h->nw == 4) && (tile == 64 || tile == 128) &&
+  h->split = env_int("AGPT_ATTN_SPLIT", 1) != 0;
+  tile = agpt_fast::kTile;
+  h->fwd_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 1, false, true);
+  h->bq_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4, true);
+  h->kv_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 2, false, false) +
+              agpt_fast::split_scratch_bytes(hg, hd);
+  const bool ok = hd >= 16 && hd <= 32 && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
                   h->qb >= 1 && h->qb <= agpt_fast::kGroup && h->kb >= 1 && h->kb <= agpt_fast::kGroup &&
                   (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(budget) &&
-                  h->kv_lds <= static_cast<size_t>(budget);
+                  h->bq_lds <= static_cast<size_t>(budget) && h->kv_lds <= static_cast<size_t>(budget);
   if (!ok) {
     h->variant = 0;
     tile = 64;
@@ -820,11 +823,24 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
         const int c = k - A;
         return static_cast<int>(std::min<int64_t>(end[s + c] - s, nt)) - c;
       };
+      // A long group whose first entry is one of the first prefix groups is
+      // split into two half-range items (merged in LDS by the kernel), so
+      // that no round is twice as long as the query side's longest.
       const int nk = A + nt;
       for (int k = 0; k < nk;) {
         int c = 1;
         while (c < h->kb && k + c < nk && chained(k + c)) ++c;
-        items.emplace_back(range_len(k), static_cast<int16_t>(agpt_fast::make_item(k, c)));
+        const int len = range_len(k);
+        const bool split = h->split && h->kb == agpt_fast::kGroup && k % agpt_fast::kGroup == 0 &&
+                           k / agpt_fast::kGroup < agpt_fast::kSplitSlots && k < A &&
+                           len > agpt_fast::kSplitLen;
+        if (split) {
+          const int first = agpt_fast::split_first_len(len);
+          items.emplace_back(first, static_cast<int16_t>(agpt_fast::make_item(k, c, 1)));
+          items.emplace_back(len - first, static_cast<int16_t>(agpt_fast::make_item(k, c, 2)));
+        } else {
+          items.emplace_back(len, static_cast<int16_t>(agpt_fast::make_item(k, c)));
+        }
         k += c;
       }
       flush(k_items);
@@ -904,9 +920,9 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   char buf[320];
   if (h->variant == 5)
     snprintf(buf, sizeof(buf),
-             "lds-staged chain-grouped: tile_rows=%d tiles=%d heads_per_wg=%d waves_per_wg=%d "
-             "query_group=%d key_group=%d query_lds=%zu kv_lds=%zu lds_limit=%d",
-             h->tile, h->n_tiles, h->hg, h->nw, h->qb, h->kb, h->fwd_lds, h->kv_lds, h->max_lds);
+             "streaming chain-grouped mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
+             "query_group=%d key_group=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
+             h->tile, h->n_tiles, h->hg, h->qb, h->kb, h->fwd_lds, h->bq_lds, h->kv_lds, h->max_lds);
   else
     snprintf(buf, sizeof(buf), "global-memory walk: tile_rows=%d tiles=%d", h->tile, h->n_tiles);
   h->desc = buf;
@@ -949,9 +965,22 @@ struct ProfMarks {
   }
 };
 
-int fast_grid(const agpt_attn_s* h) {
-  const int nb = h->n_tiles * (h->cfg.n_heads / h->hg);
-  return ((nb + agpt_fast::kXcds - 1) / agpt_fast::kXcds) * agpt_fast::kXcds;
+// Persistent grid of a streaming kernel: as many workgroups as fit on the
+// device at once, a multiple of 8 (XCDs) and of the head-group count, and no
+// more than one per (tile, head group).
+template <typename Fn>
+int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds) {
+  int per_cu = 1, cus = 256;
+  (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                     agpt_fast::kThreads, lds);
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
+  const int n_hg = h->cfg.n_heads / h->hg;
+  const int m = std::lcm(agpt_fast::kXcds, n_hg);
+  const int64_t units = static_cast<int64_t>(h->n_tiles) * n_hg;
+  int64_t g = static_cast<int64_t>(std::max(per_cu, 1)) * cus;
+  g = std::min(g, (units + m - 1) / m * m);
+  g = std::max<int64_t>(g / m * m, m);
+  return static_cast<int>(g);
 }
 
 template <typename Fn>
@@ -973,12 +1002,13 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
   if (h->variant == 5) {
-    if constexpr (HD >= 16) {
+    if constexpr (HD >= 16 && HD <= 32) {
       with_124(h->hg, [&](auto hgc) {
         constexpr int HG = decltype(hgc)::value;
         auto fn = agpt_fast::fwd_kernel<HD, Tin, HG, PlanDev>;
         set_lds(fn, h->fwd_lds);
-        hipLaunchKernelGGL(fn, dim3(fast_grid(h)), dim3(64 * h->nw), h->fwd_lds, st, plan_dev(h),
+        hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds)), dim3(agpt_fast::kThreads), h->fwd_lds,
+                           st, plan_dev(h),
                            static_cast<const Tin*>(q), static_cast<const Tin*>(k),
                            static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads,
                            scale);
@@ -1000,22 +1030,22 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   const int D = h->cfg.n_heads * HD;
   pm.mark(0);
   if (h->variant == 5) {
-    if constexpr (HD >= 16) {
+    if constexpr (HD >= 16 && HD <= 32) {
       with_124(h->hg, [&](auto hgc) {
         constexpr int HG = decltype(hgc)::value;
         auto fq = agpt_fast::bwd_q_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
-        set_lds(fq, h->fwd_lds);
-        hipLaunchKernelGGL(fq, dim3(fast_grid(h)), dim3(64 * h->nw), h->fwd_lds, st, plan_dev(h),
-                           static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+        set_lds(fq, h->bq_lds);
+        hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds)), dim3(agpt_fast::kThreads), h->bq_lds,
+                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
                            static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
                            static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
         pm.mark(1);
         auto fk = agpt_fast::bwd_kv_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
         set_lds(fk, h->kv_lds);
-        hipLaunchKernelGGL(fk, dim3(fast_grid(h)), dim3(64 * h->nw), h->kv_lds, st, plan_dev(h),
-                           static_cast<const Tin*>(q), static_cast<const Tin*>(k),
-                           static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk,
-                           dv, h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+        hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds)), dim3(agpt_fast::kThreads), h->kv_lds,
+                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv,
+                           h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
       });
     }
   } else {

@@ -65,11 +65,12 @@ def bytes_per_token(D: int, H: int, b_in: int) -> dict:
     """HBM bytes per node-token, one layer. "step" is the compulsory
     (flash-standard) total: fwd reads Q,K,V and writes O, lse; bwd reads
     Q,K,V,O,dO,lse and writes dQ,dK,dV (fp32). The per-kernel figures are
-    each kernel's own minimal I/O (the backward's query and key halves each
-    read what they need)."""
+    each kernel's own minimal I/O."""
     fwd = 4 * D * b_in + 4 * H
     bwd = 5 * D * b_in + 4 * H + 3 * D * 4
     return {"step": fwd + bwd, "trie_fwd": fwd, "trie_bwd": bwd,
+            # split backward: the query half reads Q,K,V,O,dO,lse and writes
+            # dQ and δ; the key half reads Q,K,V,dO,lse,δ and writes dK,dV
             "trie_bwd_q": 5 * D * b_in + 4 * H + D * 4 + 4 * H,
             "trie_bwd_kv": 4 * D * b_in + 8 * H + 2 * D * 4}
 
@@ -214,7 +215,7 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
-    split = "global-memory" not in att.describe()
+    split = "split backward" in att.describe()
     names = (["trie_fwd", "trie_bwd_q", "trie_bwd_kv"] if split else ["trie_fwd", "trie_bwd"])
     k_ms = {n: [] for n in names + ["trie_bwd_chunk", "trie_bwd_reduce"]}
     for fe, be in evs:
