@@ -70,9 +70,9 @@ struct PlanDev {
   int32_t max_depth;
   int32_t tile;  // rows per tile (<= kMaxTileRows)
   // Fast-kernel work items per tile (agpt_fast::make_item), longest first:
-  const int16_t* q_items;     // query chain groups, by walk length
+  const int32_t* q_items;     // query chain groups, by walk length
   const int32_t* q_item_off;  // [n_tiles + 1]
-  const int16_t* k_items;     // key-set chain groups, by query-range length
+  const int32_t* k_items;     // key-set chain groups, by query-range length
   const int32_t* k_item_off;  // [n_tiles + 1]
 };
 
@@ -524,15 +524,16 @@ struct agpt_attn_s {
   float* d_Ck = nullptr;
   float* d_Cv = nullptr;
   float* d_Dl = nullptr;
-  int16_t* d_q_items = nullptr;
-  int16_t* d_k_items = nullptr;
+  int32_t* d_q_items = nullptr;
+  int32_t* d_k_items = nullptr;
   int32_t* d_q_item_off = nullptr;
   int32_t* d_k_item_off = nullptr;
   // kernel family chosen at plan time: 0 = global-memory walk (any shape),
   // 5 = LDS-staged, cost-ordered workgroups per (tile, head group) (trie_fast.h)
   int variant = 0;
   int hg = 1, nw = 2, qb = 1, kb = 1;
-  bool split = true;  // split long key groups (see agpt_fast::kSplitLen)
+  bool split = true;  // cut long work items into parts (see agpt_fast::kCutSteps)
+  int q_slots = 0, k_slots = 0;  // scratch slots of cut query / key items per tile
   size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0;
   int max_lds = 65536;
   std::string desc;
@@ -554,7 +555,7 @@ void free_plan(agpt_attn_s* h) {
       (void)hipFree(*p);
       *p = nullptr;
     }
-  int16_t** op[] = {&h->d_q_items, &h->d_k_items};
+  int32_t** op[] = {&h->d_q_items, &h->d_k_items};
   for (auto p : op)
     if (*p) {
       (void)hipFree(*p);
@@ -710,6 +711,8 @@ namespace {
 // Heads per workgroup are chosen so that one row slice is a 128-byte line;
 // chain groups hold up to QB queries / KB keys (at most four).
 // AGPT_ATTN_VARIANT / _HG / _TILE / _QB / _KB override (tuning).
+void fit_scratch(agpt_attn_s* h);
+
 void choose_variant(agpt_attn_s* h, int& tile) {
   const int hd = h->cfg.head_dim, H = h->cfg.n_heads;
   const int elem = h->cfg.dtype == AGPT_DTYPE_F32 ? 4 : 2;
@@ -735,8 +738,8 @@ void choose_variant(agpt_attn_s* h, int& tile) {
   tile = agpt_fast::kTile;
   h->fwd_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 1, false, true);
   h->bq_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4, true);
-  h->kv_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 2, false, false) +
-              agpt_fast::split_scratch_bytes(hg, hd);
+  h->kv_lds = agpt_fast::stream_lds_bytes(h->max_depth, hg, hd, elem, 2, false, false);
+  h->q_slots = h->k_slots = 0;
   const bool ok = hd >= 16 && hd <= 32 && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
                   h->qb >= 1 && h->qb <= agpt_fast::kGroup && h->kb >= 1 && h->kb <= agpt_fast::kGroup &&
                   (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(budget) &&
@@ -744,7 +747,9 @@ void choose_variant(agpt_attn_s* h, int& tile) {
   if (!ok) {
     h->variant = 0;
     tile = 64;
+    return;
   }
+  if (h->split) fit_scratch(h);
 }
 
 template <typename T>
@@ -785,20 +790,53 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
     }
   }
   // Work items of the fast kernels: chain groups (each row the previous
-  // row's child) of up to qb queries / kb key-set entries, per tile sorted
-  // by cost, longest first (stable).
-  std::vector<int16_t> q_items, k_items;
+  // row's child) of up to qb queries / kb key-set entries. Per tile the
+  // longest items (more than kCutSteps 4-row steps) are cut into parts while
+  // scratch slots last; items are then sorted by steps, longest first
+  // (stable).
+  std::vector<int32_t> q_items, k_items;
   std::vector<int32_t> q_off(static_cast<size_t>(n_tiles) + 1, 0), k_off(static_cast<size_t>(n_tiles) + 1, 0);
   if (h->variant == 5) {
-    std::vector<std::pair<int, int16_t>> items;
-    auto flush = [&](std::vector<int16_t>& out) {
+    struct Raw {
+      int len, first, count;  // len: keys walked (queries) / query range (keys)
+    };
+    std::vector<Raw> raw;
+    std::vector<int> order;
+    std::vector<std::pair<int, int32_t>> items;
+    auto emit = [&](bool cut, int slots, int max_parts, std::vector<int32_t>& out) {
+      const size_t m = raw.size();
+      std::vector<int> nparts(m, 1), slot(m, 0);
+      order.resize(m);
+      for (size_t i = 0; i < m; ++i) order[i] = static_cast<int>(i);
+      std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return raw[a].len > raw[b].len; });
+      int used = 0;
+      for (int i : order) {
+        const int nb = (raw[i].len + 3) / 4;
+        if (!cut || used >= slots || nb <= agpt_fast::kCutSteps) break;
+        nparts[i] = std::min(max_parts, (nb + agpt_fast::kCutSteps - 1) / agpt_fast::kCutSteps);
+        slot[i] = used++;
+      }
+      for (size_t i = 0; i < m; ++i) {
+        const int nb = (raw[i].len + 3) / 4;
+        for (int p = 0; p < nparts[i]; ++p) {
+          const int b0 = agpt_fast::part_begin(nb, p, nparts[i]);
+          const int b1 = agpt_fast::part_begin(nb, p + 1, nparts[i]);
+          items.emplace_back(b1 - b0,
+                             agpt_fast::make_item(raw[i].first, raw[i].count, b0, b1, p, nparts[i], slot[i]));
+        }
+      }
       std::stable_sort(items.begin(), items.end(),
-                       [](const std::pair<int, int16_t>& a, const std::pair<int, int16_t>& b) {
+                       [](const std::pair<int, int32_t>& a, const std::pair<int, int32_t>& b) {
                          return a.first > b.first;
                        });
       for (const auto& it : items) out.push_back(it.second);
       items.clear();
+      raw.clear();
     };
+    // Query parts are merged from partial softmax states (forward) and dQ
+    // partials; the bf16 backward needs δ over the whole path first, so its
+    // query items stay whole.
+    const bool cut_q = h->cfg.dtype == AGPT_DTYPE_F32;
     for (int32_t t = 0; t < n_tiles; ++t) {
       const int64_t s = static_cast<int64_t>(t) * tile;
       const int nt = static_cast<int>(std::min<int64_t>(tile, n - s));
@@ -806,10 +844,10 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
       for (int r = 0; r < nt;) {
         int c = 1;
         while (c < h->qb && r + c < nt && parent[s + r + c] == s + r + c - 1) ++c;
-        items.emplace_back(depth[s + r + c - 1], static_cast<int16_t>(agpt_fast::make_item(r, c)));
+        raw.push_back({depth[s + r + c - 1], r, c});
         r += c;
       }
-      flush(q_items);
+      emit(cut_q, h->q_slots, agpt_fast::kQParts, q_items);
       q_off[t + 1] = static_cast<int32_t>(q_items.size());
       // Key-set entry k: prefix[k] for k < A (entry k-1 is its parent), else
       // tile row k - A (chained when its parent is the previous entry).
@@ -823,27 +861,14 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
         const int c = k - A;
         return static_cast<int>(std::min<int64_t>(end[s + c] - s, nt)) - c;
       };
-      // A long group whose first entry is one of the first prefix groups is
-      // split into two half-range items (merged in LDS by the kernel), so
-      // that no round is twice as long as the query side's longest.
       const int nk = A + nt;
       for (int k = 0; k < nk;) {
         int c = 1;
         while (c < h->kb && k + c < nk && chained(k + c)) ++c;
-        const int len = range_len(k);
-        const bool split = h->split && h->kb == agpt_fast::kGroup && k % agpt_fast::kGroup == 0 &&
-                           k / agpt_fast::kGroup < agpt_fast::kSplitSlots && k < A &&
-                           len > agpt_fast::kSplitLen;
-        if (split) {
-          const int first = agpt_fast::split_first_len(len);
-          items.emplace_back(first, static_cast<int16_t>(agpt_fast::make_item(k, c, 1)));
-          items.emplace_back(len - first, static_cast<int16_t>(agpt_fast::make_item(k, c, 2)));
-        } else {
-          items.emplace_back(len, static_cast<int16_t>(agpt_fast::make_item(k, c)));
-        }
+        raw.push_back({range_len(k), k, c});
         k += c;
       }
-      flush(k_items);
+      emit(h->split, h->k_slots, agpt_fast::kKParts, k_items);
       k_off[t + 1] = static_cast<int32_t>(k_items.size());
     }
   }
@@ -921,8 +946,10 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (h->variant == 5)
     snprintf(buf, sizeof(buf),
              "streaming chain-grouped mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
-             "query_group=%d key_group=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
-             h->tile, h->n_tiles, h->hg, h->qb, h->kb, h->fwd_lds, h->bq_lds, h->kv_lds, h->max_lds);
+             "query_group=%d key_group=%d cut_slots=%d/%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu "
+             "lds_limit=%d",
+             h->tile, h->n_tiles, h->hg, h->qb, h->kb, h->q_slots, h->k_slots, h->fwd_lds, h->bq_lds,
+             h->kv_lds, h->max_lds);
   else
     snprintf(buf, sizeof(buf), "global-memory walk: tile_rows=%d tiles=%d", h->tile, h->n_tiles);
   h->desc = buf;
@@ -968,11 +995,28 @@ struct ProfMarks {
 // Persistent grid of a streaming kernel: as many workgroups as fit on the
 // device at once, a multiple of 8 (XCDs) and of the head-group count, and no
 // more than one per (tile, head group).
+// Workgroups of `fn` resident per CU with `lds` dynamic LDS bytes: the
+// runtime's estimate, capped by the LDS a CU holds when each workgroup's
+// static + dynamic LDS is allocated in 512-byte granules (the runtime's
+// estimate does not round, and an over-count leaves the persistent grid's
+// last workgroups waiting for a whole earlier workgroup to finish). 0 if
+// `fn` cannot launch with `lds`.
+template <typename Fn>
+int wg_per_cu(Fn fn, size_t lds, int lds_per_cu) {
+  hipFuncAttributes fa{};
+  if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) != hipSuccess) return 0;
+  const size_t total = (fa.sharedSizeBytes + lds + 511) & ~static_cast<size_t>(511);
+  if (total > static_cast<size_t>(lds_per_cu)) return 0;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), agpt_fast::kThreads,
+                                                   lds) != hipSuccess)
+    return 0;
+  return std::min(n, static_cast<int>(lds_per_cu / total));
+}
+
 template <typename Fn>
 int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds) {
-  int per_cu = 1, cus = 256;
-  (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
-                                                     agpt_fast::kThreads, lds);
+  int per_cu = wg_per_cu(fn, lds, h->max_lds), cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
   const int n_hg = h->cfg.n_heads / h->hg;
   const int m = std::lcm(agpt_fast::kXcds, n_hg);
@@ -1079,6 +1123,67 @@ int dispatch_hd(int hd, Fn&& fn) {
     case 64: fn(std::integral_constant<int, 64>{}); return AGPT_OK;
     default: return set_error(AGPT_ERR_UNSUPPORTED, "head_dim %d", hd);
   }
+}
+
+// Most scratch slots (up to `cap`) that keep the kernel's workgroups per CU
+// at what it reaches with none; `base` is its LDS without scratch.
+template <typename Fn>
+int slots_at_full_occupancy(Fn fn, size_t base, size_t per_slot, int cap, size_t limit) {
+  hipFuncAttributes fa{};
+  if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) != hipSuccess) return 0;
+  const size_t max_dyn = limit > fa.sharedSizeBytes ? limit - fa.sharedSizeBytes : 0;
+  auto occ = [&](size_t lds) {
+    if (lds > max_dyn) return 0;
+    set_lds(fn, lds);
+    return wg_per_cu(fn, lds, static_cast<int>(limit));
+  };
+  const int full = occ(base);
+  if (full == 0) return 0;
+  int s = 0;
+  while (s < cap && occ(base + (s + 1) * per_slot) >= full) ++s;
+  return s;
+}
+
+// Scratch slots of cut items (agpt_fast::kCutSteps): as many as the LDS left
+// beside each streaming kernel holds without costing a workgroup per CU.
+// Query items are shared by the forward and the query-side backward, and
+// are cut for fp32 only. AGPT_ATTN_QSLOTS / AGPT_ATTN_KSLOTS cap the counts.
+template <int HD, typename Tin>
+void fit_scratch_t(agpt_attn_s* h) {
+  with_124(h->hg, [&](auto hgc) {
+    constexpr int HG = decltype(hgc)::value;
+    const size_t lim = static_cast<size_t>(h->max_lds);
+    const size_t fq = agpt_fast::q_scratch_bytes(HG, HD, true) / agpt_fast::kQSlots;
+    const size_t bq = agpt_fast::q_scratch_bytes(HG, HD, false) / agpt_fast::kQSlots;
+    const size_t kq = agpt_fast::k_scratch_bytes(HG, HD) / agpt_fast::kKSlots;
+    int qs = 0;
+    if (std::is_same<Tin, float>::value) {
+      const int cap = std::min(agpt_fast::kQSlots, env_int("AGPT_ATTN_QSLOTS", agpt_fast::kQSlots));
+      qs = std::min(
+          slots_at_full_occupancy(agpt_fast::fwd_kernel<HD, Tin, HG, PlanDev>, h->fwd_lds, fq, cap, lim),
+          slots_at_full_occupancy(agpt_fast::bwd_q_kernel<HD, Tin, HG, PlanDev, RopeArgs>, h->bq_lds, bq, cap,
+                                  lim));
+    }
+    const int kcap = std::min(agpt_fast::kKSlots, env_int("AGPT_ATTN_KSLOTS", agpt_fast::kKSlots));
+    const int ks =
+        slots_at_full_occupancy(agpt_fast::bwd_kv_kernel<HD, Tin, HG, PlanDev, RopeArgs>, h->kv_lds, kq, kcap, lim);
+    h->q_slots = qs;
+    h->k_slots = ks;
+    h->fwd_lds += qs * fq;
+    h->bq_lds += qs * bq;
+    h->kv_lds += ks * kq;
+  });
+}
+
+void fit_scratch(agpt_attn_s* h) {
+  if (h->cfg.head_dim == 16) {
+    if (h->cfg.dtype == AGPT_DTYPE_F32) fit_scratch_t<16, float>(h);
+    else fit_scratch_t<16, bf16_t>(h);
+  } else if (h->cfg.head_dim == 32) {
+    if (h->cfg.dtype == AGPT_DTYPE_F32) fit_scratch_t<32, float>(h);
+    else fit_scratch_t<32, bf16_t>(h);
+  }
+  (void)hipGetLastError();  // a failed probe only means fewer slots
 }
 
 }  // namespace

@@ -65,25 +65,45 @@ constexpr int kGroup = 4;             // chain-group members = lanes per block
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr int kCopyPer = 2;           // prefix-copy jobs per thread (else reload)
 
-// A work item packs (first entry, member count, half): first | count << 10 |
-// half << 13. half 0 = the whole range; 1 / 2 = first / second part of a
-// key group split in two (see split_first_len).
-__host__ __device__ constexpr int item_first(int v) { return v & 1023; }
-__host__ __device__ constexpr int item_count(int v) { return (v >> 10) & 7; }
-__host__ __device__ constexpr int item_half(int v) { return (v >> 13) & 3; }
-__host__ __device__ constexpr int make_item(int first, int count, int half = 0) {
-  return first | (count << 10) | (half << 13);
+// A work item (int32) packs: first entry (bits 0-8), member count (9-11),
+// first step b0 (12-17), last step b1 - 1 (18-23), scratch slot (24-26),
+// part (27-28), part count - 1 (29-30). An item walks 4-row steps [b0, b1)
+// of its group's walk (the path of a query group, the query range of a key
+// group). A long walk is cut into parts of whole steps: part k of n covers
+// steps [k*nb/n, (k+1)*nb/n) of its nb steps; the parts of one group write
+// partial results to scratch slot `slot`, merged in fixed part order after
+// the rounds. n = 1 is a group that is not cut.
+__host__ __device__ constexpr int item_first(int v) { return v & 511; }
+__host__ __device__ constexpr int item_count(int v) { return (v >> 9) & 7; }
+__host__ __device__ constexpr int item_b0(int v) { return (v >> 12) & 63; }
+__host__ __device__ constexpr int item_b1(int v) { return ((v >> 18) & 63) + 1; }
+__host__ __device__ constexpr int item_slot(int v) { return (v >> 24) & 7; }
+__host__ __device__ constexpr int item_part(int v) { return (v >> 27) & 3; }
+__host__ __device__ constexpr int item_nparts(int v) { return ((v >> 29) & 3) + 1; }
+__host__ __device__ constexpr int make_item(int first, int count, int b0, int b1, int part = 0, int nparts = 1,
+                                            int slot = 0) {
+  return first | (count << 9) | (b0 << 12) | ((b1 - 1) << 18) | (slot << 24) | (part << 27) |
+         ((nparts - 1) << 29);
 }
+// First step of part `part` of `nparts` over nb steps.
+__host__ __device__ constexpr int part_begin(int nb, int part, int nparts) { return part * nb / nparts; }
 
-// Key groups with a query range longer than kSplitLen rows are split in
-// two; the first part takes whole 4-row steps. Split groups are the first
-// kSplitSlots prefix groups of a tile (group g = entries 4g..4g+3), and the
-// two parts meet in an LDS scratch slot [g][part][head][member][dK|dV][dim].
-constexpr int kSplitLen = 32;
-constexpr int kSplitSlots = 8;
-__host__ __device__ constexpr int split_first_len(int len) { return 4 * (((len + 3) / 4 + 1) / 2); }
-inline size_t split_scratch_bytes(int HG, int HD) {
-  return static_cast<size_t>(kSplitSlots) * 2 * HG * 4 * 2 * HD * sizeof(float);
+// Cutting: items longer than kCutSteps steps are cut into ceil(nb /
+// kCutSteps) parts, longest items first, while scratch slots last: the
+// query side has kQSlots slots of up to 2 parts, the key side kKSlots slots
+// of up to 4 parts.
+constexpr int kCutSteps = 4;
+constexpr int kQSlots = 8, kQParts = 2;
+constexpr int kKSlots = 8, kKParts = 4;
+// Scratch floats per (slot, part, head, member): the forward keeps the P·V
+// partial (HD), the running max and sum (padded to 16 B); dQ keeps HD;
+// dK|dV keep 2*HD.
+__host__ __device__ constexpr int fwd_part_floats(int HD) { return HD + 4; }
+inline size_t q_scratch_bytes(int HG, int HD, bool fwd) {
+  return static_cast<size_t>(kQSlots) * kQParts * HG * 4 * (fwd ? fwd_part_floats(HD) : HD) * sizeof(float);
+}
+inline size_t k_scratch_bytes(int HG, int HD) {
+  return static_cast<size_t>(kKSlots) * kKParts * HG * 4 * 2 * HD * sizeof(float);
 }
 
 // anc row length: max depth rounded up to whole 4-key steps, plus 4 so that
@@ -209,11 +229,18 @@ struct StreamTables {
   int32_t depth[kTile];
   int32_t tend[kTile];        // absolute subtree end of the tile rows
   int32_t pend[kMaxDepth];    // absolute subtree end of the prefix slots
-  int16_t qitem[kTile];
-  int16_t kitem[kTile + kMaxDepth];
+  int32_t qitem[kTile + kQSlots * (kQParts - 1)];
+  int32_t kitem[kTile + kMaxDepth + kKSlots * kKParts];
   float l2[HG][kTile];        // lse * log2(e) of the tile rows (backward)
   float dl[HG][kTile];        // δ of the tile rows (backward)
+  int32_t cut[kWaves];        // per wave: some item it loaded is cut
 };
+
+// Item counts per tile: one query item per row at most, one key item per
+// key-set entry (prefix + rows), plus the extra parts of cut items; the item
+// fields hold the slot and part numbers.
+static_assert(kQSlots <= 8 && kKSlots <= 8 && kQParts <= 4 && kKParts <= 4, "item fields");
+static_assert(kMaxDepth <= 4 * 64 && kTile <= 4 * 64 && kMaxDepth + kTile <= 512, "item fields");
 
 // The workgroup's head group and tile range [t0, t1).
 __device__ __forceinline__ void assign_range(int n_tiles, int n_hg, int& hg, int& t0, int& t1) {
@@ -263,6 +290,7 @@ struct Stream {
   StreamTables<HG>& tb;
   // current tile
   int t, s, ntile, A, poff, nq, nk;
+  bool cut;  // the tile has cut items (a merge pass follows its rounds)
   // next tile (prefetched)
   int n_t, n_s, n_ntile, n_A, n_poff, n_qoff, n_nq, n_koff, n_nk;
   u4 kv[KV_PER];
@@ -427,12 +455,20 @@ struct Stream {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     if (tid < 64) tb.depth[tid] = dep;
-    if constexpr (kQ)
-      if (tid < n_nq) tb.qitem[tid] = static_cast<int16_t>(qit);
+    bool cut_here = false;
+    if constexpr (kQ) {
+      if (tid < n_nq) tb.qitem[tid] = qit;
+      cut_here = tid < n_nq && item_nparts(qit) > 1;
+    }
     if constexpr (kK) {
       if (tid < n_ntile) tb.tend[tid] = tend_r;
-      if (tid < n_nk) tb.kitem[tid] = static_cast<int16_t>(kit0);
-      if (tid + kThreads < n_nk) tb.kitem[tid + kThreads] = static_cast<int16_t>(kit1);
+      if (tid < n_nk) tb.kitem[tid] = kit0;
+      if (tid + kThreads < n_nk) tb.kitem[tid + kThreads] = kit1;
+      cut_here = (tid < n_nk && item_nparts(kit0) > 1) || (tid + kThreads < n_nk && item_nparts(kit1) > 1);
+    }
+    {
+      const bool any_cut = __any(cut_here);
+      if (lane == 0) tb.cut[wave] = any_cut;
     }
     if (tid < n_ntile * HG) {
       const int r = tid / HG;
@@ -461,6 +497,7 @@ struct Stream {
     if constexpr (kQ) nq = n_nq;
     if constexpr (kK) nk = n_nk;
     __syncthreads();
+    cut = (tb.cut[0] | tb.cut[1] | tb.cut[2] | tb.cut[3]) != 0;
   }
 
   // Slot of tile row r, and of key-set entry k (prefix entries first).
@@ -483,10 +520,19 @@ __device__ __forceinline__ int pick(const int (&sl)[kGroup], int x) {
   return x & 2 ? hi : lo;
 }
 
-// Query chain group of one quad: rows, depths and the member this lane owns.
+// Walk steps of a round: those of its first (longest) item.
+__device__ __forceinline__ int round_steps(int it) { return uniform(item_b1(it) - item_b0(it)); }
+
+// Query chain group of one quad: rows, depths, the member this lane owns and
+// the item's part: steps [b0, b1) of the path walk; member x takes the keys
+// at path index < lim.
 struct QueryItem {
-  int r0, cnt, rl, p_last, pm, rx;
+  int it, r0, cnt, rl, p_last, pm, rx, b0, b1, lim;
   bool live;
+  // Step index of walk step b (clamped into the part: past-the-end steps are
+  // masked by lim).
+  __device__ __forceinline__ int step(int b) const { return min(b0 + b, b1 - 1); }
+  __device__ __forceinline__ bool key_live(int b, int r) const { return 4 * (b0 + b) + r < lim; }
 };
 
 template <int HG>
@@ -495,12 +541,16 @@ __device__ __forceinline__ QueryItem query_item(const StreamTables<HG>& tb, int 
   QueryItem q;
   q.live = pos < n_items;
   const int it = tb.qitem[q.live ? pos : first];
+  q.it = it;
   q.r0 = item_first(it);
   q.cnt = item_count(it);
   q.rl = q.r0 + q.cnt - 1;
   q.p_last = tb.depth[q.rl];
   q.pm = (q.live && x < q.cnt) ? q.p_last - (q.cnt - 1 - x) : 0;  // member x sees depths d < pm
   q.rx = q.r0 + min(x, q.cnt - 1);
+  q.b0 = item_b0(it);
+  q.b1 = item_b1(it);
+  q.lim = min(q.pm, 4 * q.b1);
   return q;
 }
 
@@ -521,6 +571,12 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   assign_range(pl.n_tiles, H / HG, hg, t0, t1);
   if (t0 >= t1) return;
   ST st(pl, K, V, Q, nullptr, nullptr, nullptr, nullptr, H, hg, dyn, tb);
+  // Scratch of cut items: [slot][part][head][member][P·V (HD) | m, l, pad].
+  constexpr int FP = fwd_part_floats(HD);
+  float* scr = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));
+  auto scr_at = [&](int slot, int part, int hh, int m) {
+    return scr + (((slot * kQParts + part) * HG + hh) * kGroup + m) * FP;
+  };
   const int D = H * HD;
   const Lane<HG> ln;
   const int x = ln.x;
@@ -534,8 +590,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
     if (t + 1 < t1) st.prefetch(t + 1);
     for (int round = ln.wave; round * ITEMS < st.nq; round += kWaves) {
       const int first = round * ITEMS;
-      const int f_it = tb.qitem[first];
-      const int nblk = uniform((tb.depth[item_first(f_it) + item_count(f_it) - 1] + 3) >> 2);
+      const int nblk = round_steps(tb.qitem[first]);
       const QueryItem qi = query_item<HG>(tb, st.nq, first + ln.slot, first, x);
       float q[HD], ks[HD];
       load_vec<HD>(st.Ts + qi.rx * WS + hoff, q);
@@ -549,7 +604,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
       for (int i = 0; i < DPL; ++i) acc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
       for (int b = 0; b < nblk; ++b) {
         int sl[kGroup];
-        st.slots(qi.rl, b, sl);
+        st.slots(qi.rl, qi.step(b), sl);
         float kr[HD], vc[kGroup][DPL];
         load_vec<HD>(st.Ks + pick(sl, x) * WS + hoff, kr);
 #pragma unroll
@@ -558,7 +613,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
         float sc[kGroup], mx = m;
 #pragma unroll
         for (int r = 0; r < kGroup; ++r) {
-          sc[r] = 4 * b + r < qi.pm ? sv[r] : -__builtin_inff();
+          sc[r] = qi.key_live(b, r) ? sv[r] : -__builtin_inff();
           mx = fmaxf(mx, sc[r]);
         }
         const bool resc = mx > m + kRescaleLog2;
@@ -581,6 +636,26 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
         }
         mfma_accum<DPL>(acc, p, vc);
       }
+      if (item_nparts(qi.it) > 1) {
+        // One part of a cut item: its softmax state to the scratch slot.
+        if (qi.live) {
+          const int sl = item_slot(qi.it), pt = item_part(qi.it);
+#pragma unroll
+          for (int g = 0; g < kGroup; ++g) {
+            if (g < qi.cnt) {
+              float o[DPL];
+#pragma unroll
+              for (int i = 0; i < DPL; ++i) o[i] = acc[i][g];
+              store_vec<DPL>(scr_at(sl, pt, ln.hl, g) + x * DPL, o);
+            }
+          }
+          if (x < qi.cnt) {
+            scr_at(sl, pt, ln.hl, x)[HD] = m;
+            scr_at(sl, pt, ln.hl, x)[HD + 1] = l;
+          }
+        }
+        continue;
+      }
       const float inv = qi.pm > 0 ? 1.0f / l : 0.0f;
       float il[kGroup];
       quad_bcast_all(inv, il);
@@ -595,6 +670,49 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
           }
         }
         if (x < qi.cnt) lse[(static_cast<int64_t>(st.s) + qi.rx) * H + h] = (m + fast_log2(l)) * kLn2;
+      }
+    }
+    // Cut items: combine the parts' softmax states in part order. One thread
+    // per (member, head, DPL-slice) of an item.
+    if (st.cut) {
+      __syncthreads();
+      constexpr int kJobs = kGroup * HG * kGroup;
+      for (int j = threadIdx.x; j < st.nq * kJobs; j += kThreads) {
+        const int it = tb.qitem[j / kJobs];
+        if (item_nparts(it) == 1 || item_part(it) != 0) continue;
+        const int r = j % kJobs;
+        const int g = r / (HG * kGroup);
+        const int hh = (r / kGroup) % HG;
+        const int d0 = (r % kGroup) * DPL;
+        if (g >= item_count(it)) continue;
+        const int sl = item_slot(it), np = item_nparts(it);
+        float mp[kQParts], mx = -__builtin_inff();
+#pragma unroll
+        for (int p = 0; p < kQParts; ++p) {
+          mp[p] = p < np ? scr_at(sl, p, hh, g)[HD] : -__builtin_inff();
+          mx = fmaxf(mx, mp[p]);
+        }
+        float l = 0.0f, o[DPL];
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < kQParts; ++p) {
+          if (p < np) {
+            const float a = fast_exp2(mp[p] - mx);
+            float y[DPL];
+            load_vec<DPL>(scr_at(sl, p, hh, g) + d0, y);
+            l += a * scr_at(sl, p, hh, g)[HD + 1];
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) o[i] += a * y[i];
+          }
+        }
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[i] *= inv;
+        const int64_t row = static_cast<int64_t>(st.s) + item_first(it) + g;
+        const int hd = hg * HG + hh;
+        store_vec<DPL>(O + row * D + hd * HD + d0, o);
+        if (d0 == 0) lse[row * H + hd] = (mx + fast_log2(l)) * kLn2;
       }
     }
     if (t + 1 < t1) st.commit(false);
@@ -624,6 +742,12 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   assign_range(pl.n_tiles, H / HG, hg, t0, t1);
   if (t0 >= t1) return;
   ST st(pl, K, V, Q, dO, O, lse, nullptr, H, hg, dyn, tb);
+  // Scratch of cut items (fp32 only: the bf16 δ walk needs the whole path):
+  // [slot][part][head][member][HD] dQ partials.
+  float* scr = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));
+  auto scr_at = [&](int slot, int part, int hh, int m) {
+    return scr + (((slot * kQParts + part) * HG + hh) * kGroup + m) * HD;
+  };
   const int D = H * HD;
   const Lane<HG> ln;
   const int x = ln.x;
@@ -640,8 +764,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     const int64_t s = st.s;
     for (int round = ln.wave; round * ITEMS < st.nq; round += kWaves) {
       const int first = round * ITEMS;
-      const int f_it = tb.qitem[first];
-      const int nblk = uniform((tb.depth[item_first(f_it) + item_count(f_it) - 1] + 3) >> 2);
+      const int nblk = round_steps(tb.qitem[first]);
       const QueryItem qi = query_item<HG>(tb, st.nq, first + ln.slot, first, x);
       const float l2 = tb.l2[ln.hl][qi.rx];
       float q[HD], go[HD];
@@ -651,7 +774,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       for (int i = 0; i < HD; ++i) q[i] *= qscale;
       // Scores and dO·v of step b: lane x gets member x against the 4 keys.
       auto step = [&](int b, int (&sl)[kGroup], f4& sv, f4& tv) {
-        st.slots(qi.rl, b, sl);
+        st.slots(qi.rl, qi.step(b), sl);
         const int mine = pick(sl, x);
         float kr[HD], vr[HD];
         load_vec<HD>(st.Ks + mine * WS + hoff, kr);
@@ -671,7 +794,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           step(b, sl, sv, tv);
 #pragma unroll
           for (int r = 0; r < kGroup; ++r) {
-            const float w = 4 * b + r < qi.pm ? fast_exp2(sv[r] - l2) : 0.0f;
+            const float w = qi.key_live(b, r) ? fast_exp2(sv[r] - l2) : 0.0f;
             dl += w * tv[r];
           }
         }
@@ -686,7 +809,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         float ds[kGroup];
 #pragma unroll
         for (int r = 0; r < kGroup; ++r) {
-          const float w = 4 * b + r < qi.pm ? fast_exp2(sv[r] - l2) : 0.0f;
+          const float w = qi.key_live(b, r) ? fast_exp2(sv[r] - l2) : 0.0f;
           ds[r] = w * (tv[r] - dl) * scale;
         }
         // The key rows are dead here; keep the chunk loads below this point
@@ -697,7 +820,20 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         for (int k = 0; k < kGroup; ++k) load_vec<DPL>(st.Ks + sl[k] * WS + hoff + x * DPL, kc[k]);
         mfma_accum<DPL>(dq, ds, kc);
       }
-      if (qi.live) {
+      if (qi.live && item_nparts(qi.it) > 1) {
+        // One part of a cut item: its dQ partial to the scratch slot.
+        const int sl = item_slot(qi.it), pt = item_part(qi.it);
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+          if (g < qi.cnt) {
+            float v[DPL];
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) v[i] = dq[i][g];
+            store_vec<DPL>(scr_at(sl, pt, ln.hl, g) + x * DPL, v);
+          }
+        }
+        if (pt == 0 && x < qi.cnt) Dl[(s + qi.rx) * H + h] = dl;
+      } else if (qi.live) {
 #pragma unroll
         for (int g = 0; g < kGroup; ++g) {
           if (g < qi.cnt) {
@@ -711,6 +847,39 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           }
         }
         if (x < qi.cnt) Dl[(s + qi.rx) * H + h] = dl;
+      }
+    }
+    // Cut items: sum the dQ partials in part order, then inverse RoPE. One
+    // thread per (member, head, DPL-slice) of an item.
+    if (st.cut) {
+      __syncthreads();
+      constexpr int kJobs = kGroup * HG * kGroup;
+      for (int j = threadIdx.x; j < st.nq * kJobs; j += kThreads) {
+        const int it = tb.qitem[j / kJobs];
+        if (item_nparts(it) == 1 || item_part(it) != 0) continue;
+        const int r = j % kJobs;
+        const int g = r / (HG * kGroup);
+        const int hh = (r / kGroup) % HG;
+        const int d0 = (r % kGroup) * DPL;
+        const int cnt = item_count(it);
+        if (g >= cnt) continue;
+        const int sl = item_slot(it), np = item_nparts(it);
+        float v[DPL];
+        load_vec<DPL>(scr_at(sl, 0, hh, g) + d0, v);
+#pragma unroll
+        for (int p = 1; p < kQParts; ++p) {
+          if (p < np) {
+            float y[DPL];
+            load_vec<DPL>(scr_at(sl, p, hh, g) + d0, y);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) v[i] += y[i];
+          }
+        }
+        const int r0 = item_first(it);
+        if (rope.cos_t)
+          rope_inverse_part<DPL, HD>(v, rope.cos_t, rope.sin_t,
+                                     rope_pos(tb.depth[r0 + cnt - 1] - (cnt - 1 - g), rope.seq_len), d0);
+        store_vec<DPL>(dQ + (s + r0 + g) * D + (hg * HG + hh) * HD + d0, v);
       }
     }
     if (t + 1 < t1) st.commit(false);
@@ -740,15 +909,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   assign_range(pl.n_tiles, H / HG, hg, t0, t1);
   if (t0 >= t1) return;
   ST st(pl, K, V, Q, dO, nullptr, lse, Dl, H, hg, dyn, tb);
-  // Scratch of split key groups: [slot][part][head][member][dK|dV][HD].
+  // Scratch of cut items: [slot][part][head][member][dK|dV][HD].
   float* scr = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));
   auto scr_at = [&](int slot, int part, int hh, int m, int kv) {
-    return scr + ((((slot * 2 + part) * HG + hh) * kGroup + m) * 2 + kv) * HD;
+    return scr + ((((slot * kKParts + part) * HG + hh) * kGroup + m) * 2 + kv) * HD;
   };
   const int D = H * HD;
   const Lane<HG> ln;
   const int x = ln.x;
-  const int h = hg * HG + ln.hl;
   const int hoff = ln.hl * HD;
   const float qscale = scale * kLog2e;
   const Tin* Qs = st.Ts;
@@ -766,17 +934,13 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
     auto range_hi = [&](int k) {
       return k < A ? min(tb.pend[k] - st.s, ntile) : min(tb.tend[k - A] - st.s, ntile);
     };
-    // Query range of item `it`: its group's range, or the part of it.
+    // Query range of item `it`: its steps of the group's range (the first
+    // member's range contains the others').
     auto part_range = [&](int it, int& lo, int& hi) {
       const int k0 = item_first(it);
-      lo = range_lo(k0);
-      hi = range_hi(k0);  // the first member's range contains the others'
-      const int half = item_half(it);
-      if (half != 0) {
-        const int mid = lo + split_first_len(hi - lo);
-        if (half == 1) hi = mid;
-        else lo = mid;
-      }
+      const int glo = range_lo(k0);
+      lo = glo + 4 * item_b0(it);
+      hi = min(glo + 4 * item_b1(it), range_hi(k0));
     };
     // Final dK/dV of key-set entry ki (dims x*DPL.. of head h): prefix keys
     // leave the tile's partial in Pk/Pv; tile rows whose subtree ends inside
@@ -812,9 +976,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
     };
     for (int round = ln.wave; round * ITEMS < st.nk; round += kWaves) {
       const int first = round * ITEMS;
-      int flo, fhi;
-      part_range(tb.kitem[first], flo, fhi);
-      const int nblk = uniform((fhi - flo + 3) >> 2);
+      const int nblk = round_steps(tb.kitem[first]);
       const int pos = first + ln.slot;
       const bool live = pos < st.nk;
       const int it = tb.kitem[live ? pos : first];
@@ -873,7 +1035,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
         mfma_accum<DPL>(dv, w, gc);
       }
       if (!live) continue;
-      const int half = item_half(it);
+      const bool cut = item_nparts(it) > 1;
 #pragma unroll
       for (int g = 0; g < kGroup; ++g) {
         if (g >= cnt) continue;
@@ -883,40 +1045,45 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           gk[i] = dk[i][g];
           gv[i] = dv[i][g];
         }
-        if (half != 0) {  // one part of a split group: to the scratch slot
-          store_vec<DPL>(scr_at(k0 / kGroup, half - 1, ln.hl, g, 0) + x * DPL, gk);
-          store_vec<DPL>(scr_at(k0 / kGroup, half - 1, ln.hl, g, 1) + x * DPL, gv);
+        if (cut) {  // one part of a cut item: to the scratch slot
+          store_vec<DPL>(scr_at(item_slot(it), item_part(it), ln.hl, g, 0) + x * DPL, gk);
+          store_vec<DPL>(scr_at(item_slot(it), item_part(it), ln.hl, g, 1) + x * DPL, gv);
         } else {
           emit(k0 + g, ln.hl, x * DPL, gk, gv);
         }
       }
     }
-    // Split groups: both parts are in the scratch; sum them in a fixed order
-    // (first part + second part) and emit. One thread per (member, head,
-    // DPL-slice) of a group.
-    __syncthreads();
-    {
+    // Cut items: sum the parts in part order and emit. One thread per
+    // (member, head, DPL-slice) of an item.
+    if (st.cut) {
+      __syncthreads();
       constexpr int kJobs = kGroup * HG * kGroup;  // member, head, slice
       for (int j = threadIdx.x; j < st.nk * kJobs; j += kThreads) {
         const int it = tb.kitem[j / kJobs];
-        if (item_half(it) != 1) continue;
+        if (item_nparts(it) == 1 || item_part(it) != 0) continue;
         const int r = j % kJobs;
         const int g = r / (HG * kGroup);
         const int hh = (r / kGroup) % HG;
         const int d0 = (r % kGroup) * DPL;
         if (g >= item_count(it)) continue;
-        const int slot = item_first(it) / kGroup;
-        float a0[DPL], a1[DPL], b0[DPL], b1[DPL];
-        load_vec<DPL>(scr_at(slot, 0, hh, g, 0) + d0, a0);
-        load_vec<DPL>(scr_at(slot, 1, hh, g, 0) + d0, a1);
-        load_vec<DPL>(scr_at(slot, 0, hh, g, 1) + d0, b0);
-        load_vec<DPL>(scr_at(slot, 1, hh, g, 1) + d0, b1);
+        const int sl = item_slot(it), np = item_nparts(it);
+        float a[DPL], b[DPL];
+        load_vec<DPL>(scr_at(sl, 0, hh, g, 0) + d0, a);
+        load_vec<DPL>(scr_at(sl, 0, hh, g, 1) + d0, b);
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) {
-          a0[i] += a1[i];
-          b0[i] += b1[i];
+        for (int p = 1; p < kKParts; ++p) {
+          if (p < np) {
+            float y[DPL], z[DPL];
+            load_vec<DPL>(scr_at(sl, p, hh, g, 0) + d0, y);
+            load_vec<DPL>(scr_at(sl, p, hh, g, 1) + d0, z);
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) {
+              a[i] += y[i];
+              b[i] += z[i];
+            }
+          }
         }
-        emit(item_first(it) + g, hh, d0, a0, b0);
+        emit(item_first(it) + g, hh, d0, a, b);
       }
     }
     if (t + 1 < t1) st.commit(false);
