@@ -496,6 +496,7 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
 }  // namespace
 
 #include "trie_fast.h"
+#include "trie_block.h"
 
 // ===========================================================================
 // Host side: handle, plan, launches.
@@ -529,7 +530,8 @@ struct agpt_attn_s {
   int32_t* d_q_item_off = nullptr;
   int32_t* d_k_item_off = nullptr;
   // kernel family chosen at plan time: 0 = global-memory walk (any shape),
-  // 5 = LDS-staged, cost-ordered workgroups per (tile, head group) (trie_fast.h)
+  // 5 = streaming chain-group walk (trie_fast.h), 6 = streaming block-sparse
+  // 16x16 matrix tiles (trie_block.h)
   int variant = 0;
   int hg = 1, nw = 2, qb = 1, kb = 1;
   bool split = true;  // cut long work items into parts (see agpt_fast::kCutSteps)
@@ -720,7 +722,28 @@ void choose_variant(agpt_attn_s* h, int& tile) {
   (void)hipDeviceGetAttribute(&lim, hipDeviceAttributeMaxSharedMemoryPerBlock, h->device);
   h->max_lds = lim;
   const int budget = lim - static_cast<int>(sizeof(agpt_fast::StreamTables<4>));
-  h->variant = env_int("AGPT_ATTN_VARIANT", 5) == 5 ? 5 : 0;
+  {
+    const int v = env_int("AGPT_ATTN_VARIANT", 6);
+    h->variant = (v == 5 || v == 6) ? v : 0;
+  }
+  if (h->variant == 6) {
+    int hg = env_int("AGPT_ATTN_HG", 0);
+    if (hg == 0) {
+      hg = 1;
+      while (hg * 2 <= 4 && H % (hg * 2) == 0 && hg * 2 * hd * elem <= 128) hg *= 2;
+    }
+    h->hg = hg;
+    tile = agpt_blk::kTile;
+    h->fwd_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 1, false);
+    h->bq_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4);
+    h->kv_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, false);
+    const int bbudget = lim - static_cast<int>(sizeof(agpt_blk::BlockTables<4>));
+    const bool ok = (hd == 16 || hd == 32) && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
+                    (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(bbudget) &&
+                    h->bq_lds <= static_cast<size_t>(bbudget) && h->kv_lds <= static_cast<size_t>(bbudget);
+    if (ok) return;
+    h->variant = 5;  // try the chain-group walk
+  }
   if (h->variant != 5) {
     const int t = env_int("AGPT_ATTN_TILE", 64);
     tile = (t == 64 || t == 128 || t == 256) ? t : 64;
@@ -897,7 +920,7 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
   const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Ck), cbytes));
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
-  if (h->variant == 5)
+  if (h->variant == 5 || h->variant == 6)
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
   h->planned = true;
   g_last_error.clear();
@@ -943,7 +966,12 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (!h) return "null handle";
   if (!h->planned) return "no plan";
   char buf[320];
-  if (h->variant == 5)
+  if (h->variant == 6)
+    snprintf(buf, sizeof(buf),
+             "streaming block-sparse 16x16 mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
+             "fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
+             h->tile, h->n_tiles, h->hg, h->fwd_lds, h->bq_lds, h->kv_lds, h->max_lds);
+  else if (h->variant == 5)
     snprintf(buf, sizeof(buf),
              "streaming chain-grouped mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
              "query_group=%d key_group=%d cut_slots=%d/%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu "
@@ -1045,7 +1073,18 @@ template <int HD, typename Tin>
 void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, void* o,
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
-  if (h->variant == 5) {
+  if (h->variant == 6) {
+    if constexpr (HD == 16 || HD == 32) {
+      with_124(h->hg, [&](auto hgc) {
+        constexpr int HG = decltype(hgc)::value;
+        auto fn = agpt_blk::fwd_kernel<HD, Tin, HG, PlanDev>;
+        set_lds(fn, h->fwd_lds);
+        hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds)), dim3(agpt_blk::kThreads), h->fwd_lds,
+                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+      });
+    }
+  } else if (h->variant == 5) {
     if constexpr (HD >= 16 && HD <= 32) {
       with_124(h->hg, [&](auto hgc) {
         constexpr int HG = decltype(hgc)::value;
@@ -1073,7 +1112,26 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                 hipStream_t st, const ProfMarks& pm) {
   const int D = h->cfg.n_heads * HD;
   pm.mark(0);
-  if (h->variant == 5) {
+  if (h->variant == 6) {
+    if constexpr (HD == 16 || HD == 32) {
+      with_124(h->hg, [&](auto hgc) {
+        constexpr int HG = decltype(hgc)::value;
+        auto fq = agpt_blk::bwd_q_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+        set_lds(fq, h->bq_lds);
+        hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds)), dim3(agpt_blk::kThreads), h->bq_lds,
+                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
+                           static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
+        pm.mark(1);
+        auto fk = agpt_blk::bwd_kv_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+        set_lds(fk, h->kv_lds);
+        hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds)), dim3(agpt_blk::kThreads), h->kv_lds,
+                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv,
+                           h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+      });
+    }
+  } else if (h->variant == 5) {
     if constexpr (HD >= 16 && HD <= 32) {
       with_124(h->hg, [&](auto hgc) {
         constexpr int HG = decltype(hgc)::value;

@@ -1,0 +1,723 @@
+// trie_block.h — block-sparse trie-attention kernels on 16x16 fp32 matrix
+// instructions (included by trie_attn.hip after trie_fast.h).
+//
+// Same persistent streaming scheme as trie_fast.h: a workgroup (256 threads,
+// 4 waves) owns one head group of HG heads and a contiguous range of kTile-row
+// tiles, keeps the tile context in LDS and prefetches the next tile into
+// registers while the current one computes. What differs is the unit of
+// work. The tile's attention pattern is a mask over (tile row, key-set slot):
+// in DFS preorder the rows that see a key form one interval,
+//   prefix key (ancestor of the tile's first row s): rows [0, end - s),
+//   tile row c:                                      rows [c, end(c) - s),
+// so a 16-row query block and a 16-slot key block either share no pair or
+// are handled as one dense 16x16 block with a per-pair interval mask. On the
+// C2 corpus a 64-row tile touches ~12.7 such block pairs per head (36% of
+// their pairs are live), against ~5x more LDS traffic and instructions per
+// live pair for the 4x4 chain-group walk of trie_fast.h.
+//
+// LDS key set: slots [P - A, P) hold the A prefix rows right-aligned (entry d
+// = depth d+1 at slot P - A + d), slots P.. the tile rows; P = max_depth - 1
+// rounded up to 16, so key blocks (16 slots) never straddle the prefix/row
+// boundary. Slots below P - A are dead (empty interval). Moving to the next
+// tile copies each prefix row LDS to LDS, from the current prefix (same
+// depth) or from a current tile row; only the first tile of a range (or a
+// prefix too long to copy) loads its prefix from memory.
+//
+// Matrix instruction v_mfma_f32_16x16x4f32: D[16][16] += A[16][4] B[4][16]
+// with lane l = 16g + c supplying A[c][g] and B[g][c] and holding D[4g+r][c]
+// in register r. The contraction index is permuted freely: step j pairs
+// lane group g with dim KD*g + j (KD = HD/4), so every lane reads one
+// contiguous KD-slice of a row; for the second product the 4x4 register
+// block of D is reused directly as B (key 4g + j at step j).
+//
+//  query side (forward, dQ): unit = (head, query block i). S^T = K_blk Q_i^T
+//    puts query c in lane column c with keys 4g..4g+3 in its registers; the
+//    softmax max is reduced over the four lane groups (permlane swaps), and
+//    P^T feeds O^T += V^T P^T directly (O^T: dims 4g+r of query c).
+//  key side (dK, dV): unit = (head, key block). S = Q_i K_blk^T puts key c in
+//    lane column c with queries 4g..4g+3 in registers; P and dS feed
+//    dV^T += dO^T P and dK^T += Q^T dS directly.
+//
+// Units are dealt to the waves in snake order (wave w takes units w, 7-w,
+// 8+w, 15-w, ...) after ordering them longest first, which balances the
+// waves of a tile without a sort.
+#pragma once
+
+namespace agpt_blk {
+
+using namespace agpt;
+using agpt_fast::assign_range;
+using agpt_fast::f4;
+using agpt_fast::lds_stride;
+using agpt_fast::u4;
+using agpt_fast::uniform;
+
+constexpr int kTile = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kBlk = 16;               // rows per query block, slots per key block
+constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (log2 units)
+constexpr int kCopyPer = 2;            // prefix-copy jobs per thread (else reload)
+constexpr int kMaxSlots = kMaxDepth + kTile;
+constexpr int kLse = 1, kDl = 2;       // stream table flags
+
+// Prefix capacity P: max_depth - 1 rounded up to whole key blocks.
+__host__ __device__ constexpr int prefix_cap(int max_depth) {
+  return (max_depth - 1 + kBlk - 1) / kBlk * kBlk;
+}
+
+// Dynamic LDS: key set K, V [P + kTile][WS], ns staged tile tensors
+// [kTile][WS], and with pdl the δ partials [kTile][HG][HD/EPC] fp32.
+__host__ __device__ inline size_t block_lds_bytes(int max_depth, int HG, int HD, int elem, int ns, bool pdl) {
+  const int ws = HG * HD + 16 / elem;
+  size_t b = static_cast<size_t>(2 * (prefix_cap(max_depth) + kTile) + ns * kTile) * ws * elem;
+  b = (b + 15) & ~static_cast<size_t>(15);
+  if (pdl) b += static_cast<size_t>(kTile) * HG * (HD / (16 / elem)) * sizeof(float);
+  return b;
+}
+
+template <int HG>
+struct alignas(16) BlockTables {
+  alignas(16) int32_t kint[kMaxSlots];  // per key slot: lo | hi << 16, rows [lo, hi) see it
+  int32_t bhi[kMaxSlots / kBlk];    // per key block: max hi of its slots
+  int32_t depth[kTile];
+  int32_t tend[kTile];              // absolute subtree end of the tile rows
+  int32_t pend[kMaxDepth];          // absolute subtree end of prefix entry d
+  alignas(16) float l2[HG][kTile];  // lse * log2(e) of the tile rows (backward)
+  alignas(16) float dl[HG][kTile];  // δ of the tile rows (backward)
+};
+
+__device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Reductions over the four lane groups g (lanes c, c+16, c+32, c+48): each
+// swap leaves a lane's own value and its partner's (lane ^ 16, lane ^ 32)
+// in the two results.
+__device__ __forceinline__ float group_max(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(x);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group_sum(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned v = __float_as_uint(x);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ bool in_interval(int q, int iv) {
+  const int lo = iv & 0xffff, hi = iv >> 16;
+  return static_cast<unsigned>(q - lo) < static_cast<unsigned>(hi - lo);
+}
+
+__device__ __forceinline__ float ld1(const float* p) { return *p; }
+__device__ __forceinline__ float ld1(const bf16_t* p) { return to_f32(*p); }
+
+// k-th unit of wave w in snake order.
+__device__ __forceinline__ int snake_unit(int k, int w) { return kWaves * k + ((k & 1) ? kWaves - 1 - w : w); }
+
+// ---------------------------------------------------------------------------
+// Tile context stream. NT = tile-row tensors fetched: 1 = Q (forward);
+// 2 = Q, dO; 3 = Q, dO, O (O is reduced to δ partials, not staged).
+// kTabs: kLse / kDl tables of the tile rows.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, int HG, int NT, int kTabs, typename PlanT>
+struct BStream {
+  static constexpr int W = HG * HD;
+  static constexpr int WS = lds_stride<Tin>(W);
+  static constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));  // elements per 16-B chunk
+  static constexpr int CPR = W / EPC;                              // chunks per row slice
+  static constexpr int CPH = HD / EPC;                             // chunks per head
+  static constexpr int ROWJ = kTile * CPR;                         // chunk jobs per row tensor
+  static constexpr int KV_PER = (2 * ROWJ + kThreads - 1) / kThreads;
+  static constexpr int T_PER = (ROWJ + kThreads - 1) / kThreads;
+  static constexpr int NS = NT < 2 ? NT : 2;  // staged tile tensors
+  static constexpr int PJ = 2 * CPR;          // copy jobs per prefix entry (K and V)
+
+  const PlanT pl;
+  const Tin* K;
+  const Tin* V;
+  const Tin* TT[NT];
+  const float* lse;
+  const float* Dl;
+  int D, H, hg, P;
+  Tin* Ks;
+  Tin* Vs;
+  Tin* Ts;     // [NS][kTile][WS]
+  float* pdl;  // [kTile][HG][CPH] δ partials (NT == 3)
+  BlockTables<HG>& tb;
+  // current tile
+  int s, ntile, A, poff;
+  // next tile (prefetched)
+  int n_s, n_ntile, n_A, n_poff;
+  u4 kv[KV_PER];
+  u4 tt[NT][T_PER];
+  int dep, tend_r;
+  float lse_r, dl_r;
+  int cp_id[kCopyPer];
+
+  __device__ __forceinline__ BStream(const PlanT& pl_, const Tin* K_, const Tin* V_, const Tin* T0,
+                                     const Tin* T1, const Tin* T2, const float* lse_, const float* Dl_,
+                                     int H_, int hg_, unsigned char* dyn, BlockTables<HG>& tb_)
+      : pl(pl_), K(K_), V(V_), lse(lse_), Dl(Dl_), H(H_), hg(hg_), tb(tb_) {
+    TT[0] = T0;
+    if constexpr (NT > 1) TT[1] = T1;
+    if constexpr (NT > 2) TT[2] = T2;
+    D = H * HD;
+    P = prefix_cap(pl.max_depth);
+    Ks = reinterpret_cast<Tin*>(dyn);
+    Vs = Ks + (P + kTile) * WS;
+    Ts = Vs + (P + kTile) * WS;
+    pdl = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(Ts + NS * kTile * WS) + 15) &
+                                   ~static_cast<uintptr_t>(15));
+    s = 0;
+    A = 0;
+    // Every staged value stays finite: a matrix step multiplies dead slots
+    // and rows past the tile by zero weights, and 0 * NaN would leak.
+    const int n16 = static_cast<int>(block_lds_bytes(pl.max_depth, HG, HD, sizeof(Tin), NS, NT == 3) / 16);
+    u4* z = reinterpret_cast<u4*>(dyn);
+    for (int j = threadIdx.x; j < n16; j += kThreads) z[j] = u4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
+
+  __device__ __forceinline__ const Tin* gsrc(const Tin* base, int64_t row, int c) const {
+    return base + row * D + hg * W + c * EPC;
+  }
+
+  // Issues the loads of tile nt into registers (consumed by commit()).
+  __device__ __forceinline__ void prefetch(int nt) {
+    const int tid = threadIdx.x;
+    n_s = nt * kTile;
+    n_ntile = min(kTile, static_cast<int>(pl.T - n_s));
+    n_poff = pl.pref_off[nt];
+    n_A = pl.pref_off[nt + 1] - n_poff;
+    // Unconditional loads from in-range addresses (indices past the tile are
+    // clamped; commit() ignores those values).
+    const int last = n_ntile - 1;
+#pragma unroll
+    for (int k = 0; k < KV_PER; ++k) {
+      const int j = min(tid + k * kThreads, 2 * ROWJ - 1);
+      const int ten = j / ROWJ;
+      const int r = min((j - ten * ROWJ) / CPR, last);
+      kv[k] = *reinterpret_cast<const u4*>(gsrc(ten ? V : K, n_s + r, j % CPR));
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+      for (int k = 0; k < T_PER; ++k) {
+        const int j = min(tid + k * kThreads, ROWJ - 1);
+        const int r = min(j / CPR, last);
+        tt[i][k] = *reinterpret_cast<const u4*>(gsrc(TT[i], n_s + r, j % CPR));
+      }
+    const int lane = tid & 63;
+    dep = pl.depth[n_s + min(lane, last)];
+    tend_r = pl.end[n_s + min(lane, last)];
+    if constexpr (kTabs != 0) {
+      const int i = min(tid, n_ntile * HG - 1);
+      const int r = i / HG;
+      const int64_t o = (static_cast<int64_t>(n_s) + r) * H + hg * HG + (i - r * HG);
+      if constexpr ((kTabs & kLse) != 0) lse_r = lse[o];
+      if constexpr ((kTabs & kDl) != 0) dl_r = Dl[o];
+    }
+#pragma unroll
+    for (int k = 0; k < kCopyPer; ++k) {
+      const int d = (tid + k * kThreads) / PJ;
+      cp_id[k] = pl.prefix[n_poff + min(d, max(n_A - 1, 0))];
+      if (d >= n_A) cp_id[k] = -1;
+    }
+  }
+
+  // Interval entry of prefix entry d of the next tile (subtree end e).
+  __device__ __forceinline__ void set_prefix_entry(int d, int e) {
+    const int slot = P - n_A + d;
+    const int hi = min(e - n_s, n_ntile);
+    tb.pend[d] = e;
+    tb.kint[slot] = hi << 16;
+    if ((slot & (kBlk - 1)) == 0 || d == 0) tb.bhi[slot / kBlk] = hi;
+  }
+
+  // Installs the prefetched tile in LDS. cold: the prefix rows are loaded
+  // from memory (first tile of a range, or a prefix too long to copy).
+  __device__ __forceinline__ void commit(bool cold) {
+    const int tid = threadIdx.x;
+    cold = cold || n_A * PJ > kCopyPer * kThreads;
+    u4 cpv[kCopyPer];
+    int cpe[kCopyPer];
+#pragma unroll
+    for (int k = 0; k < kCopyPer; ++k) {
+      // Source of prefix entry d of the next tile: a current tile row (id >=
+      // s) or the current prefix entry of the same depth.
+      const int j = tid + k * kThreads;
+      const int d = j / PJ;
+      const int rem = j % PJ;
+      const int id = cp_id[k];
+      int src = P, e = 0;  // cold or no entry: a dummy read
+      if (!cold && id >= s) {
+        src = P + (id - s);
+        e = tb.tend[id - s];
+      } else if (!cold && id >= 0) {  // an ancestor of s: d < A
+        src = P - A + d;
+        e = tb.pend[d];
+      }
+      cpv[k] = *reinterpret_cast<const u4*>((rem < CPR ? Ks : Vs) + src * WS + (rem % CPR) * EPC);
+      cpe[k] = e;
+    }
+    __syncthreads();  // the current tile's context is no longer read
+#pragma unroll
+    for (int k = 0; k < KV_PER; ++k) {
+      const int j = tid + k * kThreads;
+      const int ten = j / ROWJ;
+      const int r = (j - ten * ROWJ) / CPR;
+      const int c = j % CPR;
+      if (j < 2 * ROWJ && r < n_ntile)
+        *reinterpret_cast<u4*>((ten ? Vs : Ks) + (P + r) * WS + c * EPC) = kv[k];
+    }
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int k = 0; k < T_PER; ++k) {
+        const int j = tid + k * kThreads;
+        const int r = j / CPR;
+        if (j < ROWJ && r < n_ntile)
+          *reinterpret_cast<u4*>(Ts + (i * kTile + r) * WS + (j % CPR) * EPC) = tt[i][k];
+      }
+    if constexpr (NT == 3) {  // δ partials: dO·O over each 16-byte chunk
+#pragma unroll
+      for (int k = 0; k < T_PER; ++k) {
+        const int j = tid + k * kThreads;
+        const int r = j / CPR;
+        if (j < ROWJ && r < n_ntile) {
+          const float* g = reinterpret_cast<const float*>(&tt[1][k]);
+          const float* o = reinterpret_cast<const float*>(&tt[2][k]);
+          pdl[r * (HG * CPH) + j % CPR] = (g[0] * o[0] + g[1] * o[1]) + (g[2] * o[2] + g[3] * o[3]);
+        }
+      }
+    }
+    if (!cold) {
+#pragma unroll
+      for (int k = 0; k < kCopyPer; ++k) {
+        const int j = tid + k * kThreads;
+        const int d = j / PJ;
+        const int rem = j % PJ;
+        if (d < n_A) {
+          const int dst = P - n_A + d;
+          const bool moved = cp_id[k] >= s || A != n_A;  // else it is already in place
+          if (moved) *reinterpret_cast<u4*>((rem < CPR ? Ks : Vs) + dst * WS + (rem % CPR) * EPC) = cpv[k];
+          if (rem == 0) set_prefix_entry(d, cpe[k]);
+        }
+      }
+    } else {
+      for (int j = tid; j < n_A * PJ; j += kThreads) {
+        const int d = j / PJ;
+        const int rem = j % PJ;
+        const int id = pl.prefix[n_poff + d];
+        *reinterpret_cast<u4*>((rem < CPR ? Ks : Vs) + (P - n_A + d) * WS + (rem % CPR) * EPC) =
+            *reinterpret_cast<const u4*>(gsrc(rem < CPR ? K : V, id, rem % CPR));
+        if (rem == 0) set_prefix_entry(d, pl.end[id]);
+      }
+    }
+    // Dead slots of the first prefix block, and the tile rows.
+    const int dead0 = (P - n_A) & ~(kBlk - 1);
+    if (tid < kBlk && dead0 + tid < P - n_A) tb.kint[dead0 + tid] = 0;
+    if (tid < kTile) {
+      const int r = tid;
+      const bool live = r < n_ntile;
+      const int hi = live ? min(tend_r - n_s, n_ntile) : r;
+      tb.kint[P + r] = r | (hi << 16);
+      tb.depth[r] = dep;
+      tb.tend[r] = tend_r;
+      // Row block maxima over the 16 lanes of each block (wave 0).
+      int m = live ? hi : 0;
+#pragma unroll
+      for (int sh = 1; sh < kBlk; sh <<= 1) m = max(m, __shfl_xor(m, sh, kBlk));
+      if ((r & (kBlk - 1)) == 0) tb.bhi[(P + r) / kBlk] = m;
+    }
+    if constexpr (kTabs != 0) {
+      if (tid < n_ntile * HG) {
+        const int r = tid / HG;
+        if constexpr ((kTabs & kLse) != 0) tb.l2[tid - r * HG][r] = lse_r * kLog2e;
+        if constexpr ((kTabs & kDl) != 0) tb.dl[tid - r * HG][r] = dl_r;
+      }
+    }
+    s = n_s;
+    ntile = n_ntile;
+    A = n_A;
+    poff = n_poff;
+    __syncthreads();
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Forward: O and lse.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, int HG, typename PlanT>
+__global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __restrict__ Q,
+                                                       const Tin* __restrict__ K,
+                                                       const Tin* __restrict__ V,
+                                                       Tin* __restrict__ O,
+                                                       float* __restrict__ lse, int H, float scale) {
+  constexpr int KD = HD / 4;   // contraction dims per lane group
+  constexpr int MT = HD / 16;  // 16-dim output tiles
+  using ST = BStream<HD, Tin, HG, 1, 0, PlanT>;
+  constexpr int WS = ST::WS;
+  __shared__ BlockTables<HG> tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  int hg, t0, t1;
+  assign_range(pl.n_tiles, H / HG, hg, t0, t1);
+  if (t0 >= t1) return;
+  ST st(pl, K, V, Q, nullptr, nullptr, nullptr, nullptr, H, hg, dyn, tb);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int P = st.P;
+  st.prefetch(t0);
+  st.commit(true);
+  for (int t = t0; t < t1; ++t) {
+    if (t + 1 < t1) st.prefetch(t + 1);
+    const int nqb = (st.ntile + kBlk - 1) / kBlk;
+    const int pb0 = (P - st.A) / kBlk;  // first key block with prefix slots
+    for (int k = 0;; ++k) {
+      const int u = snake_unit(k, wave);
+      if (u >= nqb * HG) break;
+      const int i = nqb - 1 - u / HG;  // query block, longest first
+      const int hh = u % HG;
+      const int hoff = hh * HD;
+      const int q = kBlk * i + c;
+      float qf[KD];
+      load_vec<KD>(st.Ts + q * WS + hoff + KD * g, qf);
+#pragma unroll
+      for (int j = 0; j < KD; ++j) qf[j] *= qscale;
+      float m = -__builtin_inff(), l = 0.0f;
+      f4 o[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      const int b_end = P / kBlk + i;
+      for (int b = pb0; b <= b_end; ++b) {
+        if (kBlk * i >= uniform(tb.bhi[b])) continue;  // no live pair
+        const int k0 = kBlk * b;
+        float kf[KD];
+        load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
+        f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < KD; ++j) sv = mfma16(kf[j], qf[j], sv);  // sv[r]: key k0+4g+r, query q
+        const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
+        const int ivr[4] = {iv.x, iv.y, iv.z, iv.w};
+        float sc[4];
+        bool live[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          live[r] = in_interval(q, ivr[r]);
+          sc[r] = live[r] ? sv[r] : -__builtin_inff();
+        }
+        const float mx = group_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+        const bool resc = mx > m + kRescaleLog2;
+        if (__any(resc)) {
+          const float a = resc ? fast_exp2(m - mx) : 1.0f;
+          m = resc ? mx : m;
+          l *= a;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) o[j] *= a;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = live[r] ? fast_exp2(sc[r] - m) : 0.0f;
+          l += p[r];
+        }
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o[j] = mfma16(ld1(st.Vs + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), p[r], o[j]);
+      }
+      l = group_sum(l);
+      if (q < st.ntile) {
+        const float inv = 1.0f / l;
+        const int h = hg * HG + hh;
+        const int64_t row = static_cast<int64_t>(st.s) + q;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
+          store_vec<4>(O + row * D + h * HD + kBlk * j + 4 * g, v);
+        }
+        if (g == 0) lse[row * H + h] = (m + fast_log2(l)) * kLn2;
+      }
+    }
+    if (t + 1 < t1) st.commit(false);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, query side: δ and dQ (see trie_fast.h for δ: dO·O for fp32
+// inputs; recomputed over the path for bf16 inputs). δ is written to Dl.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_q_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
+    float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
+  constexpr int NT = kDeltaFromO ? 3 : 2;
+  using ST = BStream<HD, Tin, HG, NT, kLse, PlanT>;
+  constexpr int WS = ST::WS;
+  __shared__ BlockTables<HG> tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  int hg, t0, t1;
+  assign_range(pl.n_tiles, H / HG, hg, t0, t1);
+  if (t0 >= t1) return;
+  ST st(pl, K, V, Q, dO, O, lse, nullptr, H, hg, dyn, tb);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int P = st.P;
+  const Tin* Qs = st.Ts;
+  const Tin* Gs = st.Ts + kTile * WS;
+  st.prefetch(t0);
+  st.commit(true);
+  for (int t = t0; t < t1; ++t) {
+    if (t + 1 < t1) st.prefetch(t + 1);
+    const int nqb = (st.ntile + kBlk - 1) / kBlk;
+    const int pb0 = (P - st.A) / kBlk;
+    for (int k = 0;; ++k) {
+      const int u = snake_unit(k, wave);
+      if (u >= nqb * HG) break;
+      const int i = nqb - 1 - u / HG;
+      const int hh = u % HG;
+      const int hoff = hh * HD;
+      const int q = kBlk * i + c;
+      float qf[KD], gf[KD];
+      load_vec<KD>(Qs + q * WS + hoff + KD * g, qf);
+      load_vec<KD>(Gs + q * WS + hoff + KD * g, gf);
+#pragma unroll
+      for (int j = 0; j < KD; ++j) qf[j] *= qscale;
+      const float l2 = tb.l2[hh][q];
+      const int b_end = P / kBlk + i;
+      // Scores and dO·v of key block b: register r holds key 16b+4g+r
+      // against query q; live[r] marks the pairs of the mask.
+      auto block = [&](int b, f4& sv, f4& tv, bool (&live)[4]) {
+        const int k0 = kBlk * b;
+        float kf[KD], vf[KD];
+        load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
+        load_vec<KD>(st.Vs + (k0 + c) * WS + hoff + KD * g, vf);
+        sv = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        tv = sv;
+#pragma unroll
+        for (int j = 0; j < KD; ++j) {
+          sv = mfma16(kf[j], qf[j], sv);
+          tv = mfma16(vf[j], gf[j], tv);
+        }
+        const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
+        live[0] = in_interval(q, iv.x);
+        live[1] = in_interval(q, iv.y);
+        live[2] = in_interval(q, iv.z);
+        live[3] = in_interval(q, iv.w);
+      };
+      float dl;
+      if constexpr (kDeltaFromO) {
+        dl = 0.0f;
+        const float* pp = st.pdl + (q * HG + hh) * ST::CPH;
+#pragma unroll
+        for (int j = 0; j < ST::CPH; ++j) dl += pp[j];
+      } else {
+        float acc = 0.0f;
+        for (int b = pb0; b <= b_end; ++b) {
+          if (kBlk * i >= uniform(tb.bhi[b])) continue;
+          f4 sv, tv;
+          bool live[4];
+          block(b, sv, tv, live);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc += live[r] ? fast_exp2(sv[r] - l2) * tv[r] : 0.0f;
+        }
+        dl = group_sum(acc);
+      }
+      f4 dq[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int b = pb0; b <= b_end; ++b) {
+        if (kBlk * i >= uniform(tb.bhi[b])) continue;
+        f4 sv, tv;
+        bool live[4];
+        block(b, sv, tv, live);
+        float ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ds[r] = live[r] ? fast_exp2(sv[r] - l2) * (tv[r] - dl) * scale : 0.0f;
+        const int k0 = kBlk * b;
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            dq[j] = mfma16(ld1(st.Ks + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), ds[r], dq[j]);
+      }
+      if (q < st.ntile) {
+        const int h = hg * HG + hh;
+        const int64_t row = static_cast<int64_t>(st.s) + q;
+        const int pos = rope.cos_t ? rope_pos(tb.depth[q], rope.seq_len) : 0;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          float v[4] = {dq[j][0], dq[j][1], dq[j][2], dq[j][3]};
+          if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
+          store_vec<4>(dQ + row * D + h * HD + kBlk * j + 4 * g, v);
+        }
+        if (g == 0) Dl[row * H + h] = dl;
+      }
+    }
+    if (t + 1 < t1) st.commit(false);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, key side: dK / dV of the tile's key set. Prefix keys leave their
+// partial over this tile in Pk/Pv (row pref_off[t] + depth-1); tile rows
+// whose subtree ends inside the tile are finished here (seed, inverse RoPE);
+// open tile rows leave their partial in dK/dV for the reduction kernels.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
+    float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ Pk, float* __restrict__ Pv,
+    const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeT rope, int H,
+    float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  using ST = BStream<HD, Tin, HG, 2, kLse | kDl, PlanT>;
+  constexpr int WS = ST::WS;
+  __shared__ BlockTables<HG> tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  int hg, t0, t1;
+  assign_range(pl.n_tiles, H / HG, hg, t0, t1);
+  if (t0 >= t1) return;
+  ST st(pl, K, V, Q, dO, nullptr, lse, Dl, H, hg, dyn, tb);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int P = st.P;
+  const Tin* Qs = st.Ts;
+  const Tin* Gs = st.Ts + kTile * WS;
+  st.prefetch(t0);
+  st.commit(true);
+  for (int t = t0; t < t1; ++t) {
+    if (t + 1 < t1) st.prefetch(t + 1);
+    const int nrb = (st.ntile + kBlk - 1) / kBlk;
+    const int pb0 = (P - st.A) / kBlk;
+    const int rb0 = P / kBlk;
+    const int nkb = rb0 - pb0 + nrb;  // prefix blocks (shallowest first), then row blocks
+    for (int k = 0;; ++k) {
+      const int u = snake_unit(k, wave);
+      if (u >= nkb * HG) break;
+      const int b = pb0 + u / HG;
+      const int hh = u % HG;
+      const int hoff = hh * HD;
+      const int kslot = kBlk * b + c;  // this lane's key
+      float kf[KD], vf[KD];
+      load_vec<KD>(st.Ks + kslot * WS + hoff + KD * g, kf);
+      load_vec<KD>(st.Vs + kslot * WS + hoff + KD * g, vf);
+#pragma unroll
+      for (int j = 0; j < KD; ++j) kf[j] *= qscale;
+      const int iv = tb.kint[kslot];
+      const int i0 = b < rb0 ? 0 : b - rb0;
+      const int i1 = uniform((tb.bhi[b] + kBlk - 1) / kBlk);
+      const float* l2h = tb.l2[hh];
+      const float* dlh = tb.dl[hh];
+      f4 dk[MT], dv[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        dv[j] = dk[j];
+      }
+      for (int i = i0; i < i1; ++i) {
+        const int qr = kBlk * i + c;  // query row this lane supplies
+        float qa[KD], ga[KD];
+        load_vec<KD>(Qs + qr * WS + hoff + KD * g, qa);
+        load_vec<KD>(Gs + qr * WS + hoff + KD * g, ga);
+        f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f}, tv = sv;
+#pragma unroll
+        for (int j = 0; j < KD; ++j) {
+          sv = mfma16(qa[j], kf[j], sv);  // sv[r]: query 16i+4g+r against key kslot
+          tv = mfma16(ga[j], vf[j], tv);
+        }
+        const int q0 = kBlk * i + 4 * g;
+        const f4 l2v = *reinterpret_cast<const f4*>(l2h + q0);
+        const f4 dlv = *reinterpret_cast<const f4*>(dlh + q0);
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool live = in_interval(q0 + r, iv);
+          p[r] = live ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
+          ds[r] = live ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = (q0 + r) * WS + hoff + kBlk * j + c;
+            dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
+            dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+          }
+      }
+      // Emit dims 16j+4g.. of key kslot.
+      const int hd = hg * HG + hh;
+      if (kslot < P) {
+        const int d = kslot - (P - st.A);
+        if (d >= 0) {
+          const int64_t row = static_cast<int64_t>(st.poff) + d;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+            float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+            store_vec<4>(Pk + row * D + hd * HD + kBlk * j + 4 * g, a);
+            store_vec<4>(Pv + row * D + hd * HD + kBlk * j + 4 * g, v);
+          }
+        }
+      } else {
+        const int r = kslot - P;
+        if (r < st.ntile) {
+          const int64_t a = static_cast<int64_t>(st.s) + r;
+          const bool done = tb.tend[r] <= st.s + st.ntile;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const int d0 = kBlk * j + 4 * g;
+            float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+            float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+            if (done) {
+              if (acc_dk) {
+                float y[4];
+                load_vec<4>(acc_dk + a * D + hd * HD + d0, y);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) gk[e] += y[e];
+              }
+              if (acc_dv) {
+                float y[4];
+                load_vec<4>(acc_dv + a * D + hd * HD + d0, y);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) gv[e] += y[e];
+              }
+              if (rope.cos_t)
+                agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t,
+                                                    rope_pos(tb.depth[r], rope.seq_len), d0);
+            }
+            store_vec<4>(dK + a * D + hd * HD + d0, gk);
+            store_vec<4>(dV + a * D + hd * HD + d0, gv);
+          }
+        }
+      }
+    }
+    if (t + 1 < t1) st.commit(false);
+  }
+}
+
+}  // namespace agpt_blk

@@ -19,10 +19,13 @@ pytestmark = pytest.mark.gpu
 # every parity test below runs against each of them.
 VARIANTS = {
     "default": {},
-    "fast_hg1_nw1_qb1_kb1": {"AGPT_ATTN_HG": "1", "AGPT_ATTN_NW": "1", "AGPT_ATTN_QB": "1",
-                             "AGPT_ATTN_KB": "1"},
-    "fast_hg4_nw4_t128_qb2_kb4": {"AGPT_ATTN_HG": "4", "AGPT_ATTN_NW": "4", "AGPT_ATTN_TILE": "128",
-                                  "AGPT_ATTN_QB": "2", "AGPT_ATTN_KB": "4"},
+    "block_hg1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "1"},
+    "block_hg4": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4"},
+    "chain": {"AGPT_ATTN_VARIANT": "5"},
+    "chain_hg1_qb1_kb1": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "1", "AGPT_ATTN_QB": "1",
+                          "AGPT_ATTN_KB": "1"},
+    "chain_hg4_qb2_kb4_uncut": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "4", "AGPT_ATTN_QB": "2",
+                                "AGPT_ATTN_KB": "4", "AGPT_ATTN_SPLIT": "0"},
     "global_walk": {"AGPT_ATTN_VARIANT": "0"},
     "global_walk_t256": {"AGPT_ATTN_VARIANT": "0", "AGPT_ATTN_TILE": "256"},
 }
@@ -31,7 +34,8 @@ VARIANTS = {
 @pytest.fixture(params=list(VARIANTS), autouse=True)
 def variant(request, monkeypatch):
     for k in ("AGPT_ATTN_VARIANT", "AGPT_ATTN_HG", "AGPT_ATTN_TILE", "AGPT_ATTN_NW",
-              "AGPT_ATTN_QB", "AGPT_ATTN_KB"):
+              "AGPT_ATTN_QB", "AGPT_ATTN_KB", "AGPT_ATTN_SPLIT", "AGPT_ATTN_QSLOTS",
+              "AGPT_ATTN_KSLOTS"):
         monkeypatch.delenv(k, raising=False)
     for k, v in VARIANTS[request.param].items():
         monkeypatch.setenv(k, v)
@@ -121,9 +125,12 @@ def test_parity_c1_sample(gpu):
     _check(tr.parent, 4, 16, seed=1, rope=True)
 
 
-@pytest.mark.parametrize("kind", ["single", "roots", "chain256", "tile_edge", "tile_edge1"])
-def test_edge_shapes(gpu, kind):
-    if kind == "single":
+@pytest.mark.parametrize("hd", [8, 16])
+@pytest.mark.parametrize("kind", ["single", "roots", "chain256", "tile_edge", "tile_edge1", "deep48"])
+def test_edge_shapes(gpu, kind, hd):
+    if kind == "deep48":  # prefixes longer than the 32-entry in-LDS copy budget
+        parent = small_trie(n_tokens=300, depth=48, seed=9).parent
+    elif kind == "single":
         parent = np.array([-1], np.int32)
     elif kind == "roots":
         parent = np.full(130, -1, np.int32)
@@ -133,7 +140,7 @@ def test_edge_shapes(gpu, kind):
         parent = np.concatenate([np.arange(-1, 63), np.arange(63, 127)]).astype(np.int32)
     else:  # a chain of 65: the tile boundary cuts the deepest row
         parent = np.arange(-1, 64, dtype=np.int32)
-    _check(parent, 2, 8, seed=len(parent), rope=True, acc=True)
+    _check(parent, 2, hd, seed=len(parent), rope=True, acc=True)
 
 
 def test_deterministic(gpu):
