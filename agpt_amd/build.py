@@ -32,6 +32,9 @@ HIP_FLAGS = [
     # Matrix-instruction accumulators in ordinary VGPRs: the kernels rescale
     # and read them between steps, which the AGPR form turns into copies.
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # No kernel result depends on NaN handling; without IEEE mode the float
+    # max/min of the softmax need no NaN-quieting instructions.
+    "-fno-honor-nans", "-Xarch_device", "-mno-amdgpu-ieee",
     "-Wall",
     "-Wno-unused-result",
 ]

@@ -59,6 +59,8 @@ int set_error(int code, const char* fmt, ...) {
       return set_error(AGPT_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(_e));   \
   } while (0)
 
+constexpr size_t kSchedBytes = 3 * kMaxHeads * sizeof(int32_t);
+
 struct PlanDev {
   const int32_t* parent;
   const int32_t* depth;
@@ -74,6 +76,11 @@ struct PlanDev {
   const int32_t* q_item_off;  // [n_tiles + 1]
   const int32_t* k_items;     // key-set chain groups, by query-range length
   const int32_t* k_item_off;  // [n_tiles + 1]
+  // Block kernels: tile chunks claimed from counters [kernel][head group]
+  // (zeroed before each launch).
+  int32_t* sched;
+  int32_t chunk_tiles;
+  int32_t n_chunks;
 };
 
 // ---------------------------------------------------------------------------
@@ -525,6 +532,8 @@ struct agpt_attn_s {
   float* d_Ck = nullptr;
   float* d_Cv = nullptr;
   float* d_Dl = nullptr;
+  int32_t* d_sched = nullptr;  // [3][kMaxHeads] chunk counters of the block kernels
+  int32_t chunk_tiles = 1, n_chunks_sched = 1;
   int32_t* d_q_items = nullptr;
   int32_t* d_k_items = nullptr;
   int32_t* d_q_item_off = nullptr;
@@ -534,6 +543,7 @@ struct agpt_attn_s {
   // 16x16 matrix tiles (trie_block.h)
   int variant = 0;
   int hg = 1, nw = 2, qb = 1, kb = 1;
+  bool unit_all_heads = false;  // block kernels: a unit takes every head of the group
   bool split = true;  // cut long work items into parts (see agpt_fast::kCutSteps)
   int q_slots = 0, k_slots = 0;  // scratch slots of cut query / key items per tile
   size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0;
@@ -557,7 +567,7 @@ void free_plan(agpt_attn_s* h) {
       (void)hipFree(*p);
       *p = nullptr;
     }
-  int32_t** op[] = {&h->d_q_items, &h->d_k_items};
+  int32_t** op[] = {&h->d_q_items, &h->d_k_items, &h->d_sched};
   for (auto p : op)
     if (*p) {
       (void)hipFree(*p);
@@ -583,6 +593,9 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.q_item_off = h->d_q_item_off;
   p.k_items = h->d_k_items;
   p.k_item_off = h->d_k_item_off;
+  p.sched = h->d_sched;
+  p.chunk_tiles = h->chunk_tiles;
+  p.n_chunks = h->n_chunks_sched;
   return p;
 }
 
@@ -733,6 +746,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
       while (hg * 2 <= 4 && H % (hg * 2) == 0 && hg * 2 * hd * elem <= 128) hg *= 2;
     }
     h->hg = hg;
+    h->unit_all_heads = env_int("AGPT_ATTN_UH", 1) != 1;
     tile = agpt_blk::kTile;
     h->fwd_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 1, false);
     h->bq_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4);
@@ -922,6 +936,11 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
   if (h->variant == 5 || h->variant == 6)
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
+  if (h->variant == 6) {
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_sched), kSchedBytes));
+    h->chunk_tiles = std::max(2, env_int("AGPT_ATTN_CHUNK", 24));
+    h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
+  }
   h->planned = true;
   g_last_error.clear();
   return AGPT_OK;
@@ -969,8 +988,9 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (h->variant == 6)
     snprintf(buf, sizeof(buf),
              "streaming block-sparse 16x16 mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
-             "fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
-             h->tile, h->n_tiles, h->hg, h->fwd_lds, h->bq_lds, h->kv_lds, h->max_lds);
+             "heads_per_unit=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
+             h->tile, h->n_tiles, h->hg, h->unit_all_heads ? h->hg : 1, h->fwd_lds, h->bq_lds, h->kv_lds,
+             h->max_lds);
   else if (h->variant == 5)
     snprintf(buf, sizeof(buf),
              "streaming chain-grouped mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
@@ -1069,15 +1089,26 @@ void with_124(int v, Fn&& fn) {  // v in {1, 2, 4}
   else fn(std::integral_constant<int, 1>{});
 }
 
+// Block kernels: heads per workgroup (1, 2, 4) and heads per unit (all or one).
+template <typename Fn>
+void with_block_heads(const agpt_attn_s* h, Fn&& fn) {
+  with_124(h->hg, [&](auto hgc) {
+    constexpr int HG = decltype(hgc)::value;
+    if (h->unit_all_heads) fn(hgc, std::integral_constant<int, HG>{});
+    else fn(hgc, std::integral_constant<int, 1>{});
+  });
+}
+
 template <int HD, typename Tin>
 void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, void* o,
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
   if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32) {
-      with_124(h->hg, [&](auto hgc) {
-        constexpr int HG = decltype(hgc)::value;
-        auto fn = agpt_blk::fwd_kernel<HD, Tin, HG, PlanDev>;
+      (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
+      with_block_heads(h, [&](auto hgc, auto uhc) {
+        constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
+        auto fn = agpt_blk::fwd_kernel<HD, Tin, HG, UH, PlanDev>;
         set_lds(fn, h->fwd_lds);
         hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds)), dim3(agpt_blk::kThreads), h->fwd_lds,
                            st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
@@ -1114,16 +1145,17 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   pm.mark(0);
   if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32) {
-      with_124(h->hg, [&](auto hgc) {
-        constexpr int HG = decltype(hgc)::value;
-        auto fq = agpt_blk::bwd_q_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+      (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
+      with_block_heads(h, [&](auto hgc, auto uhc) {
+        constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
+        auto fq = agpt_blk::bwd_q_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
         set_lds(fq, h->bq_lds);
         hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds)), dim3(agpt_blk::kThreads), h->bq_lds,
                            st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
                            static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
                            static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
         pm.mark(1);
-        auto fk = agpt_blk::bwd_kv_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+        auto fk = agpt_blk::bwd_kv_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
         set_lds(fk, h->kv_lds);
         hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds)), dim3(agpt_blk::kThreads), h->kv_lds,
                            st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),

@@ -46,7 +46,6 @@
 namespace agpt_blk {
 
 using namespace agpt;
-using agpt_fast::assign_range;
 using agpt_fast::f4;
 using agpt_fast::lds_stride;
 using agpt_fast::u4;
@@ -78,13 +77,14 @@ __host__ __device__ inline size_t block_lds_bytes(int max_depth, int HG, int HD,
 
 template <int HG>
 struct alignas(16) BlockTables {
-  alignas(16) int32_t kint[kMaxSlots];  // per key slot: lo | hi << 16, rows [lo, hi) see it
+  alignas(16) int32_t kint[kMaxSlots];  // per key slot: lo | (hi - lo) << 16, rows [lo, hi) see it
   int32_t bhi[kMaxSlots / kBlk];    // per key block: max hi of its slots
   int32_t depth[kTile];
   int32_t tend[kTile];              // absolute subtree end of the tile rows
   int32_t pend[kMaxDepth];          // absolute subtree end of prefix entry d
   alignas(16) float l2[HG][kTile];  // lse * log2(e) of the tile rows (backward)
   alignas(16) float dl[HG][kTile];  // δ of the tile rows (backward)
+  int32_t grab;                     // last chunk claimed by the workgroup
 };
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
@@ -112,8 +112,7 @@ __device__ __forceinline__ float group_sum(float x) {
 }
 
 __device__ __forceinline__ bool in_interval(int q, int iv) {
-  const int lo = iv & 0xffff, hi = iv >> 16;
-  return static_cast<unsigned>(q - lo) < static_cast<unsigned>(hi - lo);
+  return static_cast<unsigned>(q - (iv & 0xffff)) < static_cast<unsigned>(iv >> 16);
 }
 
 __device__ __forceinline__ float ld1(const float* p) { return *p; }
@@ -174,8 +173,10 @@ struct BStream {
     Ks = reinterpret_cast<Tin*>(dyn);
     Vs = Ks + (P + kTile) * WS;
     Ts = Vs + (P + kTile) * WS;
-    pdl = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(Ts + NS * kTile * WS) + 15) &
-                                   ~static_cast<uintptr_t>(15));
+    // Offsets from the LDS base (integer casts of the pointer would lose its
+    // address space and turn the accesses into flat ones).
+    const int tbytes = (2 * (P + kTile) + NS * kTile) * WS * static_cast<int>(sizeof(Tin));
+    pdl = reinterpret_cast<float*>(dyn + ((tbytes + 15) & ~15));
     s = 0;
     A = 0;
     // Every staged value stays finite: a matrix step multiplies dead slots
@@ -228,8 +229,9 @@ struct BStream {
 #pragma unroll
     for (int k = 0; k < kCopyPer; ++k) {
       const int d = (tid + k * kThreads) / PJ;
-      cp_id[k] = pl.prefix[n_poff + min(d, max(n_A - 1, 0))];
-      if (d >= n_A) cp_id[k] = -1;
+      // Entries past the prefix load a valid one; commit() ignores them (no
+      // value is used here, so the loads stay in flight until commit()).
+      cp_id[k] = pl.prefix[n_A > 0 ? n_poff + min(d, n_A - 1) : max(n_poff - 1, 0)];
     }
   }
 
@@ -243,8 +245,10 @@ struct BStream {
   }
 
   // Installs the prefetched tile in LDS. cold: the prefix rows are loaded
-  // from memory (first tile of a range, or a prefix too long to copy).
-  __device__ __forceinline__ void commit(bool cold) {
+  // from memory (first tile of a chunk, or a prefix too long to copy).
+  // publish: thread 0 stores `grab` in tb.grab for every thread to read
+  // after the call.
+  __device__ __forceinline__ void commit(bool cold, bool publish = false, int grab = 0) {
     const int tid = threadIdx.x;
     cold = cold || n_A * PJ > kCopyPer * kThreads;
     u4 cpv[kCopyPer];
@@ -256,7 +260,7 @@ struct BStream {
       const int j = tid + k * kThreads;
       const int d = j / PJ;
       const int rem = j % PJ;
-      const int id = cp_id[k];
+      const int id = d < n_A ? cp_id[k] : -1;
       int src = P, e = 0;  // cold or no entry: a dummy read
       if (!cold && id >= s) {
         src = P + (id - s);
@@ -269,6 +273,7 @@ struct BStream {
       cpe[k] = e;
     }
     __syncthreads();  // the current tile's context is no longer read
+    if (publish && tid == 0) tb.grab = grab;
 #pragma unroll
     for (int k = 0; k < KV_PER; ++k) {
       const int j = tid + k * kThreads;
@@ -329,7 +334,7 @@ struct BStream {
       const int r = tid;
       const bool live = r < n_ntile;
       const int hi = live ? min(tend_r - n_s, n_ntile) : r;
-      tb.kint[P + r] = r | (hi << 16);
+      tb.kint[P + r] = r | ((hi - r) << 16);
       tb.depth[r] = dep;
       tb.tend[r] = tend_r;
       // Row block maxima over the 16 lanes of each block (wave 0).
@@ -354,9 +359,70 @@ struct BStream {
 };
 
 // ---------------------------------------------------------------------------
-// Forward: O and lse.
+// Dynamic tile chunks. The workgroups of a head group claim chunks of
+// consecutive tiles from that group's counter (chunk c = tiles [cK, (c+1)K),
+// the last chunk running to the end, so every chunk but a lone one has at
+// least two tiles). A workgroup claims its next chunk while it computes the
+// first tile of the current one, so the claim is known before the last
+// tile's prefetch; within a chunk the prefix moves LDS to LDS, the first
+// tile of a chunk loads it from memory. Results do not depend on which
+// workgroup takes a tile.
 // ---------------------------------------------------------------------------
-template <int HD, typename Tin, int HG, typename PlanT>
+template <typename PlanT>
+struct ChunkLoop {
+  int* ctr;
+  int nch, K, ntiles;
+  int t, tend, nxt, nxt_c, nt, gr;
+  bool first;
+
+  __device__ __forceinline__ ChunkLoop(const PlanT& pl, int* ctr_, int c)
+      : ctr(ctr_), nch(pl.n_chunks), K(pl.chunk_tiles), ntiles(pl.n_tiles) {
+    t = c < nch ? c * K : ntiles;
+    tend = c < nch ? cend(c) : ntiles;
+    nxt = -1;
+    nxt_c = nch;
+    first = true;
+  }
+  __device__ __forceinline__ int cend(int c) const { return c == nch - 1 ? ntiles : (c + 1) * K; }
+
+  // Prefetches the next tile (if known) and claims the next chunk on the
+  // first tile of a chunk.
+  template <typename ST>
+  __device__ __forceinline__ void begin_tile(ST& st) {
+    nt = t + 1 < tend ? t + 1 : nxt;
+    if (nt >= 0) st.prefetch(nt);
+    gr = 0;
+    if (first && nch > 1 && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
+  }
+  // Installs the next tile; false when the workgroup is done.
+  template <typename ST>
+  __device__ __forceinline__ bool end_tile(ST& st) {
+    if (nt < 0) return false;
+    const bool cold = t + 1 >= tend;
+    const bool pub = first && nch > 1;
+    st.commit(cold, pub, gr);
+    if (pub) {
+      nxt_c = uniform(st.tb.grab);
+      nxt = nxt_c < nch ? nxt_c * K : -1;
+    }
+    if (cold) {
+      tend = cend(nxt_c);
+      nxt = -1;
+      first = true;
+    } else {
+      first = false;
+    }
+    t = nt;
+    return true;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Forward: O and lse. A unit is a query block with UH heads of the group
+// (the mask and the loop are shared by the heads; each head is its own
+// chain of matrix steps).
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, int HG, int UH, typename PlanT>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __restrict__ Q,
                                                        const Tin* __restrict__ K,
                                                        const Tin* __restrict__ V,
@@ -364,118 +430,134 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
                                                        float* __restrict__ lse, int H, float scale) {
   constexpr int KD = HD / 4;   // contraction dims per lane group
   constexpr int MT = HD / 16;  // 16-dim output tiles
+  constexpr int NUH = HG / UH;
   using ST = BStream<HD, Tin, HG, 1, 0, PlanT>;
   constexpr int WS = ST::WS;
   __shared__ BlockTables<HG> tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  int hg, t0, t1;
-  assign_range(pl.n_tiles, H / HG, hg, t0, t1);
-  if (t0 >= t1) return;
+  const int hg = blockIdx.x % (H / HG);
+  int* ctr = pl.sched + 0 * kMaxHeads + hg;
+  if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
   ST st(pl, K, V, Q, nullptr, nullptr, nullptr, nullptr, H, hg, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
   const int P = st.P;
-  st.prefetch(t0);
+  st.prefetch(cl.t);
   st.commit(true);
-  for (int t = t0; t < t1; ++t) {
-    if (t + 1 < t1) st.prefetch(t + 1);
+  do {
+    cl.begin_tile(st);
     const int nqb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;  // first key block with prefix slots
+    const int rb0 = P / kBlk;
     for (int k = 0;; ++k) {
       const int u = snake_unit(k, wave);
-      if (u >= nqb * HG) break;
-      const int i = nqb - 1 - u / HG;  // query block, longest first
-      const int hh = u % HG;
-      const int hoff = hh * HD;
+      if (u >= nqb * NUH) break;
+      const int i = nqb - 1 - u / NUH;  // query block, longest first
+      const int h0 = (u % NUH) * UH;    // first head of the unit (in the group)
       const int q = kBlk * i + c;
-      float qf[KD];
-      load_vec<KD>(st.Ts + q * WS + hoff + KD * g, qf);
+      float qf[UH][KD], m[UH], l[UH];
+      f4 o[UH][MT];
 #pragma unroll
-      for (int j = 0; j < KD; ++j) qf[j] *= qscale;
-      float m = -__builtin_inff(), l = 0.0f;
-      f4 o[MT];
+      for (int e = 0; e < UH; ++e) {
+        load_vec<KD>(st.Ts + q * WS + (h0 + e) * HD + KD * g, qf[e]);
 #pragma unroll
-      for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-      const int b_end = P / kBlk + i;
-      for (int b = pb0; b <= b_end; ++b) {
+        for (int j = 0; j < KD; ++j) qf[e][j] *= qscale;
+        m[e] = -__builtin_inff();
+        l[e] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) o[e][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      // The diagonal block first (it holds every row's own key), then the
+      // prefix blocks and the row blocks above the diagonal.
+      for (int n = 0, b = rb0 + i; n <= i + rb0 - pb0; ++n, b = pb0 + n - 1) {
         if (kBlk * i >= uniform(tb.bhi[b])) continue;  // no live pair
         const int k0 = kBlk * b;
-        float kf[KD];
-        load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
-        f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < KD; ++j) sv = mfma16(kf[j], qf[j], sv);  // sv[r]: key k0+4g+r, query q
         const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
-        const int ivr[4] = {iv.x, iv.y, iv.z, iv.w};
-        float sc[4];
-        bool live[4];
+        const bool live[4] = {in_interval(q, iv.x), in_interval(q, iv.y), in_interval(q, iv.z),
+                              in_interval(q, iv.w)};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          live[r] = in_interval(q, ivr[r]);
-          sc[r] = live[r] ? sv[r] : -__builtin_inff();
+        for (int e = 0; e < UH; ++e) {
+          const int hoff = (h0 + e) * HD;
+          float kf[KD];
+          load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
+          f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int j = 0; j < KD; ++j) sv = mfma16(kf[j], qf[e][j], sv);  // key k0+4g+r, query q
+          float sc[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[r] = live[r] ? sv[r] : -__builtin_inff();
+          const float mx = group_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+          const bool resc = mx > m[e] + kRescaleLog2;
+          if (__any(resc)) {
+            const float a = resc ? fast_exp2(m[e] - mx) : 1.0f;
+            m[e] = resc ? mx : m[e];
+            l[e] *= a;
+#pragma unroll
+            for (int j = 0; j < MT; ++j) o[e][j] *= a;
+          }
+          float p[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[r] = fast_exp2(sc[r] - m[e]);  // masked: exp2(-inf) = 0
+            l[e] += p[r];
+          }
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              o[e][j] = mfma16(ld1(st.Vs + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), p[r], o[e][j]);
         }
-        const float mx = group_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-        const bool resc = mx > m + kRescaleLog2;
-        if (__any(resc)) {
-          const float a = resc ? fast_exp2(m - mx) : 1.0f;
-          m = resc ? mx : m;
-          l *= a;
-#pragma unroll
-          for (int j = 0; j < MT; ++j) o[j] *= a;
-        }
-        float p[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[r] = live[r] ? fast_exp2(sc[r] - m) : 0.0f;
-          l += p[r];
-        }
-#pragma unroll
-        for (int j = 0; j < MT; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            o[j] = mfma16(ld1(st.Vs + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), p[r], o[j]);
       }
-      l = group_sum(l);
       if (q < st.ntile) {
-        const float inv = 1.0f / l;
-        const int h = hg * HG + hh;
         const int64_t row = static_cast<int64_t>(st.s) + q;
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
-          store_vec<4>(O + row * D + h * HD + kBlk * j + 4 * g, v);
+        for (int e = 0; e < UH; ++e) {
+          const float le = group_sum(l[e]);
+          const float inv = __builtin_amdgcn_rcpf(le);
+          const int h = hg * HG + h0 + e;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            float v[4] = {o[e][j][0] * inv, o[e][j][1] * inv, o[e][j][2] * inv, o[e][j][3] * inv};
+            store_vec<4>(O + row * D + h * HD + kBlk * j + 4 * g, v);
+          }
+          if (g == 0) lse[row * H + h] = (m[e] + fast_log2(le)) * kLn2;
         }
-        if (g == 0) lse[row * H + h] = (m + fast_log2(l)) * kLn2;
       }
     }
-    if (t + 1 < t1) st.commit(false);
-  }
+  } while (cl.end_tile(st));
 }
 
 // ---------------------------------------------------------------------------
-// Backward, query side: δ and dQ (see trie_fast.h for δ: dO·O for fp32
-// inputs; recomputed over the path for bf16 inputs). δ is written to Dl.
+// Backward, query side: δ and dQ. δ = dO·O for fp32 inputs (from the chunk
+// partials); for bf16 inputs O is a rounded output, so δ = Σ_j w_j dO·v_j is
+// recomputed over the path in fp32 (batched_depth_backward.cr:637-646). δ is
+// written to Dl [T, H] for the key side.
 // ---------------------------------------------------------------------------
-template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
+template <int HD, typename Tin, int HG, int UH, typename PlanT, typename RopeT>
 __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
     float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
+  constexpr int NUH = HG / UH;
   constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
   constexpr int NT = kDeltaFromO ? 3 : 2;
   using ST = BStream<HD, Tin, HG, NT, kLse, PlanT>;
   constexpr int WS = ST::WS;
   __shared__ BlockTables<HG> tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  int hg, t0, t1;
-  assign_range(pl.n_tiles, H / HG, hg, t0, t1);
-  if (t0 >= t1) return;
+  const int hg = blockIdx.x % (H / HG);
+  int* ctr = pl.sched + 1 * kMaxHeads + hg;
+  if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
   ST st(pl, K, V, Q, dO, O, lse, nullptr, H, hg, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -484,30 +566,35 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   const int P = st.P;
   const Tin* Qs = st.Ts;
   const Tin* Gs = st.Ts + kTile * WS;
-  st.prefetch(t0);
+  st.prefetch(cl.t);
   st.commit(true);
-  for (int t = t0; t < t1; ++t) {
-    if (t + 1 < t1) st.prefetch(t + 1);
+  do {
+    cl.begin_tile(st);
     const int nqb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;
+    const int rb0 = P / kBlk;
     for (int k = 0;; ++k) {
       const int u = snake_unit(k, wave);
-      if (u >= nqb * HG) break;
-      const int i = nqb - 1 - u / HG;
-      const int hh = u % HG;
-      const int hoff = hh * HD;
+      if (u >= nqb * NUH) break;
+      const int i = nqb - 1 - u / NUH;
+      const int h0 = (u % NUH) * UH;
       const int q = kBlk * i + c;
-      float qf[KD], gf[KD];
-      load_vec<KD>(Qs + q * WS + hoff + KD * g, qf);
-      load_vec<KD>(Gs + q * WS + hoff + KD * g, gf);
+      float qf[UH][KD], gf[UH][KD], l2[UH], dl[UH];
+      f4 dq[UH][MT];
 #pragma unroll
-      for (int j = 0; j < KD; ++j) qf[j] *= qscale;
-      const float l2 = tb.l2[hh][q];
-      const int b_end = P / kBlk + i;
-      // Scores and dO·v of key block b: register r holds key 16b+4g+r
-      // against query q; live[r] marks the pairs of the mask.
-      auto block = [&](int b, f4& sv, f4& tv, bool (&live)[4]) {
-        const int k0 = kBlk * b;
+      for (int e = 0; e < UH; ++e) {
+        load_vec<KD>(Qs + q * WS + (h0 + e) * HD + KD * g, qf[e]);
+        load_vec<KD>(Gs + q * WS + (h0 + e) * HD + KD * g, gf[e]);
+#pragma unroll
+        for (int j = 0; j < KD; ++j) qf[e][j] *= qscale;
+        l2[e] = tb.l2[h0 + e][q];
+#pragma unroll
+        for (int j = 0; j < MT; ++j) dq[e][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      // Scores and dO·v of head e against key block k0: register r holds key
+      // k0+4g+r against query q.
+      auto scores = [&](int e, int k0, f4& sv, f4& tv) {
+        const int hoff = (h0 + e) * HD;
         float kf[KD], vf[KD];
         load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
         load_vec<KD>(st.Vs + (k0 + c) * WS + hoff + KD * g, vf);
@@ -515,75 +602,93 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         tv = sv;
 #pragma unroll
         for (int j = 0; j < KD; ++j) {
-          sv = mfma16(kf[j], qf[j], sv);
-          tv = mfma16(vf[j], gf[j], tv);
+          sv = mfma16(kf[j], qf[e][j], sv);
+          tv = mfma16(vf[j], gf[e][j], tv);
         }
+      };
+      auto mask = [&](int k0, bool (&live)[4]) {
         const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
         live[0] = in_interval(q, iv.x);
         live[1] = in_interval(q, iv.y);
         live[2] = in_interval(q, iv.z);
         live[3] = in_interval(q, iv.w);
       };
-      float dl;
+      const int nblk = i + rb0 - pb0;  // blocks after the diagonal one
       if constexpr (kDeltaFromO) {
-        dl = 0.0f;
-        const float* pp = st.pdl + (q * HG + hh) * ST::CPH;
 #pragma unroll
-        for (int j = 0; j < ST::CPH; ++j) dl += pp[j];
-      } else {
-        float acc = 0.0f;
-        for (int b = pb0; b <= b_end; ++b) {
-          if (kBlk * i >= uniform(tb.bhi[b])) continue;
-          f4 sv, tv;
-          bool live[4];
-          block(b, sv, tv, live);
+        for (int e = 0; e < UH; ++e) {
+          dl[e] = 0.0f;
+          const float* pp = st.pdl + (q * HG + h0 + e) * ST::CPH;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc += live[r] ? fast_exp2(sv[r] - l2) * tv[r] : 0.0f;
+          for (int j = 0; j < ST::CPH; ++j) dl[e] += pp[j];
         }
-        dl = group_sum(acc);
+      } else {
+        float acc[UH];
+#pragma unroll
+        for (int e = 0; e < UH; ++e) acc[e] = 0.0f;
+        for (int n = 0, b = rb0 + i; n <= nblk; ++n, b = pb0 + n - 1) {
+          if (kBlk * i >= uniform(tb.bhi[b])) continue;
+          bool live[4];
+          mask(kBlk * b, live);
+#pragma unroll
+          for (int e = 0; e < UH; ++e) {
+            f4 sv, tv;
+            scores(e, kBlk * b, sv, tv);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[e] += live[r] ? fast_exp2(sv[r] - l2[e]) * tv[r] : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < UH; ++e) dl[e] = group_sum(acc[e]);
       }
-      f4 dq[MT];
-#pragma unroll
-      for (int j = 0; j < MT; ++j) dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-      for (int b = pb0; b <= b_end; ++b) {
+      for (int n = 0, b = rb0 + i; n <= nblk; ++n, b = pb0 + n - 1) {
         if (kBlk * i >= uniform(tb.bhi[b])) continue;
-        f4 sv, tv;
-        bool live[4];
-        block(b, sv, tv, live);
-        float ds[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ds[r] = live[r] ? fast_exp2(sv[r] - l2) * (tv[r] - dl) * scale : 0.0f;
         const int k0 = kBlk * b;
+        bool live[4];
+        mask(k0, live);
 #pragma unroll
-        for (int j = 0; j < MT; ++j)
+        for (int e = 0; e < UH; ++e) {
+          f4 sv, tv;
+          scores(e, k0, sv, tv);
+          float ds[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            dq[j] = mfma16(ld1(st.Ks + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), ds[r], dq[j]);
+            ds[r] = live[r] ? fast_exp2(sv[r] - l2[e]) * (tv[r] - dl[e]) * scale : 0.0f;
+          const int hoff = (h0 + e) * HD;
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              dq[e][j] = mfma16(ld1(st.Ks + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), ds[r], dq[e][j]);
+        }
       }
       if (q < st.ntile) {
-        const int h = hg * HG + hh;
         const int64_t row = static_cast<int64_t>(st.s) + q;
         const int pos = rope.cos_t ? rope_pos(tb.depth[q], rope.seq_len) : 0;
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          float v[4] = {dq[j][0], dq[j][1], dq[j][2], dq[j][3]};
-          if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
-          store_vec<4>(dQ + row * D + h * HD + kBlk * j + 4 * g, v);
+        for (int e = 0; e < UH; ++e) {
+          const int h = hg * HG + h0 + e;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            float v[4] = {dq[e][j][0], dq[e][j][1], dq[e][j][2], dq[e][j][3]};
+            if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
+            store_vec<4>(dQ + row * D + h * HD + kBlk * j + 4 * g, v);
+          }
+          if (g == 0) Dl[row * H + h] = dl[e];
         }
-        if (g == 0) Dl[row * H + h] = dl;
       }
     }
-    if (t + 1 < t1) st.commit(false);
-  }
+  } while (cl.end_tile(st));
 }
 
 // ---------------------------------------------------------------------------
-// Backward, key side: dK / dV of the tile's key set. Prefix keys leave their
-// partial over this tile in Pk/Pv (row pref_off[t] + depth-1); tile rows
-// whose subtree ends inside the tile are finished here (seed, inverse RoPE);
-// open tile rows leave their partial in dK/dV for the reduction kernels.
+// Backward, key side: dK / dV of the tile's key set, a unit being a key
+// block with UH heads. Prefix keys leave their partial over this tile in
+// Pk/Pv (row pref_off[t] + depth-1); tile rows whose subtree ends inside the
+// tile are finished here (seed, inverse RoPE); open tile rows leave their
+// partial in dK/dV for the reduction kernels.
 // ---------------------------------------------------------------------------
-template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
+template <int HD, typename Tin, int HG, int UH, typename PlanT, typename RopeT>
 __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
@@ -592,14 +697,17 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
     float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
+  constexpr int NUH = HG / UH;
   using ST = BStream<HD, Tin, HG, 2, kLse | kDl, PlanT>;
   constexpr int WS = ST::WS;
   __shared__ BlockTables<HG> tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  int hg, t0, t1;
-  assign_range(pl.n_tiles, H / HG, hg, t0, t1);
-  if (t0 >= t1) return;
+  const int hg = blockIdx.x % (H / HG);
+  int* ctr = pl.sched + 2 * kMaxHeads + hg;
+  if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
   ST st(pl, K, V, Q, dO, nullptr, lse, Dl, H, hg, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -608,79 +716,88 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   const int P = st.P;
   const Tin* Qs = st.Ts;
   const Tin* Gs = st.Ts + kTile * WS;
-  st.prefetch(t0);
+  st.prefetch(cl.t);
   st.commit(true);
-  for (int t = t0; t < t1; ++t) {
-    if (t + 1 < t1) st.prefetch(t + 1);
+  do {
+    cl.begin_tile(st);
     const int nrb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;
     const int rb0 = P / kBlk;
     const int nkb = rb0 - pb0 + nrb;  // prefix blocks (shallowest first), then row blocks
     for (int k = 0;; ++k) {
       const int u = snake_unit(k, wave);
-      if (u >= nkb * HG) break;
-      const int b = pb0 + u / HG;
-      const int hh = u % HG;
-      const int hoff = hh * HD;
+      if (u >= nkb * NUH) break;
+      const int b = pb0 + u / NUH;
+      const int h0 = (u % NUH) * UH;
       const int kslot = kBlk * b + c;  // this lane's key
-      float kf[KD], vf[KD];
-      load_vec<KD>(st.Ks + kslot * WS + hoff + KD * g, kf);
-      load_vec<KD>(st.Vs + kslot * WS + hoff + KD * g, vf);
+      float kf[UH][KD], vf[UH][KD];
+      f4 dk[UH][MT], dv[UH][MT];
 #pragma unroll
-      for (int j = 0; j < KD; ++j) kf[j] *= qscale;
+      for (int e = 0; e < UH; ++e) {
+        load_vec<KD>(st.Ks + kslot * WS + (h0 + e) * HD + KD * g, kf[e]);
+        load_vec<KD>(st.Vs + kslot * WS + (h0 + e) * HD + KD * g, vf[e]);
+#pragma unroll
+        for (int j = 0; j < KD; ++j) kf[e][j] *= qscale;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          dk[e][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+          dv[e][j] = dk[e][j];
+        }
+      }
       const int iv = tb.kint[kslot];
       const int i0 = b < rb0 ? 0 : b - rb0;
       const int i1 = uniform((tb.bhi[b] + kBlk - 1) / kBlk);
-      const float* l2h = tb.l2[hh];
-      const float* dlh = tb.dl[hh];
-      f4 dk[MT], dv[MT];
-#pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        dv[j] = dk[j];
-      }
       for (int i = i0; i < i1; ++i) {
         const int qr = kBlk * i + c;  // query row this lane supplies
-        float qa[KD], ga[KD];
-        load_vec<KD>(Qs + qr * WS + hoff + KD * g, qa);
-        load_vec<KD>(Gs + qr * WS + hoff + KD * g, ga);
-        f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f}, tv = sv;
-#pragma unroll
-        for (int j = 0; j < KD; ++j) {
-          sv = mfma16(qa[j], kf[j], sv);  // sv[r]: query 16i+4g+r against key kslot
-          tv = mfma16(ga[j], vf[j], tv);
-        }
         const int q0 = kBlk * i + 4 * g;
-        const f4 l2v = *reinterpret_cast<const f4*>(l2h + q0);
-        const f4 dlv = *reinterpret_cast<const f4*>(dlh + q0);
-        float p[4], ds[4];
+        bool live[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool live = in_interval(q0 + r, iv);
-          p[r] = live ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
-          ds[r] = live ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
-        }
+        for (int r = 0; r < 4; ++r) live[r] = in_interval(q0 + r, iv);
 #pragma unroll
-        for (int j = 0; j < MT; ++j)
+        for (int e = 0; e < UH; ++e) {
+          const int hoff = (h0 + e) * HD;
+          float qa[KD], ga[KD];
+          load_vec<KD>(Qs + qr * WS + hoff + KD * g, qa);
+          load_vec<KD>(Gs + qr * WS + hoff + KD * g, ga);
+          f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f}, tv = sv;
+#pragma unroll
+          for (int j = 0; j < KD; ++j) {
+            sv = mfma16(qa[j], kf[e][j], sv);  // sv[r]: query q0+r against key kslot
+            tv = mfma16(ga[j], vf[e][j], tv);
+          }
+          const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[h0 + e][q0]);
+          const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[h0 + e][q0]);
+          float p[4], ds[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int row = (q0 + r) * WS + hoff + kBlk * j + c;
-            dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
-            dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+            p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
+            ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
           }
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = (q0 + r) * WS + hoff + kBlk * j + c;
+              dv[e][j] = mfma16(ld1(Gs + row), p[r], dv[e][j]);
+              dk[e][j] = mfma16(ld1(Qs + row), ds[r], dk[e][j]);
+            }
+        }
       }
       // Emit dims 16j+4g.. of key kslot.
-      const int hd = hg * HG + hh;
       if (kslot < P) {
         const int d = kslot - (P - st.A);
         if (d >= 0) {
           const int64_t row = static_cast<int64_t>(st.poff) + d;
 #pragma unroll
-          for (int j = 0; j < MT; ++j) {
-            float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
-            float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
-            store_vec<4>(Pk + row * D + hd * HD + kBlk * j + 4 * g, a);
-            store_vec<4>(Pv + row * D + hd * HD + kBlk * j + 4 * g, v);
+          for (int e = 0; e < UH; ++e) {
+            const int hd = hg * HG + h0 + e;
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              float a[4] = {dk[e][j][0], dk[e][j][1], dk[e][j][2], dk[e][j][3]};
+              float v[4] = {dv[e][j][0], dv[e][j][1], dv[e][j][2], dv[e][j][3]};
+              store_vec<4>(Pk + row * D + hd * HD + kBlk * j + 4 * g, a);
+              store_vec<4>(Pv + row * D + hd * HD + kBlk * j + 4 * g, v);
+            }
           }
         }
       } else {
@@ -688,36 +805,38 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
         if (r < st.ntile) {
           const int64_t a = static_cast<int64_t>(st.s) + r;
           const bool done = tb.tend[r] <= st.s + st.ntile;
+          const int pos = rope.cos_t ? rope_pos(tb.depth[r], rope.seq_len) : 0;
 #pragma unroll
-          for (int j = 0; j < MT; ++j) {
-            const int d0 = kBlk * j + 4 * g;
-            float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
-            float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
-            if (done) {
-              if (acc_dk) {
-                float y[4];
-                load_vec<4>(acc_dk + a * D + hd * HD + d0, y);
+          for (int e = 0; e < UH; ++e) {
+            const int hd = hg * HG + h0 + e;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) gk[e] += y[e];
+            for (int j = 0; j < MT; ++j) {
+              const int d0 = kBlk * j + 4 * g;
+              float gk[4] = {dk[e][j][0], dk[e][j][1], dk[e][j][2], dk[e][j][3]};
+              float gv[4] = {dv[e][j][0], dv[e][j][1], dv[e][j][2], dv[e][j][3]};
+              if (done) {
+                if (acc_dk) {
+                  float y[4];
+                  load_vec<4>(acc_dk + a * D + hd * HD + d0, y);
+#pragma unroll
+                  for (int x = 0; x < 4; ++x) gk[x] += y[x];
+                }
+                if (acc_dv) {
+                  float y[4];
+                  load_vec<4>(acc_dv + a * D + hd * HD + d0, y);
+#pragma unroll
+                  for (int x = 0; x < 4; ++x) gv[x] += y[x];
+                }
+                if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
               }
-              if (acc_dv) {
-                float y[4];
-                load_vec<4>(acc_dv + a * D + hd * HD + d0, y);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) gv[e] += y[e];
-              }
-              if (rope.cos_t)
-                agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t,
-                                                    rope_pos(tb.depth[r], rope.seq_len), d0);
+              store_vec<4>(dK + a * D + hd * HD + d0, gk);
+              store_vec<4>(dV + a * D + hd * HD + d0, gv);
             }
-            store_vec<4>(dK + a * D + hd * HD + d0, gk);
-            store_vec<4>(dV + a * D + hd * HD + d0, gv);
           }
         }
       }
     }
-    if (t + 1 < t1) st.commit(false);
-  }
+  } while (cl.end_tile(st));
 }
 
 }  // namespace agpt_blk

@@ -313,8 +313,11 @@ struct Stream {
     Vs = Ks + (P + kTile) * WS;
     Ts = Vs + (P + kTile) * WS;
     anc = reinterpret_cast<int16_t*>(Ts + NS * kTile * WS);
-    pdl = reinterpret_cast<float*>(
-        (reinterpret_cast<uintptr_t>(anc + (kQ ? kTile * ldd : 0)) + 15) & ~static_cast<uintptr_t>(15));
+    // Offsets from the LDS base (integer casts of the pointer would lose its
+    // address space and turn the accesses into flat ones).
+    const int abytes = (2 * (P + kTile) + NS * kTile) * WS * static_cast<int>(sizeof(Tin)) +
+                       (kQ ? kTile * ldd * static_cast<int>(sizeof(int16_t)) : 0);
+    pdl = reinterpret_cast<float*>(dyn + ((abytes + 15) & ~15));
   }
 
   __host__ __device__ static size_t lds_bytes(int max_depth) {
@@ -378,8 +381,9 @@ struct Stream {
 #pragma unroll
     for (int k = 0; k < kCopyPer; ++k) {
       const int d = (tid + k * kThreads) / PJ;
-      cp_id[k] = pl.prefix[n_poff + min(d, max(n_A - 1, 0))];
-      if (d >= n_A) cp_id[k] = -1;
+      // Entries past the prefix load a valid one; commit() ignores them (no
+      // value is used here, so the loads stay in flight until commit()).
+      cp_id[k] = pl.prefix[n_A > 0 ? n_poff + min(d, n_A - 1) : max(n_poff - 1, 0)];
     }
   }
 
