@@ -81,6 +81,7 @@ struct PlanDev {
   int32_t* sched;
   int32_t chunk_tiles;
   int32_t n_chunks;
+  int32_t n_prefix;  // pref_off[n_tiles]
 };
 
 // ---------------------------------------------------------------------------
@@ -544,6 +545,9 @@ struct agpt_attn_s {
   int variant = 0;
   int hg = 1, nw = 2, qb = 1, kb = 1;
   bool unit_all_heads = false;  // block kernels: a unit takes every head of the group
+  bool fused = false;           // block kernels: one-pass backward (fp32)
+  int fhg = 1;                  // heads per workgroup of the one-pass backward
+  size_t fb_lds = 0;
   bool split = true;  // cut long work items into parts (see agpt_fast::kCutSteps)
   int q_slots = 0, k_slots = 0;  // scratch slots of cut query / key items per tile
   size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0;
@@ -596,6 +600,7 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.sched = h->d_sched;
   p.chunk_tiles = h->chunk_tiles;
   p.n_chunks = h->n_chunks_sched;
+  p.n_prefix = static_cast<int32_t>(h->n_prefix_rows);
   return p;
 }
 
@@ -751,10 +756,16 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     h->fwd_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 1, false);
     h->bq_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4);
     h->kv_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, false);
+    h->fhg = env_int("AGPT_ATTN_FHG", 1);
+    h->fused = elem == 4 && env_int("AGPT_ATTN_FUSED", 1) != 0 && H % h->fhg == 0 &&
+               (h->fhg == 1 || h->fhg == 2);
+    h->fb_lds = agpt_blk::block_lds_bytes(h->max_depth, h->fhg, hd, elem, 2, false) +
+                agpt_blk::fused_scratch_bytes(hd, h->fhg);
     const int bbudget = lim - static_cast<int>(sizeof(agpt_blk::BlockTables<4>));
     const bool ok = (hd == 16 || hd == 32) && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
                     (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(bbudget) &&
                     h->bq_lds <= static_cast<size_t>(bbudget) && h->kv_lds <= static_cast<size_t>(bbudget);
+    if (h->fused && h->fb_lds > static_cast<size_t>(bbudget)) h->fused = false;
     if (ok) return;
     h->variant = 5;  // try the chain-group walk
   }
@@ -987,10 +998,10 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   char buf[320];
   if (h->variant == 6)
     snprintf(buf, sizeof(buf),
-             "streaming block-sparse 16x16 mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
-             "heads_per_unit=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
-             h->tile, h->n_tiles, h->hg, h->unit_all_heads ? h->hg : 1, h->fwd_lds, h->bq_lds, h->kv_lds,
-             h->max_lds);
+             "streaming block-sparse 16x16 mfma, %s backward: tile_rows=%d tiles=%d heads_per_wg=%d "
+             "heads_per_unit=%d fwd_lds=%zu bwd_lds=%zu/%zu lds_limit=%d",
+             h->fused ? "one-pass" : "split", h->tile, h->n_tiles, h->hg, h->unit_all_heads ? h->hg : 1,
+             h->fwd_lds, h->fused ? h->fb_lds : h->bq_lds, h->fused ? 0 : h->kv_lds, h->max_lds);
   else if (h->variant == 5)
     snprintf(buf, sizeof(buf),
              "streaming chain-grouped mfma, split backward: tile_rows=%d tiles=%d heads_per_wg=%d "
@@ -1063,10 +1074,10 @@ int wg_per_cu(Fn fn, size_t lds, int lds_per_cu) {
 }
 
 template <typename Fn>
-int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds) {
+int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds, int hg = 0) {
   int per_cu = wg_per_cu(fn, lds, h->max_lds), cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
-  const int n_hg = h->cfg.n_heads / h->hg;
+  const int n_hg = h->cfg.n_heads / (hg > 0 ? hg : h->hg);
   const int m = std::lcm(agpt_fast::kXcds, n_hg);
   const int64_t units = static_cast<int64_t>(h->n_tiles) * n_hg;
   int64_t g = static_cast<int64_t>(std::max(per_cu, 1)) * cus;
@@ -1143,7 +1154,28 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                 hipStream_t st, const ProfMarks& pm) {
   const int D = h->cfg.n_heads * HD;
   pm.mark(0);
-  if (h->variant == 6) {
+  bool fused_done = false;
+  if constexpr ((HD == 16 || HD == 32) && std::is_same<Tin, float>::value) {
+    if (h->variant == 6 && h->fused) {
+      (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
+      with_124(h->fhg, [&](auto hgc) {
+        constexpr int HG = decltype(hgc)::value;
+        if constexpr (HG <= 2) {
+          auto fb = agpt_blk::bwd_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+          set_lds(fb, h->fb_lds);
+          hipLaunchKernelGGL(fb, dim3(stream_grid(h, fb, h->fb_lds, HG)), dim3(agpt_blk::kThreads), h->fb_lds,
+                             st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                             static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
+                             static_cast<const Tin*>(dO), dq, dk, dv, h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope,
+                             h->cfg.n_heads, scale);
+        }
+      });
+      pm.mark(1);
+      fused_done = true;
+    }
+  }
+  if (fused_done) {
+  } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32) {
       (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
       with_block_heads(h, [&](auto hgc, auto uhc) {

@@ -58,7 +58,9 @@ constexpr int kBlk = 16;               // rows per query block, slots per key bl
 constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (log2 units)
 constexpr int kCopyPer = 2;            // prefix-copy jobs per thread (else reload)
 constexpr int kMaxSlots = kMaxDepth + kTile;
-constexpr int kLse = 1, kDl = 2;       // stream table flags
+// Stream table flags: lse of the tile rows; δ of the tile rows read from Dl;
+// δ = dO·O computed from the fetched O (NT == 3) into the δ table.
+constexpr int kLse = 1, kDl = 2, kDeltaO = 4;
 
 // Prefix capacity P: max_depth - 1 rounded up to whole key blocks.
 __host__ __device__ constexpr int prefix_cap(int max_depth) {
@@ -75,16 +77,18 @@ __host__ __device__ inline size_t block_lds_bytes(int max_depth, int HG, int HD,
   return b;
 }
 
-template <int HG>
+// LDS tables of a tile. BT = rows of the lse / δ tables (kTile for the
+// backward, 0 for the forward: its workgroup then fits four to a CU).
+template <int HG, int BT = kTile>
 struct alignas(16) BlockTables {
   alignas(16) int32_t kint[kMaxSlots];  // per key slot: lo | (hi - lo) << 16, rows [lo, hi) see it
   int32_t bhi[kMaxSlots / kBlk];    // per key block: max hi of its slots
   int32_t depth[kTile];
   int32_t tend[kTile];              // absolute subtree end of the tile rows
   int32_t pend[kMaxDepth];          // absolute subtree end of prefix entry d
-  alignas(16) float l2[HG][kTile];  // lse * log2(e) of the tile rows (backward)
-  alignas(16) float dl[HG][kTile];  // δ of the tile rows (backward)
   int32_t grab;                     // last chunk claimed by the workgroup
+  alignas(16) float l2[HG][BT];     // lse * log2(e) of the tile rows (backward)
+  alignas(16) float dl[HG][BT];     // δ of the tile rows (backward)
 };
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
@@ -128,6 +132,9 @@ __device__ __forceinline__ int snake_unit(int k, int w) { return kWaves * k + ((
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, int HG, int NT, int kTabs, typename PlanT>
 struct BStream {
+  using Tables = BlockTables<HG, kTabs != 0 ? kTile : 0>;
+  // δ partials per 16-byte chunk in LDS (NT == 3 without kDeltaO).
+  static constexpr bool kPdl = NT == 3 && (kTabs & kDeltaO) == 0;
   static constexpr int W = HG * HD;
   static constexpr int WS = lds_stride<Tin>(W);
   static constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));  // elements per 16-B chunk
@@ -150,11 +157,12 @@ struct BStream {
   Tin* Vs;
   Tin* Ts;     // [NS][kTile][WS]
   float* pdl;  // [kTile][HG][CPH] δ partials (NT == 3)
-  BlockTables<HG>& tb;
+  Tables& tb;
   // current tile
   int s, ntile, A, poff;
   // next tile (prefetched)
   int n_s, n_ntile, n_A, n_poff;
+  int n_t = -2, n_pend;  // last prefetched tile, pref_off[n_t + 1] (loaded there)
   u4 kv[KV_PER];
   u4 tt[NT][T_PER];
   int dep, tend_r;
@@ -163,7 +171,7 @@ struct BStream {
 
   __device__ __forceinline__ BStream(const PlanT& pl_, const Tin* K_, const Tin* V_, const Tin* T0,
                                      const Tin* T1, const Tin* T2, const float* lse_, const float* Dl_,
-                                     int H_, int hg_, unsigned char* dyn, BlockTables<HG>& tb_)
+                                     int H_, int hg_, unsigned char* dyn, Tables& tb_)
       : pl(pl_), K(K_), V(V_), lse(lse_), Dl(Dl_), H(H_), hg(hg_), tb(tb_) {
     TT[0] = T0;
     if constexpr (NT > 1) TT[1] = T1;
@@ -181,10 +189,14 @@ struct BStream {
     A = 0;
     // Every staged value stays finite: a matrix step multiplies dead slots
     // and rows past the tile by zero weights, and 0 * NaN would leak.
-    const int n16 = static_cast<int>(block_lds_bytes(pl.max_depth, HG, HD, sizeof(Tin), NS, NT == 3) / 16);
+    const int n16 = static_cast<int>(lds_bytes(pl.max_depth) / 16);
     u4* z = reinterpret_cast<u4*>(dyn);
     for (int j = threadIdx.x; j < n16; j += kThreads) z[j] = u4{0u, 0u, 0u, 0u};
     __syncthreads();
+  }
+
+  __host__ __device__ static size_t lds_bytes(int max_depth) {
+    return block_lds_bytes(max_depth, HG, HD, sizeof(Tin), NS, kPdl);
   }
 
   __device__ __forceinline__ const Tin* gsrc(const Tin* base, int64_t row, int c) const {
@@ -196,8 +208,12 @@ struct BStream {
     const int tid = threadIdx.x;
     n_s = nt * kTile;
     n_ntile = min(kTile, static_cast<int>(pl.T - n_s));
-    n_poff = pl.pref_off[nt];
-    n_A = pl.pref_off[nt + 1] - n_poff;
+    // The prefix offset of tile nt is the end offset of tile nt - 1, already
+    // loaded when that tile was prefetched; only a jump (new chunk) waits on
+    // a load here. The end offset is first used by commit().
+    n_poff = nt == n_t + 1 ? n_pend : pl.pref_off[nt];
+    n_pend = pl.pref_off[nt + 1];
+    n_t = nt;
     // Unconditional loads from in-range addresses (indices past the tile are
     // clamped; commit() ignores those values).
     const int last = n_ntile - 1;
@@ -231,7 +247,7 @@ struct BStream {
       const int d = (tid + k * kThreads) / PJ;
       // Entries past the prefix load a valid one; commit() ignores them (no
       // value is used here, so the loads stay in flight until commit()).
-      cp_id[k] = pl.prefix[n_A > 0 ? n_poff + min(d, n_A - 1) : max(n_poff - 1, 0)];
+      cp_id[k] = pl.prefix[max(min(n_poff + d, pl.n_prefix - 1), 0)];
     }
   }
 
@@ -250,6 +266,7 @@ struct BStream {
   // after the call.
   __device__ __forceinline__ void commit(bool cold, bool publish = false, int grab = 0) {
     const int tid = threadIdx.x;
+    n_A = n_pend - n_poff;
     cold = cold || n_A * PJ > kCopyPer * kThreads;
     u4 cpv[kCopyPer];
     int cpe[kCopyPer];
@@ -292,15 +309,21 @@ struct BStream {
         if (j < ROWJ && r < n_ntile)
           *reinterpret_cast<u4*>(Ts + (i * kTile + r) * WS + (j % CPR) * EPC) = tt[i][k];
       }
-    if constexpr (NT == 3) {  // δ partials: dO·O over each 16-byte chunk
+    if constexpr (NT == 3) {  // δ = dO·O: per 16-byte chunk, then per head
 #pragma unroll
       for (int k = 0; k < T_PER; ++k) {
         const int j = tid + k * kThreads;
         const int r = j / CPR;
-        if (j < ROWJ && r < n_ntile) {
-          const float* g = reinterpret_cast<const float*>(&tt[1][k]);
-          const float* o = reinterpret_cast<const float*>(&tt[2][k]);
-          pdl[r * (HG * CPH) + j % CPR] = (g[0] * o[0] + g[1] * o[1]) + (g[2] * o[2] + g[3] * o[3]);
+        const float* g = reinterpret_cast<const float*>(&tt[1][k]);
+        const float* o = reinterpret_cast<const float*>(&tt[2][k]);
+        float v = (g[0] * o[0] + g[1] * o[1]) + (g[2] * o[2] + g[3] * o[3]);
+        if constexpr (kPdl) {
+          if (j < ROWJ && r < n_ntile) pdl[r * (HG * CPH) + j % CPR] = v;
+        } else {
+          // The CPH chunks of a head sit in CPH consecutive lanes.
+#pragma unroll
+          for (int m = 1; m < CPH; m <<= 1) v += __shfl_xor(v, m, CPH);
+          if (j < ROWJ && r < n_ntile && (j % CPH) == 0) tb.dl[(j % CPR) / CPH][r] = v;
         }
       }
     }
@@ -433,7 +456,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   constexpr int NUH = HG / UH;
   using ST = BStream<HD, Tin, HG, 1, 0, PlanT>;
   constexpr int WS = ST::WS;
-  __shared__ BlockTables<HG> tb;
+  __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
   const int hg = blockIdx.x % (H / HG);
   int* ctr = pl.sched + 0 * kMaxHeads + hg;
@@ -550,7 +573,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   constexpr int NT = kDeltaFromO ? 3 : 2;
   using ST = BStream<HD, Tin, HG, NT, kLse, PlanT>;
   constexpr int WS = ST::WS;
-  __shared__ BlockTables<HG> tb;
+  __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
   const int hg = blockIdx.x % (H / HG);
   int* ctr = pl.sched + 1 * kMaxHeads + hg;
@@ -700,7 +723,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   constexpr int NUH = HG / UH;
   using ST = BStream<HD, Tin, HG, 2, kLse | kDl, PlanT>;
   constexpr int WS = ST::WS;
-  __shared__ BlockTables<HG> tb;
+  __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
   const int hg = blockIdx.x % (H / HG);
   int* ctr = pl.sched + 2 * kMaxHeads + hg;
@@ -835,6 +858,218 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           }
         }
       }
+    }
+  } while (cl.end_tile(st));
+}
+
+// ---------------------------------------------------------------------------
+// Fused backward (fp32 inputs): dQ, dK, dV in one pass over the tiles. A
+// unit is a key block of one head (kv orientation: S = Q_i K^T puts key c in
+// lane column c). Per block pair (query block i, key block) the scores, P,
+// dP and dS are formed once and feed
+//   dV^T += dO^T P,   dK^T += Q^T dS    (registers of the unit, emitted at
+//                                        its end as in bwd_kv_kernel),
+//   dQ_i^T += K^T dS^T                   (dS transposed through a per-wave
+//                                        LDS tile; accumulated in the
+//                                        wave's own LDS dQ tile).
+// The units of a tile are dealt to the waves longest first, each to the
+// least loaded wave (every wave computes the same assignment). After the
+// units the workgroup sums the waves' dQ tiles in wave order, then applies
+// inverse RoPE: the order of every sum is fixed, so results are bitwise
+// reproducible. δ = dO·O comes with the tile (the stream reduces the
+// fetched O).
+// ---------------------------------------------------------------------------
+// LDS past the stream: dQ partials [wave][HG][kTile][HD] and dS^T tiles
+// [wave][16][20].
+__host__ __device__ constexpr size_t fused_scratch_bytes(int HD, int HG) {
+  return static_cast<size_t>(kWaves) * (HG * kTile * HD + kBlk * 20) * sizeof(float);
+}
+
+template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ Pk,
+    float* __restrict__ Pv, const float* __restrict__ acc_dk, const float* __restrict__ acc_dv,
+    RopeT rope, int H, float scale) {
+  static_assert(sizeof(Tin) == sizeof(float), "the fused backward takes fp32 inputs (δ = dO·O)");
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  using ST = BStream<HD, Tin, HG, 3, kLse | kDeltaO, PlanT>;
+  constexpr int WS = ST::WS;
+  __shared__ typename ST::Tables tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  const int hg = blockIdx.x % (H / HG);
+  int* ctr = pl.sched + 1 * kMaxHeads + hg;
+  if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
+  ST st(pl, K, V, Q, dO, O, lse, nullptr, H, hg, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  if (cl.t >= cl.ntiles) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int P = st.P;
+  const Tin* Qs = st.Ts;
+  const Tin* Gs = st.Ts + kTile * WS;
+  float* dqs = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));  // [wave][HG][kTile][HD]
+  float* tr = dqs + kWaves * HG * kTile * HD + wave * (kBlk * 20);         // this wave's dS^T tile
+  st.prefetch(cl.t);
+  st.commit(true);
+  do {
+    cl.begin_tile(st);
+    const int nrb = (st.ntile + kBlk - 1) / kBlk;
+    const int pb0 = (P - st.A) / kBlk;
+    const int rb0 = P / kBlk;
+    const int nu = (rb0 - pb0 + nrb) * HG;  // units: key blocks (prefix first) x heads
+    // This wave's dQ tile [HG][kTile][HD] starts at zero.
+    float* mydq = dqs + wave * HG * kTile * HD;
+    for (int x = lane; x < HG * kTile * HD / 4; x += 64)
+      reinterpret_cast<f4*>(mydq)[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    int load0 = 0, load1 = 0, load2 = 0, load3 = 0;
+    for (int u = 0; u < nu; ++u) {
+      const int b = pb0 + u / HG;
+      const int hh = u % HG;
+      const int i0 = b < rb0 ? 0 : b - rb0;
+      const int i1 = uniform((tb.bhi[b] + kBlk - 1) / kBlk);
+      // Least loaded wave (lowest index on ties) takes the unit.
+      int w = 0, lmin = load0;
+      if (load1 < lmin) { w = 1; lmin = load1; }
+      if (load2 < lmin) { w = 2; lmin = load2; }
+      if (load3 < lmin) { w = 3; lmin = load3; }
+      const int cost = i1 - i0;
+      if (w == 0) load0 += cost;
+      else if (w == 1) load1 += cost;
+      else if (w == 2) load2 += cost;
+      else load3 += cost;
+      if (w != wave) continue;
+      const int hoff = hh * HD;
+      const int kslot = kBlk * b + c;  // this lane's key
+      float kf[KD], vf[KD], kt[MT][4];
+      load_vec<KD>(st.Ks + kslot * WS + hoff + KD * g, kf);
+      load_vec<KD>(st.Vs + kslot * WS + hoff + KD * g, vf);
+#pragma unroll
+      for (int j = 0; j < KD; ++j) kf[j] *= qscale;
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) kt[t][r] = ld1(st.Ks + (kBlk * b + 4 * g + r) * WS + hoff + kBlk * t + c);
+      const int iv = tb.kint[kslot];
+      f4 dk[MT], dv[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        dv[j] = dk[j];
+      }
+      for (int i = i0; i < i1; ++i) {
+        const int qr = kBlk * i + c;  // query row this lane supplies
+        const int q0 = kBlk * i + 4 * g;
+        float qa[KD], ga[KD];
+        load_vec<KD>(Qs + qr * WS + hoff + KD * g, qa);
+        load_vec<KD>(Gs + qr * WS + hoff + KD * g, ga);
+        f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f}, tv = sv;
+#pragma unroll
+        for (int j = 0; j < KD; ++j) {
+          sv = mfma16(qa[j], kf[j], sv);  // sv[r]: query q0+r against key kslot
+          tv = mfma16(ga[j], vf[j], tv);
+        }
+        const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[hh][q0]);
+        const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[hh][q0]);
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool live = in_interval(q0 + r, iv);
+          p[r] = live ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
+          ds[r] = live ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+        }
+        // dS^T for the dQ product: write key c's four queries, read back
+        // query c's four keys (LDS operations of a wave complete in order).
+        *reinterpret_cast<f4*>(tr + c * 20 + 4 * g) = f4{ds[0], ds[1], ds[2], ds[3]};
+        float dst[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[r] = tr[(4 * g + r) * 20 + c];
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = (q0 + r) * WS + hoff + kBlk * j + c;
+            dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
+            dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+          }
+        // lane: dims 16j+4g.. of query row qr
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          f4* dqp = reinterpret_cast<f4*>(mydq + (hh * kTile + qr) * HD + kBlk * j + 4 * g);
+          f4 acc = *dqp;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc = mfma16(kt[j][r], dst[r], acc);
+          *dqp = acc;
+        }
+      }
+      // Emit dims 16j+4g.. of key kslot.
+      if (kslot < P) {
+        const int d = kslot - (P - st.A);
+        if (d >= 0) {
+          const int64_t row = static_cast<int64_t>(st.poff) + d;
+          const int hd = hg * HG + hh;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+            float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+            store_vec<4>(Pk + row * D + hd * HD + kBlk * j + 4 * g, a);
+            store_vec<4>(Pv + row * D + hd * HD + kBlk * j + 4 * g, v);
+          }
+        }
+      } else {
+        const int r = kslot - P;
+        if (r < st.ntile) {
+          const int64_t a = static_cast<int64_t>(st.s) + r;
+          const bool done = tb.tend[r] <= st.s + st.ntile;
+          const int pos = rope.cos_t ? rope_pos(tb.depth[r], rope.seq_len) : 0;
+          const int hd = hg * HG + hh;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const int d0 = kBlk * j + 4 * g;
+            float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+            float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+            if (done) {
+              if (acc_dk) {
+                float y[4];
+                load_vec<4>(acc_dk + a * D + hd * HD + d0, y);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) gk[x] += y[x];
+              }
+              if (acc_dv) {
+                float y[4];
+                load_vec<4>(acc_dv + a * D + hd * HD + d0, y);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) gv[x] += y[x];
+              }
+              if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
+            }
+            store_vec<4>(dK + a * D + hd * HD + d0, gk);
+            store_vec<4>(dV + a * D + hd * HD + d0, gv);
+          }
+        }
+      }
+    }
+    // dQ: the sum of the waves' tiles in wave order.
+    __syncthreads();
+    constexpr int kQuads = HG * kTile * HD / 4;  // 4 consecutive dims of a row of a head
+    for (int x = threadIdx.x; x < kQuads; x += kThreads) {
+      const int e = x / (kTile * HD / 4);
+      const int rem = x - e * (kTile * HD / 4);
+      const int q = rem / (HD / 4);
+      const int d0 = (rem - q * (HD / 4)) * 4;
+      if (q >= st.ntile) continue;
+      f4 sum = *reinterpret_cast<const f4*>(dqs + (e * kTile + q) * HD + d0);
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) sum += *reinterpret_cast<const f4*>(dqs + ((w * HG + e) * kTile + q) * HD + d0);
+      float v[4] = {sum[0], sum[1], sum[2], sum[3]};
+      if (rope.cos_t)
+        agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, rope_pos(tb.depth[q], rope.seq_len), d0);
+      store_vec<4>(dQ + (static_cast<int64_t>(st.s) + q) * D + (hg * HG + e) * HD + d0, v);
     }
   } while (cl.end_tile(st));
 }

@@ -19,7 +19,8 @@ pytestmark = pytest.mark.gpu
 # every parity test below runs against each of them.
 VARIANTS = {
     "default": {},
-    "block_hg1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "1"},
+    "block_hg1_fused_hg2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "1", "AGPT_ATTN_FHG": "2"},
+    "block_split": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUSED": "0"},
     "block_hg4_all_heads_chunk2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4", "AGPT_ATTN_UH": "4",
                                    "AGPT_ATTN_CHUNK": "2"},
     "chain": {"AGPT_ATTN_VARIANT": "5"},
@@ -36,7 +37,8 @@ VARIANTS = {
 def variant(request, monkeypatch):
     for k in ("AGPT_ATTN_VARIANT", "AGPT_ATTN_HG", "AGPT_ATTN_TILE", "AGPT_ATTN_NW",
               "AGPT_ATTN_QB", "AGPT_ATTN_KB", "AGPT_ATTN_SPLIT", "AGPT_ATTN_QSLOTS",
-              "AGPT_ATTN_KSLOTS", "AGPT_ATTN_UH", "AGPT_ATTN_CHUNK"):
+              "AGPT_ATTN_KSLOTS", "AGPT_ATTN_UH", "AGPT_ATTN_CHUNK", "AGPT_ATTN_FUSED",
+              "AGPT_ATTN_FHG"):
         monkeypatch.delenv(k, raising=False)
     for k, v in VARIANTS[request.param].items():
         monkeypatch.setenv(k, v)
