@@ -162,7 +162,7 @@ struct BStream {
   int s, ntile, A, poff;
   // next tile (prefetched)
   int n_s, n_ntile, n_A, n_poff;
-  int n_t = -2, n_pend;  // last prefetched tile, pref_off[n_t + 1] (loaded there)
+  int n_t = -2, n_pend, n_pend_v;  // last prefetched tile, pref_off[n_t + 1] (loaded there)
   u4 kv[KV_PER];
   u4 tt[NT][T_PER];
   int dep, tend_r;
@@ -212,7 +212,13 @@ struct BStream {
     // loaded when that tile was prefetched; only a jump (new chunk) waits on
     // a load here. The end offset is first used by commit().
     n_poff = nt == n_t + 1 ? n_pend : pl.pref_off[nt];
-    n_pend = pl.pref_off[nt + 1];
+    {
+      // Loaded as a per-lane value, so that nothing waits for it before
+      // commit() makes it uniform again.
+      int idx = nt + 1;
+      asm volatile("" : "+v"(idx));
+      n_pend_v = pl.pref_off[idx];
+    }
     n_t = nt;
     // Unconditional loads from in-range addresses (indices past the tile are
     // clamped; commit() ignores those values).
@@ -266,6 +272,7 @@ struct BStream {
   // after the call.
   __device__ __forceinline__ void commit(bool cold, bool publish = false, int grab = 0) {
     const int tid = threadIdx.x;
+    n_pend = uniform(n_pend_v);
     n_A = n_pend - n_poff;
     cold = cold || n_A * PJ > kCopyPer * kThreads;
     u4 cpv[kCopyPer];
@@ -384,19 +391,18 @@ struct BStream {
 // ---------------------------------------------------------------------------
 // Dynamic tile chunks. The workgroups of a head group claim chunks of
 // consecutive tiles from that group's counter (chunk c = tiles [cK, (c+1)K),
-// the last chunk running to the end, so every chunk but a lone one has at
-// least two tiles). A workgroup claims its next chunk while it computes the
-// first tile of the current one, so the claim is known before the last
-// tile's prefetch; within a chunk the prefix moves LDS to LDS, the first
-// tile of a chunk loads it from memory. Results do not depend on which
-// workgroup takes a tile.
+// K >= 3, the last chunk running to the end, so every chunk but a lone one
+// has at least three tiles). A workgroup claims its next chunk during the
+// current one, so the claim is known before the last tile's prefetch;
+// within a chunk the prefix moves LDS to LDS, the first tile of a chunk
+// loads it from memory. Results do not depend on which workgroup takes a
+// tile.
 // ---------------------------------------------------------------------------
 template <typename PlanT>
 struct ChunkLoop {
   int* ctr;
   int nch, K, ntiles;
-  int t, tend, nxt, nxt_c, nt, gr;
-  bool first;
+  int t, tend, nxt, nxt_c, nt, gr, phase;
 
   __device__ __forceinline__ ChunkLoop(const PlanT& pl, int* ctr_, int c)
       : ctr(ctr_), nch(pl.n_chunks), K(pl.chunk_tiles), ntiles(pl.n_tiles) {
@@ -404,25 +410,30 @@ struct ChunkLoop {
     tend = c < nch ? cend(c) : ntiles;
     nxt = -1;
     nxt_c = nch;
-    first = true;
+    phase = 0;
+    gr = 0;
   }
   __device__ __forceinline__ int cend(int c) const { return c == nch - 1 ? ntiles : (c + 1) * K; }
 
-  // Prefetches the next tile (if known) and claims the next chunk on the
-  // first tile of a chunk.
+  // Prefetches the next tile when it is known. settle: wait for the loads
+  // here (the one-pass backward runs faster when no fetch is in flight
+  // during its compute and stores; the other kernels keep them in flight).
   template <typename ST>
-  __device__ __forceinline__ void begin_tile(ST& st) {
+  __device__ __forceinline__ void begin_tile(ST& st, bool settle = false) {
     nt = t + 1 < tend ? t + 1 : nxt;
     if (nt >= 0) st.prefetch(nt);
-    gr = 0;
-    if (first && nch > 1 && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
+    if (settle) __builtin_amdgcn_s_waitcnt(0);
   }
-  // Installs the next tile; false when the workgroup is done.
+  // Installs the next tile; false when the workgroup is done. The claim of
+  // the next chunk is sent at the end of a chunk's first tile and published
+  // at the end of its second (chunks have at least three tiles), so its
+  // round trip overlaps a whole tile and no wait precedes the atomic.
   template <typename ST>
   __device__ __forceinline__ bool end_tile(ST& st) {
     if (nt < 0) return false;
     const bool cold = t + 1 >= tend;
-    const bool pub = first && nch > 1;
+    const bool pub = phase == 1 && nch > 1;
+    if (phase == 0 && nch > 1 && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
     st.commit(cold, pub, gr);
     if (pub) {
       nxt_c = uniform(st.tb.grab);
@@ -431,9 +442,9 @@ struct ChunkLoop {
     if (cold) {
       tend = cend(nxt_c);
       nxt = -1;
-      first = true;
+      phase = 0;
     } else {
-      first = false;
+      ++phase;
     }
     t = nt;
     return true;
@@ -918,7 +929,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   st.prefetch(cl.t);
   st.commit(true);
   do {
-    cl.begin_tile(st);
+    cl.begin_tile(st, true);
     const int nrb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;
     const int rb0 = P / kBlk;
