@@ -152,7 +152,8 @@ struct BStream {
   const Tin* TT[NT];
   const float* lse;
   const float* Dl;
-  int D, H, hg, P;
+  int D, H, P;
+  int hg, n_hg;  // head group of the current / the prefetched tile
   Tin* Ks;
   Tin* Vs;
   Tin* Ts;     // [NS][kTile][WS]
@@ -172,7 +173,7 @@ struct BStream {
   __device__ __forceinline__ BStream(const PlanT& pl_, const Tin* K_, const Tin* V_, const Tin* T0,
                                      const Tin* T1, const Tin* T2, const float* lse_, const float* Dl_,
                                      int H_, int hg_, unsigned char* dyn, Tables& tb_)
-      : pl(pl_), K(K_), V(V_), lse(lse_), Dl(Dl_), H(H_), hg(hg_), tb(tb_) {
+      : pl(pl_), K(K_), V(V_), lse(lse_), Dl(Dl_), H(H_), hg(hg_), n_hg(hg_), tb(tb_) {
     TT[0] = T0;
     if constexpr (NT > 1) TT[1] = T1;
     if constexpr (NT > 2) TT[2] = T2;
@@ -200,12 +201,14 @@ struct BStream {
   }
 
   __device__ __forceinline__ const Tin* gsrc(const Tin* base, int64_t row, int c) const {
-    return base + row * D + hg * W + c * EPC;
+    return base + row * D + n_hg * W + c * EPC;
   }
 
-  // Issues the loads of tile nt into registers (consumed by commit()).
-  __device__ __forceinline__ void prefetch(int nt) {
+  // Issues the loads of tile nt, head group g, into registers (consumed by
+  // commit()).
+  __device__ __forceinline__ void prefetch(int nt, int g) {
     const int tid = threadIdx.x;
+    n_hg = g;
     n_s = nt * kTile;
     n_ntile = min(kTile, static_cast<int>(pl.T - n_s));
     // The prefix offset of tile nt is the end offset of tile nt - 1, already
@@ -244,7 +247,7 @@ struct BStream {
     if constexpr (kTabs != 0) {
       const int i = min(tid, n_ntile * HG - 1);
       const int r = i / HG;
-      const int64_t o = (static_cast<int64_t>(n_s) + r) * H + hg * HG + (i - r * HG);
+      const int64_t o = (static_cast<int64_t>(n_s) + r) * H + n_hg * HG + (i - r * HG);
       if constexpr ((kTabs & kLse) != 0) lse_r = lse[o];
       if constexpr ((kTabs & kDl) != 0) dl_r = Dl[o];
     }
@@ -384,6 +387,7 @@ struct BStream {
     ntile = n_ntile;
     A = n_A;
     poff = n_poff;
+    hg = n_hg;
     __syncthreads();
   }
 };
@@ -401,27 +405,34 @@ struct BStream {
 template <typename PlanT>
 struct ChunkLoop {
   int* ctr;
-  int nch, K, ntiles;
-  int t, tend, nxt, nxt_c, nt, gr, phase;
+  int nch, ngr, K, ntiles;
+  int t, tend, hg, nxt, nxt_c, nt, gr, phase;
 
-  __device__ __forceinline__ ChunkLoop(const PlanT& pl, int* ctr_, int c)
-      : ctr(ctr_), nch(pl.n_chunks), K(pl.chunk_tiles), ntiles(pl.n_tiles) {
-    t = c < nch ? c * K : ntiles;
-    tend = c < nch ? cend(c) : ntiles;
+  // c: the workgroup's first claim. Claim c is tile chunk c / ngr of head
+  // group c % ngr, so the head groups of a chunk run at about the same time
+  // and the rows they split are fetched together.
+  __device__ __forceinline__ ChunkLoop(const PlanT& pl, int* ctr_, int ngr_, int c)
+      : ctr(ctr_), nch(pl.n_chunks), ngr(ngr_), K(pl.chunk_tiles), ntiles(pl.n_tiles) {
+    const int ch = c / ngr;
+    hg = c - ch * ngr;
+    t = ch < nch ? ch * K : ntiles;
+    tend = ch < nch ? cend(ch) : ntiles;
     nxt = -1;
-    nxt_c = nch;
+    nxt_c = nch * ngr;
     phase = 0;
     gr = 0;
   }
-  __device__ __forceinline__ int cend(int c) const { return c == nch - 1 ? ntiles : (c + 1) * K; }
+  __device__ __forceinline__ int cend(int ch) const { return ch == nch - 1 ? ntiles : (ch + 1) * K; }
+  __device__ __forceinline__ int claims() const { return nch * ngr; }
 
   // Prefetches the next tile when it is known. settle: wait for the loads
   // here (the one-pass backward runs faster when no fetch is in flight
   // during its compute and stores; the other kernels keep them in flight).
   template <typename ST>
   __device__ __forceinline__ void begin_tile(ST& st, bool settle = false) {
-    nt = t + 1 < tend ? t + 1 : nxt;
-    if (nt >= 0) st.prefetch(nt);
+    const bool within = t + 1 < tend;
+    nt = within ? t + 1 : nxt;
+    if (nt >= 0) st.prefetch(nt, within ? hg : nxt_c % ngr);
     if (settle) __builtin_amdgcn_s_waitcnt(0);
   }
   // Installs the next tile; false when the workgroup is done. The claim of
@@ -432,15 +443,16 @@ struct ChunkLoop {
   __device__ __forceinline__ bool end_tile(ST& st) {
     if (nt < 0) return false;
     const bool cold = t + 1 >= tend;
-    const bool pub = phase == 1 && nch > 1;
-    if (phase == 0 && nch > 1 && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
+    const bool pub = phase == 1 && claims() > 1;
+    if (phase == 0 && claims() > 1 && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
     st.commit(cold, pub, gr);
     if (pub) {
       nxt_c = uniform(st.tb.grab);
-      nxt = nxt_c < nch ? nxt_c * K : -1;
+      nxt = nxt_c < claims() ? (nxt_c / ngr) * K : -1;
     }
     if (cold) {
-      tend = cend(nxt_c);
+      tend = cend(nxt_c / ngr);
+      hg = nxt_c % ngr;
       nxt = -1;
       phase = 0;
     } else {
@@ -469,11 +481,10 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   constexpr int WS = ST::WS;
   __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int hg = blockIdx.x % (H / HG);
-  int* ctr = pl.sched + 0 * kMaxHeads + hg;
+  int* ctr = pl.sched + 0;
   if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
-  ST st(pl, K, V, Q, nullptr, nullptr, nullptr, nullptr, H, hg, dyn, tb);
-  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  ST st(pl, K, V, Q, nullptr, nullptr, nullptr, nullptr, H, 0, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, H / HG, uniform(tb.grab));  // the constructor's barrier publishes the claim
   if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -481,7 +492,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   const int D = H * HD;
   const float qscale = scale * kLog2e;
   const int P = st.P;
-  st.prefetch(cl.t);
+  st.prefetch(cl.t, cl.hg);
   st.commit(true);
   do {
     cl.begin_tile(st);
@@ -553,7 +564,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
         for (int e = 0; e < UH; ++e) {
           const float le = group_sum(l[e]);
           const float inv = __builtin_amdgcn_rcpf(le);
-          const int h = hg * HG + h0 + e;
+          const int h = st.hg * HG + h0 + e;
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
             float v[4] = {o[e][j][0] * inv, o[e][j][1] * inv, o[e][j][2] * inv, o[e][j][3] * inv};
@@ -586,11 +597,10 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   constexpr int WS = ST::WS;
   __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int hg = blockIdx.x % (H / HG);
-  int* ctr = pl.sched + 1 * kMaxHeads + hg;
+  int* ctr = pl.sched + 1;
   if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
-  ST st(pl, K, V, Q, dO, O, lse, nullptr, H, hg, dyn, tb);
-  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  ST st(pl, K, V, Q, dO, O, lse, nullptr, H, 0, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, H / HG, uniform(tb.grab));  // the constructor's barrier publishes the claim
   if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -600,7 +610,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   const int P = st.P;
   const Tin* Qs = st.Ts;
   const Tin* Gs = st.Ts + kTile * WS;
-  st.prefetch(cl.t);
+  st.prefetch(cl.t, cl.hg);
   st.commit(true);
   do {
     cl.begin_tile(st);
@@ -701,7 +711,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         const int pos = rope.cos_t ? rope_pos(tb.depth[q], rope.seq_len) : 0;
 #pragma unroll
         for (int e = 0; e < UH; ++e) {
-          const int h = hg * HG + h0 + e;
+          const int h = st.hg * HG + h0 + e;
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
             float v[4] = {dq[e][j][0], dq[e][j][1], dq[e][j][2], dq[e][j][3]};
@@ -736,11 +746,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   constexpr int WS = ST::WS;
   __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int hg = blockIdx.x % (H / HG);
-  int* ctr = pl.sched + 2 * kMaxHeads + hg;
+  int* ctr = pl.sched + 2;
   if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
-  ST st(pl, K, V, Q, dO, nullptr, lse, Dl, H, hg, dyn, tb);
-  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  ST st(pl, K, V, Q, dO, nullptr, lse, Dl, H, 0, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, H / HG, uniform(tb.grab));  // the constructor's barrier publishes the claim
   if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -750,7 +759,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   const int P = st.P;
   const Tin* Qs = st.Ts;
   const Tin* Gs = st.Ts + kTile * WS;
-  st.prefetch(cl.t);
+  st.prefetch(cl.t, cl.hg);
   st.commit(true);
   do {
     cl.begin_tile(st);
@@ -824,7 +833,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           const int64_t row = static_cast<int64_t>(st.poff) + d;
 #pragma unroll
           for (int e = 0; e < UH; ++e) {
-            const int hd = hg * HG + h0 + e;
+            const int hd = st.hg * HG + h0 + e;
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
               float a[4] = {dk[e][j][0], dk[e][j][1], dk[e][j][2], dk[e][j][3]};
@@ -842,7 +851,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           const int pos = rope.cos_t ? rope_pos(tb.depth[r], rope.seq_len) : 0;
 #pragma unroll
           for (int e = 0; e < UH; ++e) {
-            const int hd = hg * HG + h0 + e;
+            const int hd = st.hg * HG + h0 + e;
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
               const int d0 = kBlk * j + 4 * g;
@@ -910,11 +919,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   constexpr int WS = ST::WS;
   __shared__ typename ST::Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
-  const int hg = blockIdx.x % (H / HG);
-  int* ctr = pl.sched + 1 * kMaxHeads + hg;
+  int* ctr = pl.sched + 1;
   if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
-  ST st(pl, K, V, Q, dO, O, lse, nullptr, H, hg, dyn, tb);
-  ChunkLoop<PlanT> cl(pl, ctr, uniform(tb.grab));  // the constructor's barrier publishes the claim
+  ST st(pl, K, V, Q, dO, O, lse, nullptr, H, 0, dyn, tb);
+  ChunkLoop<PlanT> cl(pl, ctr, H / HG, uniform(tb.grab));  // the constructor's barrier publishes the claim
   if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -926,7 +934,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const Tin* Gs = st.Ts + kTile * WS;
   float* dqs = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));  // [wave][HG][kTile][HD]
   float* tr = dqs + kWaves * HG * kTile * HD + wave * (kBlk * 20);         // this wave's dS^T tile
-  st.prefetch(cl.t);
+  st.prefetch(cl.t, cl.hg);
   st.commit(true);
   do {
     cl.begin_tile(st, true);
@@ -1023,7 +1031,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         const int d = kslot - (P - st.A);
         if (d >= 0) {
           const int64_t row = static_cast<int64_t>(st.poff) + d;
-          const int hd = hg * HG + hh;
+          const int hd = st.hg * HG + hh;
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
             float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
@@ -1038,7 +1046,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           const int64_t a = static_cast<int64_t>(st.s) + r;
           const bool done = tb.tend[r] <= st.s + st.ntile;
           const int pos = rope.cos_t ? rope_pos(tb.depth[r], rope.seq_len) : 0;
-          const int hd = hg * HG + hh;
+          const int hd = st.hg * HG + hh;
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
             const int d0 = kBlk * j + 4 * g;
@@ -1080,7 +1088,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       float v[4] = {sum[0], sum[1], sum[2], sum[3]};
       if (rope.cos_t)
         agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, rope_pos(tb.depth[q], rope.seq_len), d0);
-      store_vec<4>(dQ + (static_cast<int64_t>(st.s) + q) * D + (hg * HG + e) * HD + d0, v);
+      store_vec<4>(dQ + (static_cast<int64_t>(st.s) + q) * D + (st.hg * HG + e) * HD + d0, v);
     }
   } while (cl.end_tile(st));
 }
