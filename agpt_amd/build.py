@@ -32,6 +32,9 @@ HIP_FLAGS = [
     # Matrix-instruction accumulators in ordinary VGPRs: the kernels rescale
     # and read them between steps, which the AGPR form turns into copies.
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # One lane takes each scheduling ticket; combining the lanes' atomics
+    # would make the wave wait for the ticket right where it is issued.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     # No kernel result depends on NaN handling; without IEEE mode the float
     # max/min of the softmax need no NaN-quieting instructions.
     "-fno-honor-nans", "-Xarch_device", "-mno-amdgpu-ieee",

@@ -425,15 +425,12 @@ struct ChunkLoop {
   __device__ __forceinline__ int cend(int ch) const { return ch == nch - 1 ? ntiles : (ch + 1) * K; }
   __device__ __forceinline__ int claims() const { return nch * ngr; }
 
-  // Prefetches the next tile when it is known. settle: wait for the loads
-  // here (the one-pass backward runs faster when no fetch is in flight
-  // during its compute and stores; the other kernels keep them in flight).
+  // Prefetches the next tile when it is known.
   template <typename ST>
-  __device__ __forceinline__ void begin_tile(ST& st, bool settle = false) {
+  __device__ __forceinline__ void begin_tile(ST& st) {
     const bool within = t + 1 < tend;
     nt = within ? t + 1 : nxt;
     if (nt >= 0) st.prefetch(nt, within ? hg : nxt_c % ngr);
-    if (settle) __builtin_amdgcn_s_waitcnt(0);
   }
   // Installs the next tile; false when the workgroup is done. The claim of
   // the next chunk is sent at the end of a chunk's first tile and published
@@ -937,7 +934,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   st.prefetch(cl.t, cl.hg);
   st.commit(true);
   do {
-    cl.begin_tile(st, true);
+    cl.begin_tile(st);
     const int nrb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;
     const int rb0 = P / kBlk;
