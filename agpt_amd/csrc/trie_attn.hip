@@ -949,7 +949,7 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
   if (h->variant == 6) {
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_sched), kSchedBytes));
-    h->chunk_tiles = std::max(3, env_int("AGPT_ATTN_CHUNK", 24));
+    h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", 24));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
   }
   h->planned = true;

@@ -393,65 +393,82 @@ struct BStream {
 };
 
 // ---------------------------------------------------------------------------
-// Dynamic tile chunks. The workgroups of a head group claim chunks of
-// consecutive tiles from that group's counter (chunk c = tiles [cK, (c+1)K),
-// K >= 3, the last chunk running to the end, so every chunk but a lone one
-// has at least three tiles). A workgroup claims its next chunk during the
-// current one, so the claim is known before the last tile's prefetch;
-// within a chunk the prefix moves LDS to LDS, the first tile of a chunk
-// loads it from memory. Results do not depend on which workgroup takes a
-// tile.
+// Dynamic tile chunks. Workgroups claim (chunk, head group) pairs from one
+// counter per kernel (chunk c = tiles [cK, (c+1)K), the last chunk running
+// to the end). A workgroup claims
+// its next chunk during the current one, so with three or more tiles per
+// chunk the claim is known before the last tile's prefetch; within a chunk
+// the prefix moves LDS to LDS, the first tile of a chunk loads it from
+// memory. Results do not depend on which workgroup takes a tile.
 // ---------------------------------------------------------------------------
 template <typename PlanT>
 struct ChunkLoop {
   int* ctr;
   int nch, ngr, K, ntiles;
   int t, tend, hg, nxt, nxt_c, nt, gr, phase;
+  bool sent, known;  // the next claim is sent / published
 
-  // c: the workgroup's first claim. Claim c is tile chunk c / ngr of head
-  // group c % ngr, so the head groups of a chunk run at about the same time
-  // and the rows they split are fetched together.
+  // Claim c is tile chunk c / ngr of head group c % ngr, so the head groups
+  // of a chunk run at about the same time and the rows they split are
+  // fetched together.
+  __device__ __forceinline__ int chunk_of(int c) const { return c / ngr; }
+  __device__ __forceinline__ bool valid(int c) const { return chunk_of(c) < nch; }
+
   __device__ __forceinline__ ChunkLoop(const PlanT& pl, int* ctr_, int ngr_, int c)
       : ctr(ctr_), nch(pl.n_chunks), ngr(ngr_), K(pl.chunk_tiles), ntiles(pl.n_tiles) {
-    const int ch = c / ngr;
-    hg = c - ch * ngr;
-    t = ch < nch ? ch * K : ntiles;
-    tend = ch < nch ? cend(ch) : ntiles;
+    hg = c % ngr;
+    t = valid(c) ? chunk_of(c) * K : ntiles;
+    tend = valid(c) ? cend(chunk_of(c)) : ntiles;
     nxt = -1;
-    nxt_c = nch * ngr;
+    nxt_c = c;
     phase = 0;
     gr = 0;
+    sent = known = false;
   }
   __device__ __forceinline__ int cend(int ch) const { return ch == nch - 1 ? ntiles : (ch + 1) * K; }
-  __device__ __forceinline__ int claims() const { return nch * ngr; }
 
-  // Prefetches the next tile when it is known.
+  template <typename ST>
+  __device__ __forceinline__ void learn(ST& st) {
+    nxt_c = uniform(st.tb.grab);
+    nxt = valid(nxt_c) ? chunk_of(nxt_c) * K : -1;
+    known = true;
+  }
+
+  // Prefetches the next tile. On the last tile of a chunk whose next claim
+  // is not published yet (a chunk of one or two tiles) the claim completes
+  // here, with a barrier.
   template <typename ST>
   __device__ __forceinline__ void begin_tile(ST& st) {
     const bool within = t + 1 < tend;
+    if (!within && !known) {
+      if (!sent && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
+      sent = true;
+      if (threadIdx.x == 0) st.tb.grab = gr;
+      __syncthreads();
+      learn(st);
+    }
     nt = within ? t + 1 : nxt;
     if (nt >= 0) st.prefetch(nt, within ? hg : nxt_c % ngr);
   }
-  // Installs the next tile; false when the workgroup is done. The claim of
-  // the next chunk is sent at the end of a chunk's first tile and published
-  // at the end of its second (chunks have at least three tiles), so its
-  // round trip overlaps a whole tile and no wait precedes the atomic.
+  // Installs the next tile; false when the workgroup is done. The next claim
+  // is sent at the end of a chunk's first tile and published at the end of
+  // its second, so its round trip overlaps a whole tile and no wait
+  // precedes the atomic.
   template <typename ST>
   __device__ __forceinline__ bool end_tile(ST& st) {
     if (nt < 0) return false;
     const bool cold = t + 1 >= tend;
-    const bool pub = phase == 1 && claims() > 1;
-    if (phase == 0 && claims() > 1 && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
+    const bool pub = phase == 1 && !known;
+    if (!sent && threadIdx.x == 0) gr = atomicAdd(ctr, 1);
+    sent = true;
     st.commit(cold, pub, gr);
-    if (pub) {
-      nxt_c = uniform(st.tb.grab);
-      nxt = nxt_c < claims() ? (nxt_c / ngr) * K : -1;
-    }
+    if (pub) learn(st);
     if (cold) {
-      tend = cend(nxt_c / ngr);
+      tend = cend(chunk_of(nxt_c));
       hg = nxt_c % ngr;
       nxt = -1;
       phase = 0;
+      sent = known = false;
     } else {
       ++phase;
     }

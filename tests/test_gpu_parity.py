@@ -21,8 +21,9 @@ VARIANTS = {
     "default": {},
     "block_hg1_fused_hg2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "1", "AGPT_ATTN_FHG": "2"},
     "block_split": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUSED": "0"},
-    "block_hg4_all_heads_chunk3": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4", "AGPT_ATTN_UH": "4",
-                                   "AGPT_ATTN_CHUNK": "3"},
+    "block_chunk2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHUNK": "2"},
+    "block_hg4_all_heads_chunk1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4", "AGPT_ATTN_UH": "4",
+                                   "AGPT_ATTN_CHUNK": "1"},
     "chain": {"AGPT_ATTN_VARIANT": "5"},
     "chain_hg1_qb1_kb1": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "1", "AGPT_ATTN_QB": "1",
                           "AGPT_ATTN_KB": "1"},
