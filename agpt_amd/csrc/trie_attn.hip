@@ -756,11 +756,19 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     h->fwd_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 1, false);
     h->bq_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4);
     h->kv_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, false);
-    h->fhg = env_int("AGPT_ATTN_FHG", 1);
+    // One-pass backward: the fewest heads per workgroup whose row segment
+    // fills a 128-byte line (a half-used line is fetched whole, and its
+    // other half by another workgroup, often on another XCD's L2).
+    int fhg = env_int("AGPT_ATTN_FHG", 0);
+    if (fhg == 0) {
+      fhg = 1;
+      while (fhg * 2 <= 2 && H % (fhg * 2) == 0 && fhg * hd * elem < 128) fhg *= 2;
+    }
+    h->fhg = fhg;
     h->fused = elem == 4 && env_int("AGPT_ATTN_FUSED", 1) != 0 && H % h->fhg == 0 &&
                (h->fhg == 1 || h->fhg == 2);
     h->fb_lds = agpt_blk::block_lds_bytes(h->max_depth, h->fhg, hd, elem, 2, false) +
-                agpt_blk::fused_scratch_bytes(hd, h->fhg);
+                agpt_blk::fused_scratch_bytes(hd);
     const int bbudget = lim - static_cast<int>(sizeof(agpt_blk::BlockTables<4>));
     const bool ok = (hd == 16 || hd == 32) && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
                     (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(bbudget) &&

@@ -906,17 +906,20 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 //   dQ_i^T += K^T dS^T                   (dS transposed through a per-wave
 //                                        LDS tile; accumulated in the
 //                                        wave's own LDS dQ tile).
-// The units of a tile are dealt to the waves longest first, each to the
-// least loaded wave (every wave computes the same assignment). After the
-// units the workgroup sums the waves' dQ tiles in wave order, then applies
-// inverse RoPE: the order of every sum is fixed, so results are bitwise
-// reproducible. δ = dO·O comes with the tile (the stream reduces the
-// fetched O).
+// Each head of the group has kWaves / HG waves of its own; the units of a
+// head (its key blocks) are dealt to them longest first, each to the least
+// loaded wave (every wave computes the same assignment). After the units
+// the workgroup sums each head's wave tiles of dQ in wave order, then
+// applies inverse RoPE: the order of every sum is fixed, so results are
+// bitwise reproducible. δ = dO·O comes with the tile (the stream reduces
+// the fetched O). Two heads per workgroup (HG = 2) fetch whole 128-byte
+// row segments at hd 16, where one head would leave half of every fetched
+// line to another workgroup.
 // ---------------------------------------------------------------------------
-// LDS past the stream: dQ partials [wave][HG][kTile][HD] and dS^T tiles
-// [wave][16][20].
-__host__ __device__ constexpr size_t fused_scratch_bytes(int HD, int HG) {
-  return static_cast<size_t>(kWaves) * (HG * kTile * HD + kBlk * 20) * sizeof(float);
+// LDS past the stream: dQ partials [wave][kTile][HD] (each wave serves one
+// head) and dS^T tiles [wave][16][20].
+__host__ __device__ constexpr size_t fused_scratch_bytes(int HD) {
+  return static_cast<size_t>(kWaves) * (kTile * HD + kBlk * 20) * sizeof(float);
 }
 
 template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
@@ -927,6 +930,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     float* __restrict__ Pv, const float* __restrict__ acc_dk, const float* __restrict__ acc_dv,
     RopeT rope, int H, float scale) {
   static_assert(sizeof(Tin) == sizeof(float), "the fused backward takes fp32 inputs (δ = dO·O)");
+  static_assert(kWaves % HG == 0, "whole waves per head");
+  constexpr int WPH = kWaves / HG;  // waves per head
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
   using ST = BStream<HD, Tin, HG, 3, kLse | kDeltaO, PlanT>;
@@ -946,37 +951,45 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int P = st.P;
   const Tin* Qs = st.Ts;
   const Tin* Gs = st.Ts + kTile * WS;
-  float* dqs = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));  // [wave][HG][kTile][HD]
-  float* tr = dqs + kWaves * HG * kTile * HD + wave * (kBlk * 20);         // this wave's dS^T tile
+  float* dqs = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));  // [wave][kTile][HD]
+  float* tr = dqs + kWaves * kTile * HD + wave * (kBlk * 20);              // this wave's dS^T tile
+  const int hh = wave / WPH;  // this wave's head of the group
+  const int wl = wave % WPH;  // and its place among that head's waves
   st.prefetch(cl.t, cl.hg);
   st.commit(true);
+  bool more;
   do {
     cl.begin_tile(st);
     const int nrb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;
     const int rb0 = P / kBlk;
-    const int nu = (rb0 - pb0 + nrb) * HG;  // units: key blocks (prefix first) x heads
-    // This wave's dQ tile [HG][kTile][HD] starts at zero.
-    float* mydq = dqs + wave * HG * kTile * HD;
-    for (int x = lane; x < HG * kTile * HD / 4; x += 64)
-      reinterpret_cast<f4*>(mydq)[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int nu = rb0 - pb0 + nrb;  // units of a head: key blocks, prefix first
+    // This wave's dQ tile [kTile][HD] starts at zero.
+    float* mydq = dqs + wave * kTile * HD;
+    for (int x = lane; x < kTile * HD / 4; x += 64) reinterpret_cast<f4*>(mydq)[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int load0 = 0, load1 = 0, load2 = 0, load3 = 0;
     for (int u = 0; u < nu; ++u) {
-      const int b = pb0 + u / HG;
-      const int hh = u % HG;
+      const int b = pb0 + u;
       const int i0 = b < rb0 ? 0 : b - rb0;
       const int i1 = uniform((tb.bhi[b] + kBlk - 1) / kBlk);
-      // Least loaded wave (lowest index on ties) takes the unit.
-      int w = 0, lmin = load0;
-      if (load1 < lmin) { w = 1; lmin = load1; }
-      if (load2 < lmin) { w = 2; lmin = load2; }
-      if (load3 < lmin) { w = 3; lmin = load3; }
+      // Least loaded wave of the head (lowest index on ties) takes the unit.
       const int cost = i1 - i0;
-      if (w == 0) load0 += cost;
-      else if (w == 1) load1 += cost;
-      else if (w == 2) load2 += cost;
-      else load3 += cost;
-      if (w != wave) continue;
+      int w = 0;
+      if constexpr (WPH == 4) {
+        int lmin = load0;
+        if (load1 < lmin) { w = 1; lmin = load1; }
+        if (load2 < lmin) { w = 2; lmin = load2; }
+        if (load3 < lmin) { w = 3; lmin = load3; }
+        if (w == 0) load0 += cost;
+        else if (w == 1) load1 += cost;
+        else if (w == 2) load2 += cost;
+        else load3 += cost;
+      } else if constexpr (WPH == 2) {
+        w = load1 < load0 ? 1 : 0;
+        if (w == 0) load0 += cost;
+        else load1 += cost;
+      }
+      if (w != wl) continue;
       const int hoff = hh * HD;
       const int kslot = kBlk * b + c;  // this lane's key
       float kf[KD], vf[KD], kt[MT][4];
@@ -1033,7 +1046,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         // lane: dims 16j+4g.. of query row qr
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
-          f4* dqp = reinterpret_cast<f4*>(mydq + (hh * kTile + qr) * HD + kBlk * j + 4 * g);
+          f4* dqp = reinterpret_cast<f4*>(mydq + qr * HD + kBlk * j + 4 * g);
           f4 acc = *dqp;
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc = mfma16(kt[j][r], dst[r], acc);
@@ -1087,24 +1100,37 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         }
       }
     }
-    // dQ: the sum of the waves' tiles in wave order.
+    // dQ: the sum of the waves' tiles in wave order, held in registers while
+    // the next tile is installed and stored after it: the install waits for
+    // the prefetched rows, and the memory counter retires operations in
+    // issue order, so a store issued before it would be waited for too.
     __syncthreads();
     constexpr int kQuads = HG * kTile * HD / 4;  // 4 consecutive dims of a row of a head
-    for (int x = threadIdx.x; x < kQuads; x += kThreads) {
+    static_assert(kQuads % kThreads == 0, "whole dQ quads per thread");
+    constexpr int kPer = kQuads / kThreads;
+    float qv[kPer][4];
+    int64_t qo[kPer];  // element offset of the quad in dQ; -1: row past the tile
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int x = threadIdx.x + k * kThreads;
       const int e = x / (kTile * HD / 4);
       const int rem = x - e * (kTile * HD / 4);
       const int q = rem / (HD / 4);
       const int d0 = (rem - q * (HD / 4)) * 4;
-      if (q >= st.ntile) continue;
-      f4 sum = *reinterpret_cast<const f4*>(dqs + (e * kTile + q) * HD + d0);
+      f4 sum = *reinterpret_cast<const f4*>(dqs + (e * WPH * kTile + q) * HD + d0);
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) sum += *reinterpret_cast<const f4*>(dqs + ((w * HG + e) * kTile + q) * HD + d0);
-      float v[4] = {sum[0], sum[1], sum[2], sum[3]};
-      if (rope.cos_t)
-        agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, rope_pos(tb.depth[q], rope.seq_len), d0);
-      store_vec<4>(dQ + (static_cast<int64_t>(st.s) + q) * D + (st.hg * HG + e) * HD + d0, v);
+      for (int w = 1; w < WPH; ++w) sum += *reinterpret_cast<const f4*>(dqs + ((e * WPH + w) * kTile + q) * HD + d0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qv[k][r] = sum[r];
+      if (rope.cos_t && q < st.ntile)
+        agpt_fast::rope_inverse_part<4, HD>(qv[k], rope.cos_t, rope.sin_t, rope_pos(tb.depth[q], rope.seq_len), d0);
+      qo[k] = q < st.ntile ? (static_cast<int64_t>(st.s) + q) * D + (st.hg * HG + e) * HD + d0 : -1;
     }
-  } while (cl.end_tile(st));
+    more = cl.end_tile(st);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      if (qo[k] >= 0) store_vec<4>(dQ + qo[k], qv[k]);
+  } while (more);
 }
 
 }  // namespace agpt_blk

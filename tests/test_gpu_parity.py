@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 # every parity test below runs against each of them.
 VARIANTS = {
     "default": {},
-    "block_hg1_fused_hg2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "1", "AGPT_ATTN_FHG": "2"},
+    "block_hg1_fused_hg1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "1", "AGPT_ATTN_FHG": "1"},
     "block_split": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUSED": "0"},
     "block_chunk2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHUNK": "2"},
     "block_hg4_all_heads_chunk1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4", "AGPT_ATTN_UH": "4",
