@@ -547,6 +547,9 @@ struct agpt_attn_s {
   bool unit_all_heads = false;  // block kernels: a unit takes every head of the group
   bool fused = false;           // block kernels: one-pass backward (fp32)
   int fhg = 1;                  // heads per workgroup of the one-pass backward
+  bool carry = false;           // one-pass backward carries path sums (E, F replace Pk, Pv)
+  float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
+  float* d_F = nullptr;
   size_t fb_lds = 0;
   bool split = true;  // cut long work items into parts (see agpt_fast::kCutSteps)
   int q_slots = 0, k_slots = 0;  // scratch slots of cut query / key items per tile
@@ -565,7 +568,7 @@ void free_plan(agpt_attn_s* h) {
       (void)hipFree(*p);
       *p = nullptr;
     }
-  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv, &h->d_Dl};
+  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv, &h->d_Dl, &h->d_E, &h->d_F};
   for (auto p : fp)
     if (*p) {
       (void)hipFree(*p);
@@ -743,6 +746,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
   {
     const int v = env_int("AGPT_ATTN_VARIANT", 6);
     h->variant = (v == 5 || v == 6) ? v : 0;
+    h->fused = h->carry = false;
   }
   if (h->variant == 6) {
     int hg = env_int("AGPT_ATTN_HG", 0);
@@ -767,15 +771,25 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     h->fhg = fhg;
     h->fused = elem == 4 && env_int("AGPT_ATTN_FUSED", 1) != 0 && H % h->fhg == 0 &&
                (h->fhg == 1 || h->fhg == 2);
-    h->fb_lds = agpt_blk::block_lds_bytes(h->max_depth, h->fhg, hd, elem, 2, false) +
-                agpt_blk::fused_scratch_bytes(hd);
+    h->fb_lds = agpt_blk::fused_lds_bytes(h->max_depth, h->fhg, hd, false);
     const int bbudget = lim - static_cast<int>(sizeof(agpt_blk::BlockTables<4>));
     const bool ok = (hd == 16 || hd == 32) && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
                     (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(bbudget) &&
                     h->bq_lds <= static_cast<size_t>(bbudget) && h->kv_lds <= static_cast<size_t>(bbudget);
     if (h->fused && h->fb_lds > static_cast<size_t>(bbudget)) h->fused = false;
+    // Path carry (head_dim 16: its dQ registers fit) when its LDS keeps the
+    // workgroups per CU (registers hold the one-pass backward to two).
+    {
+      const size_t tabs = sizeof(agpt_blk::BlockTables<2>);
+      auto per_cu = [&](size_t b) { return static_cast<size_t>(lim) / ((b + tabs + 511) & ~static_cast<size_t>(511)); };
+      const size_t with = agpt_blk::fused_lds_bytes(h->max_depth, h->fhg, hd, true);
+      h->carry = h->fused && hd == 16 && env_int("AGPT_ATTN_CARRY", 1) != 0 &&
+                 per_cu(with) >= std::min<size_t>(per_cu(h->fb_lds), 2) && per_cu(with) >= 1;
+      if (h->carry) h->fb_lds = with;
+    }
     if (ok) return;
     h->variant = 5;  // try the chain-group walk
+    h->fused = h->carry = false;
   }
   if (h->variant != 5) {
     const int t = env_int("AGPT_ATTN_TILE", 64);
@@ -947,19 +961,25 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
     if ((rc = upload(&h->d_q_item_off, q_off)) != AGPT_OK) return rc;
     if ((rc = upload(&h->d_k_item_off, k_off)) != AGPT_OK) return rc;
   }
-  const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pk), pbytes));
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pv), pbytes));
-  const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Ck), cbytes));
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
-  if (h->variant == 5 || h->variant == 6)
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
   if (h->variant == 6) {
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_sched), kSchedBytes));
     h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", 24));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
   }
+  if (h->carry) {
+    const size_t ebytes = static_cast<size_t>(h->n_chunks_sched) * agpt_blk::prefix_cap(maxd) * 2 * D * sizeof(float);
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_E), std::max<size_t>(ebytes, 16)));
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_F), std::max<size_t>(ebytes, 16)));
+  } else {
+    const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pk), pbytes));
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pv), pbytes));
+    const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Ck), cbytes));
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
+  }
+  if (h->variant == 5 || h->variant == 6)
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
   h->planned = true;
   g_last_error.clear();
   return AGPT_OK;
@@ -1008,7 +1028,7 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
     snprintf(buf, sizeof(buf),
              "streaming block-sparse 16x16 mfma, %s backward: tile_rows=%d tiles=%d heads_per_wg=%d "
              "heads_per_unit=%d fwd_lds=%zu bwd_lds=%zu/%zu lds_limit=%d",
-             h->fused ? "one-pass" : "split", h->tile, h->n_tiles, h->hg, h->unit_all_heads ? h->hg : 1,
+             h->fused ? (h->carry ? "one-pass path-carry" : "one-pass") : "split", h->tile, h->n_tiles, h->hg, h->unit_all_heads ? h->hg : 1,
              h->fwd_lds, h->fused ? h->fb_lds : h->bq_lds, h->fused ? 0 : h->kv_lds, h->max_lds);
   else if (h->variant == 5)
     snprintf(buf, sizeof(buf),
@@ -1166,20 +1186,40 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if constexpr ((HD == 16 || HD == 32) && std::is_same<Tin, float>::value) {
     if (h->variant == 6 && h->fused) {
       (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
-      with_124(h->fhg, [&](auto hgc) {
+      auto run = [&](auto hgc, auto cc) {
         constexpr int HG = decltype(hgc)::value;
+        constexpr bool kCarry = decltype(cc)::value;
         if constexpr (HG <= 2) {
-          auto fb = agpt_blk::bwd_kernel<HD, Tin, HG, PlanDev, RopeArgs>;
+          auto fb = agpt_blk::bwd_kernel<HD, Tin, HG, kCarry, PlanDev, RopeArgs>;
           set_lds(fb, h->fb_lds);
           hipLaunchKernelGGL(fb, dim3(stream_grid(h, fb, h->fb_lds, HG)), dim3(agpt_blk::kThreads), h->fb_lds,
                              st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
                              static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
-                             static_cast<const Tin*>(dO), dq, dk, dv, h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope,
-                             h->cfg.n_heads, scale);
+                             static_cast<const Tin*>(dO), dq, dk, dv, kCarry ? h->d_E : h->d_Pk,
+                             kCarry ? h->d_F : h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
         }
+      };
+      with_124(h->fhg, [&](auto hgc) {
+        if constexpr (HD == 16) {
+          if (h->carry) {
+            run(hgc, std::true_type{});
+            return;
+          }
+        }
+        run(hgc, std::false_type{});
       });
       pm.mark(1);
       fused_done = true;
+      if (h->carry) {
+        pm.mark(2);
+        pm.mark(3);
+        if (HD == 16 && h->n_chunks_sched > 1)
+          hipLaunchKernelGGL((agpt_blk::bwd_carry_kernel<HD, PlanDev, RopeArgs>), dim3(h->n_chunks_sched - 1),
+                             dim3(256), 0, st, plan_dev(h), h->d_E, h->d_F, dk, dv, acc_dk, acc_dv, rope,
+                             h->cfg.n_heads);
+        pm.mark(4);
+        return;
+      }
     }
   }
   if (fused_done) {

@@ -916,19 +916,48 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 // row segments at hd 16, where one head would leave half of every fetched
 // line to another workgroup.
 // ---------------------------------------------------------------------------
-// LDS past the stream: dQ partials [wave][kTile][HD] (each wave serves one
-// head) and dS^T tiles [wave][16][20].
-__host__ __device__ constexpr size_t fused_scratch_bytes(int HD) {
-  return static_cast<size_t>(kWaves) * (kTile * HD + kBlk * 20) * sizeof(float);
+//
+// Path carry (kCarry). Within a chunk a workgroup visits consecutive tiles,
+// and the keys a tile leaves open (subtree not finished) are exactly the
+// prefix of the next tile: the ancestors of its first row, one per depth.
+// So instead of one partial per (tile, prefix key) the workgroup keeps the
+// dK/dV sums of the current path in LDS, indexed by depth: a prefix key
+// that the next tile still sees adds its tile sum there; one that it does
+// not see is finished: its total goes to dK/dV (a key first seen in this
+// chunk whose subtree ends here), or to the chunk's partial E[chunk][depth]
+// (a key from before the chunk), or at the chunk's end to F[chunk][depth]
+// (a key of this chunk still open). Open tile rows start their depth's sum.
+// The sums live in two copies by tile parity: a tile reads its prefix's
+// sums from one and writes the next tile's into the other, so a sum that
+// ends and the one that replaces it at the same depth never meet. With the
+// carry each wave also keeps its dQ in registers (one 16x16 block per query
+// block of the tile), summed across the head's waves through LDS at the end
+// of the tile; bwd_carry_kernel then adds F and the later chunks' E in
+// chunk order.
+// ---------------------------------------------------------------------------
+// LDS past the stream. Without the carry: dQ partials [wave][kTile][HD]
+// (each wave serves one head) and dS^T tiles [wave][16][20]. With it: the
+// dS^T tiles, the path sums [2][P][HG][2 * HD + 4] (dK, dV; padded) and the
+// row of each depth [2][P].
+__host__ __device__ constexpr int carry_stride(int HD) { return 2 * HD + 4; }
+__host__ __device__ constexpr size_t carry_bytes(int max_depth, int HG, int HD) {
+  return 2 * static_cast<size_t>(prefix_cap(max_depth)) * (HG * carry_stride(HD) + 1) * sizeof(float);
+}
+__host__ __device__ inline size_t fused_lds_bytes(int max_depth, int HG, int HD, bool carry) {
+  const size_t tr = static_cast<size_t>(kWaves) * kBlk * 20 * sizeof(float);
+  return block_lds_bytes(max_depth, HG, HD, sizeof(float), 2, false) + tr +
+         (carry ? carry_bytes(max_depth, HG, HD) : static_cast<size_t>(kWaves) * kTile * HD * sizeof(float));
 }
 
-template <int HD, typename Tin, int HG, typename PlanT, typename RopeT>
+template <int HD, typename Tin, int HG, bool kCarry, typename PlanT, typename RopeT>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ Pk,
     float* __restrict__ Pv, const float* __restrict__ acc_dk, const float* __restrict__ acc_dv,
     RopeT rope, int H, float scale) {
+  // With the carry, Pk holds E and Pv holds F: [n_chunks][P][2][D] (dK, dV).
+
   static_assert(sizeof(Tin) == sizeof(float), "the fused backward takes fp32 inputs (δ = dO·O)");
   static_assert(kWaves % HG == 0, "whole waves per head");
   constexpr int WPH = kWaves / HG;  // waves per head
@@ -951,8 +980,16 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int P = st.P;
   const Tin* Qs = st.Ts;
   const Tin* Gs = st.Ts + kTile * WS;
-  float* dqs = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));  // [wave][kTile][HD]
-  float* tr = dqs + kWaves * kTile * HD + wave * (kBlk * 20);              // this wave's dS^T tile
+  constexpr int NQB = kTile / kBlk;  // query blocks of a tile
+  constexpr int CS = carry_stride(HD);
+  float* scr = reinterpret_cast<float*>(dyn + ST::lds_bytes(pl.max_depth));
+  float* dqs = scr;                                                         // [wave][kTile][HD] (no carry)
+  float* tr = scr + (kCarry ? 0 : kWaves * kTile * HD) + wave * (kBlk * 20);  // this wave's dS^T tile
+  float* cry = scr + kWaves * kBlk * 20;                 // [2][P][HG][CS] path sums (carry)
+  int* cid = reinterpret_cast<int*>(cry + 2 * P * HG * CS);  // [2][P] row of each depth; -1: from before the chunk
+  // Staged Q and dO, free once a tile's units are done, carry the dQ sums
+  // across waves: two [NQB][MT][64] f4 slots.
+  static_assert(2 * NQB * MT * 64 * 4 <= 2 * kTile * WS, "dQ exchange fits the staged tile");
   const int hh = wave / WPH;  // this wave's head of the group
   const int wl = wave % WPH;  // and its place among that head's waves
   st.prefetch(cl.t, cl.hg);
@@ -963,10 +1000,22 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int nrb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;
     const int rb0 = P / kBlk;
-    const int nu = rb0 - pb0 + nrb;  // units of a head: key blocks, prefix first
-    // This wave's dQ tile [kTile][HD] starts at zero.
+    const int npu = rb0 - pb0;       // prefix units of a head
+    const int nu = npu + nrb;        // units of a head: key blocks, prefix first
+    // Chunk of the tile and its place in it (the last chunk runs to the end).
+    const int chunk = min(cl.t / cl.K, cl.nch - 1);
+    const bool first = cl.t == chunk * cl.K;
+    const bool last = cl.t + 1 == cl.tend;
+    const int cur = cl.t & 1;  // path sums of this tile's prefix; the next tile's are in cur ^ 1
+    // This wave's dQ starts at zero: registers with the carry, else its LDS tile.
     float* mydq = dqs + wave * kTile * HD;
-    for (int x = lane; x < kTile * HD / 4; x += 64) reinterpret_cast<f4*>(mydq)[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 dqr[NQB][MT];
+#pragma unroll
+    for (int x = 0; x < NQB; ++x)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) dqr[x][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (!kCarry)
+      for (int x = lane; x < kTile * HD / 4; x += 64) reinterpret_cast<f4*>(mydq)[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int load0 = 0, load1 = 0, load2 = 0, load3 = 0;
     for (int u = 0; u < nu; ++u) {
       const int b = pb0 + u;
@@ -1044,66 +1093,213 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
           }
         // lane: dims 16j+4g.. of query row qr
+        if constexpr (kCarry) {
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          f4* dqp = reinterpret_cast<f4*>(mydq + qr * HD + kBlk * j + 4 * g);
-          f4 acc = *dqp;
+          for (int x = 0; x < NQB; ++x)
+            if (x == i) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc = mfma16(kt[j][r], dst[r], acc);
-          *dqp = acc;
+              for (int j = 0; j < MT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dqr[x][j] = mfma16(kt[j][r], dst[r], dqr[x][j]);
+            }
+        } else {
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            f4* dqp = reinterpret_cast<f4*>(mydq + qr * HD + kBlk * j + 4 * g);
+            f4 acc = *dqp;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc = mfma16(kt[j][r], dst[r], acc);
+            *dqp = acc;
+          }
         }
       }
       // Emit dims 16j+4g.. of key kslot.
+      const int hd = st.hg * HG + hh;
+      float gk[MT][4], gv[MT][4];
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          gk[j][x] = dk[j][x];
+          gv[j][x] = dv[j][x];
+        }
+      // Final dK/dV of row a at depth dep: + seeds, inverse RoPE of dK.
+      auto finish = [&](int64_t a, int dep) {
+        const int pos = rope.cos_t ? rope_pos(dep, rope.seq_len) : 0;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          const int d0 = kBlk * j + 4 * g;
+          if (acc_dk) {
+            float y[4];
+            load_vec<4>(acc_dk + a * D + hd * HD + d0, y);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) gk[j][x] += y[x];
+          }
+          if (acc_dv) {
+            float y[4];
+            load_vec<4>(acc_dv + a * D + hd * HD + d0, y);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) gv[j][x] += y[x];
+          }
+          if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk[j], rope.cos_t, rope.sin_t, pos, d0);
+          store_vec<4>(dK + a * D + hd * HD + d0, gk[j]);
+          store_vec<4>(dV + a * D + hd * HD + d0, gv[j]);
+        }
+      };
+      // A chunk partial (E or F) of depth entry d.
+      auto chunk_part = [&](float* base, int d) {
+        float* o = base + (static_cast<int64_t>(chunk) * P + d) * 2 * D + hd * HD + 4 * g;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          store_vec<4>(o + kBlk * j, gk[j]);
+          store_vec<4>(o + D + kBlk * j, gv[j]);
+        }
+      };
       if (kslot < P) {
         const int d = kslot - (P - st.A);
         if (d >= 0) {
-          const int64_t row = static_cast<int64_t>(st.poff) + d;
-          const int hd = st.hg * HG + hh;
+          if constexpr (kCarry) {
+            const int e = tb.pend[d];
+            const bool cont = !last && e > st.s + st.ntile;  // the next tile of the chunk sees it
+            const float* cp = cry + ((cur * P + d) * HG + hh) * CS + 4 * g;
+            float* np = cry + (((cur ^ 1) * P + d) * HG + hh) * CS + 4 * g;
+            const int id = first ? -1 : cid[cur * P + d];
+            if (!first) {
 #pragma unroll
-          for (int j = 0; j < MT; ++j) {
-            float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
-            float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
-            store_vec<4>(Pk + row * D + hd * HD + kBlk * j + 4 * g, a);
-            store_vec<4>(Pv + row * D + hd * HD + kBlk * j + 4 * g, v);
+              for (int j = 0; j < MT; ++j) {
+                const f4 ck = *reinterpret_cast<const f4*>(cp + kBlk * j);
+                const f4 cv = *reinterpret_cast<const f4*>(cp + HD + kBlk * j);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                  gk[j][x] = ck[x] + gk[j][x];
+                  gv[j][x] = cv[x] + gv[j][x];
+                }
+              }
+            }
+            if (cont) {
+#pragma unroll
+              for (int j = 0; j < MT; ++j) {
+                store_vec<4>(np + kBlk * j, gk[j]);
+                store_vec<4>(np + HD + kBlk * j, gv[j]);
+              }
+              if (hh == 0 && g == 0) cid[(cur ^ 1) * P + d] = id;
+            } else if (id < 0) {
+              chunk_part(Pk, d);  // E: a key from before the chunk
+            } else if (e > st.s + st.ntile) {
+              chunk_part(Pv, d);  // F: the chunk ends, the key's subtree does not
+            } else {
+              finish(id, d + 1);
+            }
+          } else {
+            const int64_t row = static_cast<int64_t>(st.poff) + d;
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              store_vec<4>(Pk + row * D + hd * HD + kBlk * j + 4 * g, gk[j]);
+              store_vec<4>(Pv + row * D + hd * HD + kBlk * j + 4 * g, gv[j]);
+            }
           }
         }
       } else {
         const int r = kslot - P;
         if (r < st.ntile) {
           const int64_t a = static_cast<int64_t>(st.s) + r;
-          const bool done = tb.tend[r] <= st.s + st.ntile;
-          const int pos = rope.cos_t ? rope_pos(tb.depth[r], rope.seq_len) : 0;
-          const int hd = st.hg * HG + hh;
+          if (tb.tend[r] <= st.s + st.ntile) {
+            finish(a, tb.depth[r]);
+          } else if constexpr (kCarry) {
+            const int d = tb.depth[r] - 1;  // the row's depth entry in the next tile's prefix
+            if (last) {
+              chunk_part(Pv, d);
+            } else {
+              float* np = cry + (((cur ^ 1) * P + d) * HG + hh) * CS + 4 * g;
 #pragma unroll
-          for (int j = 0; j < MT; ++j) {
-            const int d0 = kBlk * j + 4 * g;
-            float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
-            float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
-            if (done) {
-              if (acc_dk) {
-                float y[4];
-                load_vec<4>(acc_dk + a * D + hd * HD + d0, y);
-#pragma unroll
-                for (int x = 0; x < 4; ++x) gk[x] += y[x];
+              for (int j = 0; j < MT; ++j) {
+                store_vec<4>(np + kBlk * j, gk[j]);
+                store_vec<4>(np + HD + kBlk * j, gv[j]);
               }
-              if (acc_dv) {
-                float y[4];
-                load_vec<4>(acc_dv + a * D + hd * HD + d0, y);
-#pragma unroll
-                for (int x = 0; x < 4; ++x) gv[x] += y[x];
-              }
-              if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
+              if (hh == 0 && g == 0) cid[(cur ^ 1) * P + d] = static_cast<int>(a);
             }
-            store_vec<4>(dK + a * D + hd * HD + d0, gk);
-            store_vec<4>(dV + a * D + hd * HD + d0, gv);
+          } else {
+            // Open row: its partial over this tile, finished by the reduction.
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              store_vec<4>(dK + a * D + hd * HD + kBlk * j + 4 * g, gk[j]);
+              store_vec<4>(dV + a * D + hd * HD + kBlk * j + 4 * g, gv[j]);
+            }
           }
         }
       }
     }
-    // dQ: the sum of the waves' tiles in wave order, held in registers while
-    // the next tile is installed and stored after it: the install waits for
-    // the prefetched rows, and the memory counter retires operations in
-    // issue order, so a store issued before it would be waited for too.
+    // dQ is held in registers while the next tile is installed and stored
+    // after it: the install waits for the prefetched rows, and the memory
+    // counter retires operations in issue order, so a store issued before it
+    // would be waited for too.
+    if constexpr (kCarry) {
+      // The head's wave sums, added in the fixed order ((w0 + w1) + (w2 + w3)).
+      __syncthreads();  // every unit is done: the staged Q and dO are free
+      f4* xs = reinterpret_cast<f4*>(st.Ts);
+      auto slot = [&](int k, int x, int j) { return xs + ((k * NQB + x) * MT + j) * 64 + lane; };
+      if constexpr (WPH == 2) {
+        if (wl == 1)
+#pragma unroll
+          for (int x = 0; x < NQB; ++x)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) *slot(hh, x, j) = dqr[x][j];
+        __syncthreads();
+        if (wl == 0)
+#pragma unroll
+          for (int x = 0; x < NQB; ++x)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) dqr[x][j] += *slot(hh, x, j);
+      } else if constexpr (WPH == 4) {
+        if (wl & 1)
+#pragma unroll
+          for (int x = 0; x < NQB; ++x)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) *slot(wl >> 1, x, j) = dqr[x][j];
+        __syncthreads();
+        if ((wl & 1) == 0) {
+#pragma unroll
+          for (int x = 0; x < NQB; ++x)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              dqr[x][j] += *slot(wl >> 1, x, j);
+              if (wl == 2) *slot(1, x, j) = dqr[x][j];
+            }
+        }
+        __syncthreads();
+        if (wl == 0)
+#pragma unroll
+          for (int x = 0; x < NQB; ++x)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) dqr[x][j] += *slot(1, x, j);
+      }
+      const int64_t s0 = st.s;
+      const int nt0 = st.ntile;
+      const int col = (st.hg * HG + hh) * HD + 4 * g;
+      float qv[NQB][MT][4];
+#pragma unroll
+      for (int x = 0; x < NQB; ++x)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) qv[x][j][r] = dqr[x][j][r];
+          const int q = kBlk * x + c;
+          if (wl == 0 && rope.cos_t && q < nt0)
+            agpt_fast::rope_inverse_part<4, HD>(qv[x][j], rope.cos_t, rope.sin_t, rope_pos(tb.depth[q], rope.seq_len),
+                                                kBlk * j + 4 * g);
+        }
+      more = cl.end_tile(st);
+      if (wl == 0)
+#pragma unroll
+        for (int x = 0; x < NQB; ++x) {
+          const int q = kBlk * x + c;
+          if (q < nt0)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) store_vec<4>(dQ + (s0 + q) * D + col + kBlk * j, qv[x][j]);
+        }
+      continue;
+    }
+    // The waves' dQ tiles of each head, summed in wave order.
     __syncthreads();
     constexpr int kQuads = HG * kTile * HD / 4;  // 4 consecutive dims of a row of a head
     static_assert(kQuads % kThreads == 0, "whole dQ quads per thread");
@@ -1131,6 +1327,59 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     for (int k = 0; k < kPer; ++k)
       if (qo[k] >= 0) store_vec<4>(dQ + qo[k], qv[k]);
   } while (more);
+}
+
+// ---------------------------------------------------------------------------
+// Carry reduction: one workgroup per chunk C but the last. The keys first
+// seen in chunk C and still open at its end are the prefix entries d of the
+// next chunk's first tile with row >= the chunk's first row; each one's
+// total is F[C][d] + Σ E[C'][d] over the later chunks C' whose first row
+// lies in its subtree (those are exactly the chunks it reaches, and E[C'][d]
+// is its sum over C'), in chunk order; then seeds and inverse RoPE.
+// E, F: [n_chunks][P][2][D] (dK, dV).
+// ---------------------------------------------------------------------------
+template <int HD, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(256) void bwd_carry_kernel(PlanT pl, const float* __restrict__ E,
+                                                        const float* __restrict__ F, float* __restrict__ dK,
+                                                        float* __restrict__ dV, const float* __restrict__ acc_dk,
+                                                        const float* __restrict__ acc_dv, RopeT rope, int H) {
+  const int C = blockIdx.x;
+  const int K = pl.chunk_tiles;
+  const int64_t rows_per_chunk = static_cast<int64_t>(K) * kTile;
+  const int64_t sC = C * rows_per_chunk;
+  const int t1 = (C + 1) * K;
+  const int off = pl.pref_off[t1];
+  const int A = pl.pref_off[t1 + 1] - off;
+  const int P = prefix_cap(pl.max_depth);
+  const int D = H * HD;
+  const int Q = D / 2;  // 4-float jobs of a row: dK then dV
+  for (int j = threadIdx.x; j < A * Q; j += blockDim.x) {
+    const int d = j / Q;
+    const int q = j - d * Q;
+    const int64_t a = pl.prefix[off + d];
+    if (a < sC) continue;  // first seen before chunk C: summed by its own chunk's job
+    const int tv = q / (D / 4);
+    const int col = (q - tv * (D / 4)) * 4;
+    const int64_t ea = pl.end[a];
+    float v[4];
+    load_vec<4>(F + ((static_cast<int64_t>(C) * P + d) * 2 + tv) * D + col, v);
+    for (int c2 = C + 1; c2 < pl.n_chunks && c2 * rows_per_chunk < ea; ++c2) {
+      float y[4];
+      load_vec<4>(E + ((static_cast<int64_t>(c2) * P + d) * 2 + tv) * D + col, y);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) v[x] += y[x];
+    }
+    const float* acc = tv ? acc_dv : acc_dk;
+    if (acc) {
+      float y[4];
+      load_vec<4>(acc + a * D + col, y);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) v[x] += y[x];
+    }
+    if (tv == 0 && rope.cos_t)
+      agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, rope_pos(d + 1, rope.seq_len), col % HD);
+    store_vec<4>((tv ? dV : dK) + a * D + col, v);
+  }
 }
 
 }  // namespace agpt_blk
