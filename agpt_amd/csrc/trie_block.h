@@ -1363,9 +1363,24 @@ __global__ __launch_bounds__(256) void bwd_carry_kernel(PlanT pl, const float* _
     const int64_t ea = pl.end[a];
     float v[4];
     load_vec<4>(F + ((static_cast<int64_t>(C) * P + d) * 2 + tv) * D + col, v);
-    for (int c2 = C + 1; c2 < pl.n_chunks && c2 * rows_per_chunk < ea; ++c2) {
+    // Chunks c2 > C with c2's first row inside the subtree; eight loads in
+    // flight at a time, added in chunk order.
+    const int c_end = static_cast<int>(min(static_cast<int64_t>(pl.n_chunks), (ea + rows_per_chunk - 1) / rows_per_chunk));
+    const float* e0 = E + (static_cast<int64_t>(d) * 2 + tv) * D + col;
+    const int64_t cstride = static_cast<int64_t>(P) * 2 * D;
+    int c2 = C + 1;
+    for (; c2 + 8 <= c_end; c2 += 8) {
+      float y[8][4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) load_vec<4>(e0 + (c2 + u) * cstride, y[u]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) v[x] += y[u][x];
+    }
+    for (; c2 < c_end; ++c2) {
       float y[4];
-      load_vec<4>(E + ((static_cast<int64_t>(c2) * P + d) * 2 + tv) * D + col, y);
+      load_vec<4>(e0 + c2 * cstride, y);
 #pragma unroll
       for (int x = 0; x < 4; ++x) v[x] += y[x];
     }
