@@ -383,6 +383,22 @@ struct BStream {
         if constexpr ((kTabs & kDl) != 0) tb.dl[tid - r * HG][r] = dl_r;
       }
     }
+    // Every prefetched register counts as read here on every path (waves
+    // past the row tables, the cold path, rows past a short tile): a load
+    // left pending would make the next prefetch wait, before reusing its
+    // register, for every memory operation issued after it — the stores
+    // of the tile in between included.
+    asm volatile("" ::"v"(dep), "v"(tend_r));
+#pragma unroll
+    for (int k = 0; k < kCopyPer; ++k) asm volatile("" ::"v"(cp_id[k]));
+#pragma unroll
+    for (int k = 0; k < KV_PER; ++k) asm volatile("" ::"v"(kv[k].x));
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+      for (int k = 0; k < T_PER; ++k) asm volatile("" ::"v"(tt[i][k].x));
+    if constexpr ((kTabs & kLse) != 0) asm volatile("" ::"v"(lse_r));
+    if constexpr ((kTabs & kDl) != 0) asm volatile("" ::"v"(dl_r));
     s = n_s;
     ntile = n_ntile;
     A = n_A;
@@ -513,7 +529,11 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
     const int nqb = (st.ntile + kBlk - 1) / kBlk;
     const int pb0 = (P - st.A) / kBlk;  // first key block with prefix slots
     const int rb0 = P / kBlk;
-    for (int k = 0;; ++k) {
+    // At most NUH units per wave. The loop is unrolled: a loop that stores
+    // but does not load has the compiler drain every memory operation before
+    // it, the prefetch of the next tile included.
+#pragma unroll
+    for (int k = 0; k < NUH; ++k) {
       const int u = snake_unit(k, wave);
       if (u >= nqb * NUH) break;
       const int i = nqb - 1 - u / NUH;  // query block, longest first
