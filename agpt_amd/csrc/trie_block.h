@@ -1077,7 +1077,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
         dv[j] = dk[j];
       }
-      for (int i = i0; i < i1; ++i) {
+      // Block pair (query block i, this key block): S, P, dP, dS once; dV, dK
+      // in registers; dS^T back in dst for the dQ product (the dV, dK
+      // products sit between its LDS write and read).
+      auto pair = [&](const int i, float (&dst)[4]) {
         const int qr = kBlk * i + c;  // query row this lane supplies
         const int q0 = kBlk * i + 4 * g;
         float qa[KD], ga[KD];
@@ -1101,9 +1104,6 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         // dS^T for the dQ product: write key c's four queries, read back
         // query c's four keys (LDS operations of a wave complete in order).
         *reinterpret_cast<f4*>(tr + c * 20 + 4 * g) = f4{ds[0], ds[1], ds[2], ds[3]};
-        float dst[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[r] = tr[(4 * g + r) * 20 + c];
 #pragma unroll
         for (int j = 0; j < MT; ++j)
 #pragma unroll
@@ -1112,20 +1112,30 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
             dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
           }
-        // lane: dims 16j+4g.. of query row qr
-        if constexpr (kCarry) {
 #pragma unroll
-          for (int x = 0; x < NQB; ++x)
-            if (x == i) {
+        for (int r = 0; r < 4; ++r) dst[r] = tr[(4 * g + r) * 20 + c];
+      };
+      // lane: dims 16j+4g.. of query row kBlk * i + c
+      if constexpr (kCarry) {
+        // Unrolled over the tile's query blocks (uniform guards), so each
+        // block pair is straight-line code with its own dQ registers.
 #pragma unroll
-              for (int j = 0; j < MT; ++j)
+        for (int i = 0; i < NQB; ++i) {
+          if (i < i0 || i >= i1) continue;
+          float dst[4];
+          pair(i, dst);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dqr[x][j] = mfma16(kt[j][r], dst[r], dqr[x][j]);
-            }
-        } else {
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dqr[i][j] = mfma16(kt[j][r], dst[r], dqr[i][j]);
+        }
+      } else {
+        for (int i = i0; i < i1; ++i) {
+          float dst[4];
+          pair(i, dst);
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
-            f4* dqp = reinterpret_cast<f4*>(mydq + qr * HD + kBlk * j + 4 * g);
+            f4* dqp = reinterpret_cast<f4*>(mydq + (kBlk * i + c) * HD + kBlk * j + 4 * g);
             f4 acc = *dqp;
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc = mfma16(kt[j][r], dst[r], acc);
