@@ -570,9 +570,12 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
           float sc[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) sc[r] = live[r] ? sv[r] : -__builtin_inff();
-          const float mx = group_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-          const bool resc = mx > m[e] + kRescaleLog2;
-          if (__any(resc)) {
+          // The four-group max of a query passes m + 2^8 exactly when one of
+          // its lanes' own maxima does, so the reduction runs only then.
+          const float lmx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+          if (__any(lmx > m[e] + kRescaleLog2)) {
+            const float mx = group_max(lmx);
+            const bool resc = mx > m[e] + kRescaleLog2;
             const float a = resc ? fast_exp2(m[e] - mx) : 1.0f;
             m[e] = resc ? mx : m[e];
             l[e] *= a;
