@@ -168,6 +168,7 @@ struct BStream {
   u4 tt[NT][T_PER];
   int dep, tend_r;
   float lse_r, dl_r;
+  float dscale = 1.0f;  // δ = dO·O is stored times this (NT == 3 with kDeltaO)
   int cp_id[kCopyPer];
 
   __device__ __forceinline__ BStream(const PlanT& pl_, const Tin* K_, const Tin* V_, const Tin* T0,
@@ -333,7 +334,7 @@ struct BStream {
           // The CPH chunks of a head sit in CPH consecutive lanes.
 #pragma unroll
           for (int m = 1; m < CPH; m <<= 1) v += __shfl_xor(v, m, CPH);
-          if (j < ROWJ && r < n_ntile && (j % CPH) == 0) tb.dl[(j % CPR) / CPH][r] = v;
+          if (j < ROWJ && r < n_ntile && (j % CPH) == 0) tb.dl[(j % CPR) / CPH][r] = v * dscale;
         }
       }
     }
@@ -993,6 +994,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   int* ctr = pl.sched + 1;
   if (threadIdx.x == 0) tb.grab = atomicAdd(ctr, 1);
   ST st(pl, K, V, Q, dO, O, lse, nullptr, H, 0, dyn, tb);
+  st.dscale = scale;  // dS = P (dP - δ) scale, with V and δ taken times scale
   ChunkLoop<PlanT> cl(pl, ctr, H / HG, uniform(tb.grab));  // the constructor's barrier publishes the claim
   if (cl.t >= cl.ntiles) return;
   const int lane = threadIdx.x & 63;
@@ -1068,7 +1070,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       load_vec<KD>(st.Ks + kslot * WS + hoff + KD * g, kf);
       load_vec<KD>(st.Vs + kslot * WS + hoff + KD * g, vf);
 #pragma unroll
-      for (int j = 0; j < KD; ++j) kf[j] *= qscale;
+      for (int j = 0; j < KD; ++j) {
+        kf[j] *= qscale;
+        vf[j] *= scale;
+      }
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -1102,7 +1107,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         for (int r = 0; r < 4; ++r) {
           const bool live = in_interval(q0 + r, iv);
           p[r] = live ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
-          ds[r] = live ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+          ds[r] = p[r] * (tv[r] - dlv[r]);  // tv, dlv carry the scale; zero where p is
         }
         // dS^T for the dQ product: write key c's four queries, read back
         // query c's four keys (LDS operations of a wave complete in order).
