@@ -146,7 +146,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C4", "C5"])
     ap.add_argument("--scale", type=float, default=1.0, help="corpus scale (1 = BASELINE size)")
-    ap.add_argument("--cpu-rows", type=int, default=300_000)
+    ap.add_argument("--cpu-rows", type=int, default=1_000_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC byte-counter "
@@ -215,9 +215,12 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
-    split = "split backward" in att.describe()
+    desc = att.describe()
+    split = "split backward" in desc
+    carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce
     names = (["trie_fwd", "trie_bwd_q", "trie_bwd_kv"] if split else ["trie_fwd", "trie_bwd"])
-    k_ms = {n: [] for n in names + ["trie_bwd_chunk", "trie_bwd_reduce"]}
+    tail = ["trie_bwd_carry"] if carry else ["trie_bwd_chunk", "trie_bwd_reduce"]
+    k_ms = {n: [] for n in names + tail}
     for fe, be in evs:
         k_ms["trie_fwd"].append(hev.ms(fe[0], fe[1]))
         if split:
@@ -225,8 +228,11 @@ def main() -> int:
             k_ms["trie_bwd_kv"].append(hev.ms(be[1], be[2]))
         else:
             k_ms["trie_bwd"].append(hev.ms(be[0], be[2]))
-        k_ms["trie_bwd_chunk"].append(hev.ms(be[2], be[3]))
-        k_ms["trie_bwd_reduce"].append(hev.ms(be[3], be[4]))
+        if carry:
+            k_ms["trie_bwd_carry"].append(hev.ms(be[3], be[4]))
+        else:
+            k_ms["trie_bwd_chunk"].append(hev.ms(be[2], be[3]))
+            k_ms["trie_bwd_reduce"].append(hev.ms(be[3], be[4]))
         hev.destroy(fe + be)
     avg = {n: float(np.mean(x)) for n, x in k_ms.items()}
     log("kernel avg ms: " + ", ".join(f"{n} {m:.3f}" for n, m in avg.items()))
