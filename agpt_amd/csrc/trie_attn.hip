@@ -544,7 +544,8 @@ struct agpt_attn_s {
   // 16x16 matrix tiles (trie_block.h)
   int variant = 0;
   int hg = 1, nw = 2, qb = 1, kb = 1;
-  bool unit_all_heads = false;  // block kernels: a unit takes every head of the group
+  bool unit_all_heads = false;  // split block backward: a unit takes every head of the group
+  int fwd_uh = 2;               // block forward: heads per unit (at most the group)
   bool fused = false;           // block kernels: one-pass backward (fp32)
   int fhg = 1;                  // heads per workgroup of the one-pass backward
   bool carry = false;           // one-pass backward carries path sums (E, F replace Pk, Pv)
@@ -756,6 +757,9 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     }
     h->hg = hg;
     h->unit_all_heads = env_int("AGPT_ATTN_UH", 1) != 1;
+    // Forward units of two heads: two independent chains of matrix steps
+    // and softmax work per wave, on one mask.
+    h->fwd_uh = std::max(1, env_int("AGPT_ATTN_FUH", 2));
     tile = agpt_blk::kTile;
     h->fwd_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 1, false);
     h->bq_lds = agpt_blk::block_lds_bytes(h->max_depth, hg, hd, elem, 2, elem == 4);
@@ -1027,8 +1031,9 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (h->variant == 6)
     snprintf(buf, sizeof(buf),
              "streaming block-sparse 16x16 mfma, %s backward: tile_rows=%d tiles=%d heads_per_wg=%d "
-             "heads_per_unit=%d fwd_lds=%zu bwd_lds=%zu/%zu lds_limit=%d",
-             h->fused ? (h->carry ? "one-pass path-carry" : "one-pass") : "split", h->tile, h->n_tiles, h->hg, h->unit_all_heads ? h->hg : 1,
+             "heads_per_unit=%d/%d fwd_lds=%zu bwd_lds=%zu/%zu lds_limit=%d",
+             h->fused ? (h->carry ? "one-pass path-carry" : "one-pass") : "split", h->tile, h->n_tiles, h->hg, std::min(h->fwd_uh >= 4 ? 4 : h->fwd_uh >= 2 ? 2 : 1, h->hg),
+             h->unit_all_heads ? h->hg : 1,
              h->fwd_lds, h->fused ? h->fb_lds : h->bq_lds, h->fused ? 0 : h->kv_lds, h->max_lds);
   else if (h->variant == 5)
     snprintf(buf, sizeof(buf),
@@ -1130,11 +1135,22 @@ void with_124(int v, Fn&& fn) {  // v in {1, 2, 4}
 
 // Block kernels: heads per workgroup (1, 2, 4) and heads per unit (all or one).
 template <typename Fn>
-void with_block_heads(const agpt_attn_s* h, Fn&& fn) {
+void with_block_heads(const agpt_attn_s* h, int uh, Fn&& fn) {
   with_124(h->hg, [&](auto hgc) {
     constexpr int HG = decltype(hgc)::value;
-    if (h->unit_all_heads) fn(hgc, std::integral_constant<int, HG>{});
-    else fn(hgc, std::integral_constant<int, 1>{});
+    if constexpr (HG >= 4) {
+      if (uh >= 4) {
+        fn(hgc, std::integral_constant<int, 4>{});
+        return;
+      }
+    }
+    if constexpr (HG >= 2) {
+      if (uh >= 2) {
+        fn(hgc, std::integral_constant<int, 2>{});
+        return;
+      }
+    }
+    fn(hgc, std::integral_constant<int, 1>{});
   });
 }
 
@@ -1145,7 +1161,7 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32) {
       (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
-      with_block_heads(h, [&](auto hgc, auto uhc) {
+      with_block_heads(h, h->fwd_uh, [&](auto hgc, auto uhc) {
         constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
         auto fn = agpt_blk::fwd_kernel<HD, Tin, HG, UH, PlanDev>;
         set_lds(fn, h->fwd_lds);
@@ -1226,7 +1242,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32) {
       (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
-      with_block_heads(h, [&](auto hgc, auto uhc) {
+      with_block_heads(h, h->unit_all_heads ? h->hg : 1, [&](auto hgc, auto uhc) {
         constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
         auto fq = agpt_blk::bwd_q_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
         set_lds(fq, h->bq_lds);
