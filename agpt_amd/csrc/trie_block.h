@@ -225,32 +225,47 @@ struct BStream {
     }
     n_t = nt;
     // Unconditional loads from in-range addresses (indices past the tile are
-    // clamped; commit() ignores those values).
+    // clamped; commit() ignores those values). Each address is the tile's
+    // uniform base plus a 32-bit byte offset of the lane, so the loads take
+    // a scalar base and no 64-bit arithmetic per lane.
     const int last = n_ntile - 1;
+    const int64_t rb = static_cast<int64_t>(n_s) * D + n_hg * W;  // the tile's slice, in elements
+    auto at = [&](const Tin* base, int r, int c) {
+      const unsigned off = static_cast<unsigned>(r * D + c * EPC) * static_cast<unsigned>(sizeof(Tin));
+      return *reinterpret_cast<const u4*>(reinterpret_cast<const char*>(base + rb) + off);
+    };
 #pragma unroll
     for (int k = 0; k < KV_PER; ++k) {
-      const int j = min(tid + k * kThreads, 2 * ROWJ - 1);
-      const int ten = j / ROWJ;
-      const int r = min((j - ten * ROWJ) / CPR, last);
-      kv[k] = *reinterpret_cast<const u4*>(gsrc(ten ? V : K, n_s + r, j % CPR));
+      if constexpr (ROWJ % kThreads == 0) {
+        // Whole rounds of the workgroup per tensor: K or V is fixed per k.
+        const int ten = k * kThreads / ROWJ;  // a constant once the loop is unrolled
+        const int j = tid + k * kThreads - ten * ROWJ;
+        kv[k] = at(ten ? V : K, min(j / CPR, last), j % CPR);
+      } else {
+        const int j = min(tid + k * kThreads, 2 * ROWJ - 1);
+        const int ten = j / ROWJ;
+        const int r = min((j - ten * ROWJ) / CPR, last);
+        kv[k] = *reinterpret_cast<const u4*>(gsrc(ten ? V : K, n_s + r, j % CPR));
+      }
     }
 #pragma unroll
     for (int i = 0; i < NT; ++i)
 #pragma unroll
       for (int k = 0; k < T_PER; ++k) {
         const int j = min(tid + k * kThreads, ROWJ - 1);
-        const int r = min(j / CPR, last);
-        tt[i][k] = *reinterpret_cast<const u4*>(gsrc(TT[i], n_s + r, j % CPR));
+        tt[i][k] = at(TT[i], min(j / CPR, last), j % CPR);
       }
     const int lane = tid & 63;
-    dep = pl.depth[n_s + min(lane, last)];
-    tend_r = pl.end[n_s + min(lane, last)];
+    const unsigned lr = static_cast<unsigned>(min(lane, last)) * 4u;
+    dep = *reinterpret_cast<const int*>(reinterpret_cast<const char*>(pl.depth + n_s) + lr);
+    tend_r = *reinterpret_cast<const int*>(reinterpret_cast<const char*>(pl.end + n_s) + lr);
     if constexpr (kTabs != 0) {
       const int i = min(tid, n_ntile * HG - 1);
       const int r = i / HG;
-      const int64_t o = (static_cast<int64_t>(n_s) + r) * H + n_hg * HG + (i - r * HG);
-      if constexpr ((kTabs & kLse) != 0) lse_r = lse[o];
-      if constexpr ((kTabs & kDl) != 0) dl_r = Dl[o];
+      const unsigned o = static_cast<unsigned>(r * H + (i - r * HG)) * 4u;
+      const int64_t o0 = static_cast<int64_t>(n_s) * H + n_hg * HG;
+      if constexpr ((kTabs & kLse) != 0) lse_r = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(lse + o0) + o);
+      if constexpr ((kTabs & kDl) != 0) dl_r = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(Dl + o0) + o);
     }
 #pragma unroll
     for (int k = 0; k < kCopyPer; ++k) {
