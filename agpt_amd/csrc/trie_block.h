@@ -115,6 +115,39 @@ __device__ __forceinline__ float group_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Reductions over aligned groups of consecutive lanes with DPP lane moves
+// (VALU, no LDS round trip). quad_perm [1,0,3,2] = 0xB1 and [2,3,0,1] = 0x4E
+// swap within quads; row_ror:n = 0x120 + n rotates within a row of 16.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ int dpp_n(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xf, 0xf, false);
+}
+// Sum over each aligned group of W consecutive lanes (W = 1, 2, 4, 8, 16),
+// left in every lane of the group. The order of the additions is fixed.
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  if constexpr (W >= 2) v += dpp_f<0xB1>(v);
+  if constexpr (W >= 4) v += dpp_f<0x4E>(v);
+  if constexpr (W >= 8) {
+    // lanes 0-3 of each 8 take lanes 4-7 (row_ror:12), lanes 4-7 take 0-3 (row_ror:4)
+    const float a = dpp_f<0x12C>(v), b = dpp_f<0x124>(v);
+    v += (threadIdx.x & 4) ? b : a;
+  }
+  if constexpr (W >= 16) v += dpp_f<0x128>(v);
+  return v;
+}
+// Max over each row of 16 lanes, left in every lane of the row.
+__device__ __forceinline__ int row16_max(int v) {
+  v = max(v, dpp_n<0x121>(v));
+  v = max(v, dpp_n<0x122>(v));
+  v = max(v, dpp_n<0x124>(v));
+  return max(v, dpp_n<0x128>(v));
+}
+
 __device__ __forceinline__ bool in_interval(int q, int iv) {
   return static_cast<unsigned>(q - (iv & 0xffff)) < static_cast<unsigned>(iv >> 16);
 }
@@ -347,8 +380,7 @@ struct BStream {
           if (j < ROWJ && r < n_ntile) pdl[r * (HG * CPH) + j % CPR] = v;
         } else {
           // The CPH chunks of a head sit in CPH consecutive lanes.
-#pragma unroll
-          for (int m = 1; m < CPH; m <<= 1) v += __shfl_xor(v, m, CPH);
+          v = lane_group_sum<CPH>(v);
           if (j < ROWJ && r < n_ntile && (j % CPH) == 0) tb.dl[(j % CPR) / CPH][r] = v * dscale;
         }
       }
@@ -388,8 +420,7 @@ struct BStream {
       tb.tend[r] = tend_r;
       // Row block maxima over the 16 lanes of each block (wave 0).
       int m = live ? hi : 0;
-#pragma unroll
-      for (int sh = 1; sh < kBlk; sh <<= 1) m = max(m, __shfl_xor(m, sh, kBlk));
+      m = row16_max(m);
       if ((r & (kBlk - 1)) == 0) tb.bhi[(P + r) / kBlk] = m;
     }
     if constexpr (kTabs != 0) {
