@@ -74,7 +74,7 @@ def _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=None, acc=None, max_depth
     return res
 
 
-def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0):
+def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0, normwise=False):
     T = tr_parent.shape[0]
     D = H * hd
     Q, K, V, G = tensors(T, D, seed, sharp=sharp)
@@ -94,7 +94,7 @@ def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0
         rtol, atol = RTOL_F32, ATOL_F32
     # Sharp softmax (large scores) makes dK/dV sums of terms far larger than
     # the result; there the relative bound is taken normwise per (row, head).
-    rs = hd if (sharp > 1.0 or dtype == "bf16") else None
+    rs = hd if (sharp > 1.0 or dtype == "bf16" or normwise) else None
     assert_close(o, Oo, rtol, atol, "O", row_scale=rs)
     assert_close(lse, lse_o, rtol, atol, "lse")
     dQ, dK, dV = ORC.bwd(tr_parent, Q, K, V, W, G, H, hd, scale,
@@ -105,7 +105,7 @@ def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0
     assert_close(dv, dV, rtol, atol, "dV", row_scale=rs)
 
 
-@pytest.mark.parametrize("hd,H", [(4, 2), (8, 3), (16, 4), (16, 8), (32, 2), (64, 2)])
+@pytest.mark.parametrize("hd,H", [(4, 2), (8, 3), (16, 3), (16, 4), (16, 8), (32, 2), (64, 2)])
 def test_parity_f32(gpu, hd, H):
     tr = small_trie(n_tokens=600, depth=12, seed=hd + H)
     _check(tr.parent, H, hd, seed=hd * 10 + H)
@@ -122,6 +122,19 @@ def test_parity_rope_acc_sharp(gpu, rope, acc, sharp):
 def test_parity_bf16(gpu, hd):
     tr = small_trie(n_tokens=700, depth=14, seed=21)
     _check(tr.parent, 4, hd, seed=hd, dtype="bf16", rope=True)
+
+
+def test_long_subtrees(gpu):
+    """Two-symbol corpus: root subtrees of ~27K rows span many tile chunks,
+    so path sums cross chunk boundaries and the chunk-chain walk of the
+    reduction runs its long form.
+
+    dK/dV of shallow keys sum ~15K terms that cancel (row 12698: result
+    0.036, Σ|terms| 448), so the bound is normwise per (row, head): against a
+    float64 evaluation of that element (0.0359821) the GPU is off by 1.7e-6,
+    the float32 oracle by 1.6e-5, which an elementwise 1e-4 bound rejects."""
+    tr = small_trie(n_tokens=6000, vocab=2, depth=24, seed=7)
+    _check(tr.parent, 2, 16, seed=3, rope=True, acc=True, normwise=True)
 
 
 def test_parity_c1_sample(gpu):
