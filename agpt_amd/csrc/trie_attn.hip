@@ -773,11 +773,14 @@ void choose_variant(agpt_attn_s* h, int& tile) {
       while (fhg * 2 <= 2 && H % (fhg * 2) == 0 && fhg * hd * elem < 128) fhg *= 2;
     }
     h->fhg = fhg;
-    h->fused = elem == 4 && env_int("AGPT_ATTN_FUSED", 1) != 0 && H % h->fhg == 0 &&
+    h->fused = elem == 4 && hd <= 32 && env_int("AGPT_ATTN_FUSED", 1) != 0 && H % h->fhg == 0 &&
                (h->fhg == 1 || h->fhg == 2);
     h->fb_lds = agpt_blk::fused_lds_bytes(h->max_depth, h->fhg, hd, false);
     const int bbudget = lim - static_cast<int>(sizeof(agpt_blk::BlockTables<4>));
-    const bool ok = (hd == 16 || hd == 32) && H % hg == 0 && (hg == 1 || hg == 2 || hg == 4) &&
+    // head_dim 64 runs one head per workgroup (a 256-byte fp32 / 128-byte
+    // bf16 row segment already fills whole lines).
+    const bool ok = (hd == 16 || hd == 32 || (hd == 64 && hg == 1)) && H % hg == 0 &&
+                    (hg == 1 || hg == 2 || hg == 4) &&
                     (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(bbudget) &&
                     h->bq_lds <= static_cast<size_t>(bbudget) && h->kv_lds <= static_cast<size_t>(bbudget);
     if (h->fused && h->fb_lds > static_cast<size_t>(bbudget)) h->fused = false;
@@ -1134,6 +1137,10 @@ void with_124(int v, Fn&& fn) {  // v in {1, 2, 4}
 }
 
 // Block kernels: heads per workgroup (1, 2, 4) and heads per unit (all or one).
+// Block-kernel shapes that are built: head_dim 16 and 32 with 1, 2 or 4
+// heads per workgroup; head_dim 64 with one.
+constexpr bool block_shape_ok(int hd, int hg, int uh) { return hd <= 32 || (hg == 1 && uh == 1); }
+
 template <typename Fn>
 void with_block_heads(const agpt_attn_s* h, int uh, Fn&& fn) {
   with_124(h->hg, [&](auto hgc) {
@@ -1159,15 +1166,17 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
   if (h->variant == 6) {
-    if constexpr (HD == 16 || HD == 32) {
+    if constexpr (HD == 16 || HD == 32 || HD == 64) {
       (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
       with_block_heads(h, h->fwd_uh, [&](auto hgc, auto uhc) {
         constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
-        auto fn = agpt_blk::fwd_kernel<HD, Tin, HG, UH, PlanDev>;
-        set_lds(fn, h->fwd_lds);
-        hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds)), dim3(agpt_blk::kThreads), h->fwd_lds,
-                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
-                           static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+        if constexpr (block_shape_ok(HD, HG, UH)) {
+          auto fn = agpt_blk::fwd_kernel<HD, Tin, HG, UH, PlanDev>;
+          set_lds(fn, h->fwd_lds);
+          hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds)), dim3(agpt_blk::kThreads), h->fwd_lds,
+                             st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                             static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+        }
       });
     }
   } else if (h->variant == 5) {
@@ -1240,23 +1249,25 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   }
   if (fused_done) {
   } else if (h->variant == 6) {
-    if constexpr (HD == 16 || HD == 32) {
+    if constexpr (HD == 16 || HD == 32 || HD == 64) {
       (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
       with_block_heads(h, h->unit_all_heads ? h->hg : 1, [&](auto hgc, auto uhc) {
         constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
-        auto fq = agpt_blk::bwd_q_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
-        set_lds(fq, h->bq_lds);
-        hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds)), dim3(agpt_blk::kThreads), h->bq_lds,
-                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
-                           static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
-                           static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
-        pm.mark(1);
-        auto fk = agpt_blk::bwd_kv_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
-        set_lds(fk, h->kv_lds);
-        hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds)), dim3(agpt_blk::kThreads), h->kv_lds,
-                           st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
-                           static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv,
-                           h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+        if constexpr (block_shape_ok(HD, HG, UH)) {
+          auto fq = agpt_blk::bwd_q_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
+          set_lds(fq, h->bq_lds);
+          hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds)), dim3(agpt_blk::kThreads), h->bq_lds,
+                             st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                             static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
+                             static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
+          pm.mark(1);
+          auto fk = agpt_blk::bwd_kv_kernel<HD, Tin, HG, UH, PlanDev, RopeArgs>;
+          set_lds(fk, h->kv_lds);
+          hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds)), dim3(agpt_blk::kThreads), h->kv_lds,
+                             st, plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                             static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv,
+                             h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+        }
       });
     }
   } else if (h->variant == 5) {

@@ -107,8 +107,10 @@ def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
 CONFIGS = {
     "C1": dict(n=200_000, order=3, vocab=65, zipf=1.1, depth=32, seed=1, H=4, hd=16, dtype="f32"),
     "C2": dict(n=1_100_000, order=5, vocab=65, zipf=1.1, depth=32, seed=2, H=8, hd=16, dtype="f32"),
+    # C4 at full size is ~6e8 node-tokens (0.6 TB per bf16 [T, 512] tensor):
+    # one GPU holds the 0.02 share (~1.3e7 node-tokens, ~0.15 TB of tensors).
     "C4": dict(n=5_000_000, order=8, vocab=256, zipf=1.2, depth=128, seed=4, H=8, hd=64,
-               dtype="bf16"),
+               dtype="bf16", one_gpu_scale=0.02),
     "C5": dict(chains=512, chain_len=256, vocab=65, seed=5, H=4, hd=64, dtype="bf16"),
 }
 

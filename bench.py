@@ -145,7 +145,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C4", "C5"])
-    ap.add_argument("--scale", type=float, default=1.0, help="corpus scale (1 = BASELINE size)")
+    ap.add_argument("--scale", type=float, default=None,
+                    help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
+                         "one GPU holds)")
     ap.add_argument("--cpu-rows", type=int, default=1_000_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -175,6 +177,8 @@ def main() -> int:
     from agpt_amd.attention import TrieAttention
 
     cfg = trie_mod.CONFIGS[args.workload]
+    if args.scale is None:
+        args.scale = cfg.get("one_gpu_scale", 1.0)
     H, hd = cfg["H"], cfg["hd"]
     D = H * hd
     dtype = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16

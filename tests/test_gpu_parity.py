@@ -137,6 +137,22 @@ def test_long_subtrees(gpu):
     _check(tr.parent, 2, 16, seed=3, rope=True, acc=True, normwise=True)
 
 
+def test_parity_c4_sample(gpu):
+    """C4 shape (head_dim 64, bf16, tries to depth 128) on a reduced corpus."""
+    from agpt_amd import trie
+    tr = trie.config_trie("C4", scale=0.00004)  # 200 tokens: 17K node-tokens, depth 128
+    assert int(ORC.depths(tr.parent).max()) > 64
+    _check(tr.parent, 2, 64, seed=4, dtype="bf16", rope=True)
+
+
+def test_parity_c5_sample(gpu):
+    """C5 shape (independent 256-token chains, head_dim 64, bf16): dense
+    causal attention over prefixes far past the in-LDS copy budget."""
+    from agpt_amd import trie
+    tr = trie.config_trie("C5", scale=12 / 512)  # 12 chains of 256
+    _check(tr.parent, 2, 64, seed=5, dtype="bf16", rope=True, acc=True)
+
+
 def test_parity_c1_sample(gpu):
     """C1 shape (d_model 64, 4x16, depth 32) on a reduced corpus."""
     from agpt_amd import trie
@@ -144,7 +160,7 @@ def test_parity_c1_sample(gpu):
     _check(tr.parent, 4, 16, seed=1, rope=True)
 
 
-@pytest.mark.parametrize("hd", [8, 16])
+@pytest.mark.parametrize("hd", [8, 16, 64])
 @pytest.mark.parametrize("kind", ["single", "roots", "chain256", "tile_edge", "tile_edge1", "deep48"])
 def test_edge_shapes(gpu, kind, hd):
     if kind == "deep48":  # prefixes longer than the 32-entry in-LDS copy budget
