@@ -1,4 +1,5 @@
-"""ctypes bindings of the two native libraries (include/agpt_attn.h, include/agpt_trie.h).
+"""ctypes bindings of the two native libraries (include/agpt_attn.h and
+include/agpt_loss.h in libagpt_attn.so; include/agpt_trie.h).
 
 The attention library is the product path: if it is missing or fails to load,
 every call raises — there is no Python or CPU fallback.
@@ -69,6 +70,14 @@ ATTN_SYMBOLS = {
     "agpt_sync": (C.c_int, []),
 }
 
+# include/agpt_loss.h (same library as the attention entry points).
+LOSS_SYMBOLS = {
+    "agpt_loss_per_query": (C.c_int, [_vp] * 11 + [C.c_int, C.c_int, C.c_float, C.c_float, C.c_int,
+                                                   _vp]),
+    "agpt_loss_mass_weights": (C.c_int, [_i32p] * 4 + [C.c_int, C.c_int, C.c_int,
+                                                       C.POINTER(C.c_float)]),
+}
+
 TRIE_SYMBOLS = {
     "agpt_markov_corpus": (C.c_int, [C.c_uint64, C.c_int, C.c_int, C.c_double, C.c_double,
                                      C.c_int64, _i32p]),
@@ -101,7 +110,7 @@ def _load(name: str, symbols: dict) -> C.CDLL:
 def attn_lib() -> C.CDLL:
     global _attn
     if _attn is None:
-        _attn = _load("libagpt_attn.so", ATTN_SYMBOLS)
+        _attn = _load("libagpt_attn.so", {**ATTN_SYMBOLS, **LOSS_SYMBOLS})
     return _attn
 
 

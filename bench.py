@@ -41,6 +41,7 @@ class HipEvents:
         self.lib.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
         self.lib.hipEventSynchronize.argtypes = [C.c_void_p]
         self.lib.hipEventDestroy.argtypes = [C.c_void_p]
+        self.lib.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
 
     def create(self, n: int) -> list[int]:
         out = []
@@ -49,6 +50,9 @@ class HipEvents:
             assert self.lib.hipEventCreate(C.byref(e)) == 0
             out.append(e.value)
         return out
+
+    def record(self, e: int, stream: int) -> None:
+        assert self.lib.hipEventRecord(C.c_void_p(e), C.c_void_p(stream)) == 0
 
     def ms(self, a: int, b: int) -> float:
         assert self.lib.hipEventSynchronize(C.c_void_p(b)) == 0
@@ -127,6 +131,109 @@ def cpu_baseline(tr, q, k, v, d_o, H, hd, rows: int) -> dict:
                        f"nproc {os.cpu_count()}")}
 
 
+LOSS_METRIC = "AGPT per-query loss (softmax + targets + d_logits) queries/sec (1 GPU)"
+
+
+def loss_inputs(tr, V: int, seed: int):
+    """The radix query layout of the trie (one query per node-token, radix
+    nodes in DFS order) with its tokens as the intermediate targets, and as
+    each endpoint's next-token counts its child edges' first tokens with
+    seeded counts 1..40 (the trie builder keeps no corpus counts)."""
+    rng = np.random.default_rng(seed)
+    heads = np.flatnonzero(tr.radix_head)
+    R = heads.shape[0]
+    q2n = (np.cumsum(tr.radix_head) - 1).astype(np.int32)
+    qoff = np.append(heads, tr.n_nodes).astype(np.int32)
+    rpar = q2n[tr.parent[heads]]
+    rpar[tr.parent[heads] < 0] = -1
+    kids = np.flatnonzero(rpar >= 0)  # child radix nodes, grouped by parent (DFS order keeps them sorted)
+    order = kids[np.argsort(rpar[kids], kind="stable")]
+    cnt = np.bincount(rpar[kids], minlength=R)
+    coff = np.zeros(R + 1, np.int64)
+    np.cumsum(cnt, out=coff[1:])
+    ctok = tr.token[heads[order]].astype(np.int32) % V
+    cval = rng.integers(1, 41, ctok.shape[0]).astype(np.int32)
+    return dict(query_to_node=q2n, query_offsets=qoff, radix_ids=np.arange(R, dtype=np.int32),
+                token_ids=(tr.token % V).astype(np.int32), counts_offset=coff.astype(np.int32),
+                counts_tok=ctok, counts_val=cval)
+
+
+def bench_loss(args, tr, V: int) -> int:
+    """One step = agpt_loss_per_query over every query of the trie (T_q =
+    node-tokens) with logits [T_q, V] resident; algorithmic bytes per query:
+    logits read + d_logits write (8V) + loss write, query_to_node and the
+    next token read (12)."""
+    import torch
+    from agpt_amd import loss as L
+
+    dev = torch.device("cuda:0")
+    b = loss_inputs(tr, V, seed=77)
+    T_q = tr.n_nodes
+    idx = [torch.from_numpy(b[k]).to(dev) for k in ("query_to_node", "query_offsets", "radix_ids",
+                                                     "token_ids", "counts_offset", "counts_tok",
+                                                     "counts_val")]
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    logits = torch.randn(T_q, V, generator=g, device=dev) * 2.0
+    d_logits = torch.empty_like(logits)
+    loss_out = torch.empty(T_q, device=dev)
+    torch.cuda.synchronize()
+    log(f"loss inputs resident: T_q {T_q}, V {V}, {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
+
+    def step():
+        L.loss_per_query(logits, *idx, d_logits=d_logits, loss_out=loss_out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    hev = HipEvents()
+    evs = [hev.create(2) for _ in range(args.steps)]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    t0 = time.perf_counter()
+    for e in evs:
+        hev.record(e[0], stream)
+        step()
+        hev.record(e[1], stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    k_ms = float(np.mean([hev.ms(a, c) for a, c in evs]))
+    for e in evs:
+        hev.destroy(e)
+    per_q = 8 * V + 12
+    achieved = per_q * T_q / (k_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as ORC
+        M = min(args.cpu_rows, T_q)
+        end = int(np.searchsorted(b["query_offsets"], M, side="right")) - 1  # whole radix nodes
+        M = int(b["query_offsets"][end])
+        lg = logits[:M].cpu().numpy()
+        sub = dict(b, query_to_node=b["query_to_node"][:M], token_ids=b["token_ids"][:M])
+        t0c = time.perf_counter()
+        ORC.loss_per_query(lg, sub["query_to_node"], sub["query_offsets"], sub["radix_ids"],
+                           sub["token_ids"], sub["counts_offset"], sub["counts_tok"], sub["counts_val"])
+        dt = time.perf_counter() - t0c
+        cpu = {"value": M / dt, "unit": "queries/s", "cores": 1, "kind": "port",
+               "sample": f"first {M} queries (whole radix nodes) of the same batch, oracle "
+                         f"(C restatement of agpt_loss_per_query_kernel), 1 thread, {dt:.1f} s"}
+    out = {
+        "metric": LOSS_METRIC, "value": T_q * args.steps / elapsed, "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded Markov corpus -> radix trie queries; random logits and counts)",
+        "config": {"workload": f"{args.workload}: per-query AGPT loss over every node-token",
+                   "queries": T_q, "radix_nodes": int(b["radix_ids"].shape[0]), "vocab": V,
+                   "count_entries": int(b["counts_tok"].shape[0])},
+        "roofline": {"bound": "hbm", "kernel": "agpt_loss", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic(f"agpt_loss_{args.workload}"),
+                     "algorithmic_bytes_per_launch": per_q * T_q, "avg_launch_ms": k_ms},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def load_traffic(name: str):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
@@ -145,6 +252,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C4", "C5"])
+    ap.add_argument("--path", default="attn", choices=["attn", "loss"],
+                    help="attn: trie attention fwd+bwd (the headline); loss: per-query AGPT loss")
+    ap.add_argument("--vocab", type=int, default=65, help="loss path: vocabulary size V")
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
                          "one GPU holds)")
@@ -189,6 +299,8 @@ def main() -> int:
     T = tr.n_nodes
     log(f"trie: {T} node-tokens, {tr.n_radix} radix nodes, sum depth {tr.sum_depth}, "
         f"max depth {tr.max_depth} ({time.time() - t0:.1f}s)")
+    if args.path == "loss":
+        return bench_loss(args, tr, args.vocab)
     dev = torch.device("cuda:0")
     att = TrieAttention(H, hd, max_depth=max(tr.max_depth, 1), dtype=dtype)
     att.plan(tr.parent)

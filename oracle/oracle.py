@@ -141,3 +141,27 @@ def varlen_L_bwd(q, k, v, w, d_out, q2n, qoff, kv_offsets, kv_lengths, T_q, H, h
                               _ip(_i32(kv_offsets)), _ip(_i32(kv_lengths)), _fp(dq), _fp(dk),
                               _fp(dv), max_len, C.c_float(scale))
     return dq, dk, dv
+
+
+def loss_per_query(logits, query_to_node, query_offsets, radix_ids, token_ids, counts_offset,
+                   counts_tok, counts_val, mass_weights=None, entropy_lambda=0.0,
+                   intermediate_weight=1.0, ce_only=False):
+    """agpt_train.cu:2069-2194 restated (loss_oracle.c); returns (d_logits, loss)."""
+    lg = _f32(logits)
+    T_q, V = lg.shape
+    g = np.empty_like(lg)
+    lo = np.empty(T_q, np.float32)
+    ints = [_i32(x) for x in (query_to_node, query_offsets, radix_ids, token_ids, counts_offset,
+                              counts_tok, counts_val)]
+    lib().oracle_loss_per_query(_fp(lg), *(_ip(x) for x in ints), _fp(_f32(mass_weights)), _fp(g),
+                                _fp(lo), T_q, V, C.c_float(entropy_lambda),
+                                C.c_float(intermediate_weight), int(bool(ce_only)))
+    return g, lo
+
+
+def loss_mass_weights(radix_ids, edge_mass, edge_lens, query_offsets, T_q, mode):
+    """agpt_train.cu:4608-4637 restated (loss_oracle.c)."""
+    a = [_i32(x) for x in (radix_ids, edge_mass, edge_lens, query_offsets)]
+    out = np.empty(T_q, np.float32)
+    lib().oracle_loss_mass_weights(*(_ip(x) for x in a), len(a[0]), T_q, mode, _fp(out))
+    return out

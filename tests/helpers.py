@@ -59,3 +59,42 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
     return u.astype(np.uint32).view(np.float32)
+
+
+def loss_batch(n_nodes, V, seed, max_edge=4, max_entries=6, dup=False, empty_frac=0.1,
+               logit_scale=2.0):
+    """Seeded radix query batch for the per-query loss: n_nodes radix nodes
+    with 1..max_edge queries each, global radix ids spread over 2*n_nodes,
+    next-token counts CSR by global id (distinct tokens unless dup; a share
+    of endpoints without counts), random targets and logits.
+    Returns a dict of numpy arrays keyed like agpt_loss_per_query's arguments."""
+    rng = np.random.default_rng(seed)
+    edge = rng.integers(1, max_edge + 1, n_nodes)
+    off = np.zeros(n_nodes + 1, np.int64)
+    np.cumsum(edge, out=off[1:])
+    T_q = int(off[-1])
+    q2n = np.repeat(np.arange(n_nodes, dtype=np.int32), edge)
+    R = 2 * n_nodes + 1
+    radix_ids = rng.permutation(R)[:n_nodes].astype(np.int32)
+    ne = rng.integers(1, max_entries + 1, R)
+    ne[rng.random(R) < empty_frac] = 0
+    ne = np.minimum(ne, V)
+    coff = np.zeros(R + 1, np.int64)
+    np.cumsum(ne, out=coff[1:])
+    n_ent = int(coff[-1])
+    if dup:
+        ctok = rng.integers(0, V, n_ent)
+    else:  # distinct per node: base_r + j (mod V) with a random stride coprime to V
+        j = np.arange(n_ent) - np.repeat(coff[:-1], ne)
+        base = np.repeat(rng.integers(0, V, R), ne)
+        strides = [s for s in range(1, V + 1) if math.gcd(s, V) == 1]
+        step = np.repeat(rng.choice(strides, R), ne)
+        ctok = (base + j * step) % V
+    ctok = ctok.astype(np.int32)
+    cval = rng.integers(1, 40, n_ent).astype(np.int32)
+    return dict(
+        logits=(rng.standard_normal((T_q, V)) * logit_scale).astype(np.float32),
+        query_to_node=q2n, query_offsets=off.astype(np.int32), radix_ids=radix_ids,
+        token_ids=rng.integers(0, V, T_q).astype(np.int32), counts_offset=coff.astype(np.int32),
+        counts_tok=ctok, counts_val=cval,
+        edge_mass=rng.integers(1, 1000, R).astype(np.int32), edge_len_by_id=np.zeros(R, np.int32))

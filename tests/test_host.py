@@ -21,15 +21,16 @@ def _declared(header: str) -> list[str]:
     return sorted(set(re.findall(r"\b(agpt_[A-Za-z0-9_]+)\s*\(", text)))
 
 
-@pytest.mark.parametrize("header,loader", [("agpt_attn.h", _native.attn_lib),
-                                           ("agpt_trie.h", _native.trie_lib)])
-def test_abi_exports_every_declared_symbol(header, loader):
+@pytest.mark.parametrize("header,loader,table,n_min", [
+    ("agpt_attn.h", _native.attn_lib, _native.ATTN_SYMBOLS, 8),
+    ("agpt_loss.h", _native.attn_lib, _native.LOSS_SYMBOLS, 2),
+    ("agpt_trie.h", _native.trie_lib, _native.TRIE_SYMBOLS, 8)])
+def test_abi_exports_every_declared_symbol(header, loader, table, n_min):
     lib = loader()
     names = _declared(header)
-    assert len(names) >= 8
+    assert len(names) >= n_min
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    table = _native.ATTN_SYMBOLS if header == "agpt_attn.h" else _native.TRIE_SYMBOLS
     assert set(table) == set(names)  # the ctypes table binds exactly the header
 
 
