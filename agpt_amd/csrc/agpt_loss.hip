@@ -234,14 +234,21 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(
       mwv = mass != nullptr ? mass[q] : 1.0f;
     }
   };
+  int ne = 0, rid = 0;  // second-level tables of this thread's row: node end, radix id
+  auto fetch2 = [&](int64_t r) {
+    if (static_cast<int64_t>(threadIdx.x) < min(static_cast<int64_t>(RB), T_q - r)) {
+      ne = qoff[ni + 1];
+      rid = radix_ids[ni];
+    }
+  };
   fetch(r0);
+  fetch2(r0);
   for (;;) {
     const int n = static_cast<int>(min(static_cast<int64_t>(RB), T_q - r0));
     if (static_cast<int>(threadIdx.x) < n) {
       tab.tgt[threadIdx.x] = tg;
       tab.mw[threadIdx.x] = mwv;
-      tab.end[threadIdx.x] = qoff[ni + 1];
-      const int rid = radix_ids[ni];
+      tab.end[threadIdx.x] = ne;
       tab.cs[threadIdx.x] = coff[rid];
       tab.ce[threadIdx.x] = coff[rid + 1];
     }
@@ -337,6 +344,7 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(
       }
       if (c == 0) loss_out[q] = loss;
     }
+    if (next < T_q) fetch2(next);  // its first level arrived during the rows above
     __syncthreads();
     store_run(d_logits, buf, r0 * V, (r0 + n) * V);
     if (next >= T_q) break;
