@@ -95,6 +95,73 @@ __device__ __forceinline__ f4 mfma16(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// One lane group's KD consecutive dims of a row (dims KD*g ..), as an
+// operand of the first products (S = K·Qᵀ, dO·Vᵀ), whose inputs are the
+// caller's tensors. fp32: KD floats, one 4-deep step per dim. bf16: the raw
+// halves on the bf16 matrix instructions (one 16-deep step for KD = 4, one
+// 32-deep step per 8 dims): lane group g supplies the same dims of both
+// operands, and products of bf16 values are exact in fp32, so the scores
+// match the 4-deep form up to the order of the sum. The fp32 form scales the
+// held operand once (kPre); the bf16 form scales the scores.
+template <typename Tin, int KD>
+struct Slice;
+template <int KD>
+struct Slice<float, KD> {
+  static constexpr bool kPre = true;
+  float v[KD];
+  __device__ __forceinline__ void load(const float* p) { load_vec<KD>(p, v); }
+  __device__ __forceinline__ void scale(float f) {
+#pragma unroll
+    for (int j = 0; j < KD; ++j) v[j] *= f;
+  }
+};
+template <int KD>
+struct Slice<bf16_t, KD> {
+  static_assert(KD == 4 || KD % 8 == 0, "bf16 slices of 4 or a multiple of 8 dims");
+  static constexpr bool kPre = false;
+  uint32_t w[KD / 2];
+  __device__ __forceinline__ void load(const bf16_t* p) {
+    if constexpr (KD == 4) {
+      const uint2 x = *reinterpret_cast<const uint2*>(p);
+      w[0] = x.x;
+      w[1] = x.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < KD / 8; ++i) {
+        const uint4 x = *reinterpret_cast<const uint4*>(p + 8 * i);
+        w[4 * i] = x.x;
+        w[4 * i + 1] = x.y;
+        w[4 * i + 2] = x.z;
+        w[4 * i + 3] = x.w;
+      }
+    }
+  }
+  __device__ __forceinline__ void scale(float) {}
+};
+
+template <int KD>
+__device__ __forceinline__ f4 slice_dot(const Slice<float, KD>& a, const Slice<float, KD>& b, f4 acc) {
+#pragma unroll
+  for (int j = 0; j < KD; ++j) acc = mfma16(a.v[j], b.v[j], acc);
+  return acc;
+}
+template <int KD>
+__device__ __forceinline__ f4 slice_dot(const Slice<bf16_t, KD>& a, const Slice<bf16_t, KD>& b, f4 acc) {
+  typedef __attribute__((ext_vector_type(4))) short s4;
+  typedef __attribute__((ext_vector_type(8))) __bf16 b8;
+  if constexpr (KD == 4) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, uint2{a.w[0], a.w[1]}),
+                                                      __builtin_bit_cast(s4, uint2{b.w[0], b.w[1]}), acc, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < KD / 8; ++i)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(b8, uint4{a.w[4 * i], a.w[4 * i + 1], a.w[4 * i + 2], a.w[4 * i + 3]}),
+          __builtin_bit_cast(b8, uint4{b.w[4 * i], b.w[4 * i + 1], b.w[4 * i + 2], b.w[4 * i + 3]}), acc, 0, 0, 0);
+    return acc;
+  }
+}
+
 // Reductions over the four lane groups g (lanes c, c+16, c+32, c+48): each
 // swap leaves a lane's own value and its partner's (lane ^ 16, lane ^ 32)
 // in the two results.
@@ -586,13 +653,13 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
       const int i = nqb - 1 - u / NUH;  // query block, longest first
       const int h0 = (u % NUH) * UH;    // first head of the unit (in the group)
       const int q = kBlk * i + c;
-      float qf[UH][KD], m[UH], l[UH];
+      Slice<Tin, KD> qf[UH];
+      float m[UH], l[UH];
       f4 o[UH][MT];
 #pragma unroll
       for (int e = 0; e < UH; ++e) {
-        load_vec<KD>(st.Ts + q * WS + (h0 + e) * HD + KD * g, qf[e]);
-#pragma unroll
-        for (int j = 0; j < KD; ++j) qf[e][j] *= qscale;
+        qf[e].load(st.Ts + q * WS + (h0 + e) * HD + KD * g);
+        qf[e].scale(qscale);
         m[e] = -__builtin_inff();
         l[e] = 0.0f;
 #pragma unroll
@@ -609,11 +676,10 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
 #pragma unroll
         for (int e = 0; e < UH; ++e) {
           const int hoff = (h0 + e) * HD;
-          float kf[KD];
-          load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
-          f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int j = 0; j < KD; ++j) sv = mfma16(kf[j], qf[e][j], sv);  // key k0+4g+r, query q
+          Slice<Tin, KD> kf;
+          kf.load(st.Ks + (k0 + c) * WS + hoff + KD * g);
+          f4 sv = slice_dot(kf, qf[e], f4{0.0f, 0.0f, 0.0f, 0.0f});  // key k0+4g+r, query q
+          if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
           float sc[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) sc[r] = live[r] ? sv[r] : -__builtin_inff();
@@ -707,14 +773,14 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       const int i = nqb - 1 - u / NUH;
       const int h0 = (u % NUH) * UH;
       const int q = kBlk * i + c;
-      float qf[UH][KD], gf[UH][KD], l2[UH], dl[UH];
+      Slice<Tin, KD> qf[UH], gf[UH];
+      float l2[UH], dl[UH];
       f4 dq[UH][MT];
 #pragma unroll
       for (int e = 0; e < UH; ++e) {
-        load_vec<KD>(Qs + q * WS + (h0 + e) * HD + KD * g, qf[e]);
-        load_vec<KD>(Gs + q * WS + (h0 + e) * HD + KD * g, gf[e]);
-#pragma unroll
-        for (int j = 0; j < KD; ++j) qf[e][j] *= qscale;
+        qf[e].load(Qs + q * WS + (h0 + e) * HD + KD * g);
+        gf[e].load(Gs + q * WS + (h0 + e) * HD + KD * g);
+        qf[e].scale(qscale);
         l2[e] = tb.l2[h0 + e][q];
 #pragma unroll
         for (int j = 0; j < MT; ++j) dq[e][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -723,16 +789,12 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       // k0+4g+r against query q.
       auto scores = [&](int e, int k0, f4& sv, f4& tv) {
         const int hoff = (h0 + e) * HD;
-        float kf[KD], vf[KD];
-        load_vec<KD>(st.Ks + (k0 + c) * WS + hoff + KD * g, kf);
-        load_vec<KD>(st.Vs + (k0 + c) * WS + hoff + KD * g, vf);
-        sv = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        tv = sv;
-#pragma unroll
-        for (int j = 0; j < KD; ++j) {
-          sv = mfma16(kf[j], qf[e][j], sv);
-          tv = mfma16(vf[j], gf[e][j], tv);
-        }
+        Slice<Tin, KD> kf, vf;
+        kf.load(st.Ks + (k0 + c) * WS + hoff + KD * g);
+        vf.load(st.Vs + (k0 + c) * WS + hoff + KD * g);
+        sv = slice_dot(kf, qf[e], f4{0.0f, 0.0f, 0.0f, 0.0f});
+        tv = slice_dot(vf, gf[e], f4{0.0f, 0.0f, 0.0f, 0.0f});
+        if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
       };
       auto mask = [&](int k0, bool (&live)[4]) {
         const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
@@ -857,14 +919,13 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
       const int b = pb0 + u / NUH;
       const int h0 = (u % NUH) * UH;
       const int kslot = kBlk * b + c;  // this lane's key
-      float kf[UH][KD], vf[UH][KD];
+      Slice<Tin, KD> kf[UH], vf[UH];
       f4 dk[UH][MT], dv[UH][MT];
 #pragma unroll
       for (int e = 0; e < UH; ++e) {
-        load_vec<KD>(st.Ks + kslot * WS + (h0 + e) * HD + KD * g, kf[e]);
-        load_vec<KD>(st.Vs + kslot * WS + (h0 + e) * HD + KD * g, vf[e]);
-#pragma unroll
-        for (int j = 0; j < KD; ++j) kf[e][j] *= qscale;
+        kf[e].load(st.Ks + kslot * WS + (h0 + e) * HD + KD * g);
+        vf[e].load(st.Vs + kslot * WS + (h0 + e) * HD + KD * g);
+        kf[e].scale(qscale);
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
           dk[e][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -883,15 +944,12 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 #pragma unroll
         for (int e = 0; e < UH; ++e) {
           const int hoff = (h0 + e) * HD;
-          float qa[KD], ga[KD];
-          load_vec<KD>(Qs + qr * WS + hoff + KD * g, qa);
-          load_vec<KD>(Gs + qr * WS + hoff + KD * g, ga);
-          f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f}, tv = sv;
-#pragma unroll
-          for (int j = 0; j < KD; ++j) {
-            sv = mfma16(qa[j], kf[e][j], sv);  // sv[r]: query q0+r against key kslot
-            tv = mfma16(ga[j], vf[e][j], tv);
-          }
+          Slice<Tin, KD> qa, ga;
+          qa.load(Qs + qr * WS + hoff + KD * g);
+          ga.load(Gs + qr * WS + hoff + KD * g);
+          f4 sv = slice_dot(qa, kf[e], f4{0.0f, 0.0f, 0.0f, 0.0f});  // sv[r]: query q0+r against key kslot
+          const f4 tv = slice_dot(ga, vf[e], f4{0.0f, 0.0f, 0.0f, 0.0f});
+          if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
           const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[h0 + e][q0]);
           const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[h0 + e][q0]);
           float p[4], ds[4];
