@@ -701,11 +701,31 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
             p[r] = fast_exp2(sc[r] - m[e]);  // masked: exp2(-inf) = 0
             l[e] += p[r];
           }
+          if constexpr (sizeof(Tin) == 2) {
+            // bf16 inputs: P rounded to bf16 (O is returned in bf16) and one
+            // 16-deep bf16 step per output tile; lane (g, c) supplies
+            // V[keys 4g..4g+3][dim c] and its own P[query c][keys 4g..4g+3].
+            typedef __attribute__((ext_vector_type(2))) float f2;
+            typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+            typedef __attribute__((ext_vector_type(4))) short s4;
+            const uint32_t pw0 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[0], p[1]}, b2));
+            const uint32_t pw1 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[2], p[3]}, b2));
+            const uint16_t* vb = reinterpret_cast<const uint16_t*>(st.Vs) + (k0 + 4 * g) * WS + hoff + c;
 #pragma unroll
-          for (int j = 0; j < MT; ++j)
+            for (int j = 0; j < MT; ++j) {
+              const uint32_t a0 = vb[kBlk * j] | (static_cast<uint32_t>(vb[kBlk * j + WS]) << 16);
+              const uint32_t a1 = vb[kBlk * j + 2 * WS] | (static_cast<uint32_t>(vb[kBlk * j + 3 * WS]) << 16);
+              o[e][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, uint2{a0, a1}),
+                                                                   __builtin_bit_cast(s4, uint2{pw0, pw1}), o[e][j],
+                                                                   0, 0, 0);
+            }
+          } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              o[e][j] = mfma16(ld1(st.Vs + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), p[r], o[e][j]);
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                o[e][j] = mfma16(ld1(st.Vs + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), p[r], o[e][j]);
+          }
         }
       }
       if (q < st.ntile) {
