@@ -162,6 +162,25 @@ __device__ __forceinline__ f4 slice_dot(const Slice<bf16_t, KD>& a, const Slice<
   }
 }
 
+// Second products with bf16 inputs, one 16-deep bf16 step: lane (g, c)
+// supplies column c of rows 4g .. 4g+3 of a bf16 LDS tile (`col` points at
+// row 4g, column c; rows WS apart) and its own four fp32 weights rounded to
+// bf16 (pack_bf16), i.e. A[c][4g+i] and B[4g+i][c].
+typedef __attribute__((ext_vector_type(4))) short bf16x4_bits;
+__device__ __forceinline__ uint2 pack_bf16(const float (&w)[4]) {
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+  return uint2{__builtin_bit_cast(uint32_t, __builtin_convertvector(f2{w[0], w[1]}, b2)),
+               __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{w[2], w[3]}, b2))};
+}
+__device__ __forceinline__ f4 mfma_rows_bf16(const bf16_t* col, int WS, uint2 wb, f4 acc) {
+  const uint16_t* v = reinterpret_cast<const uint16_t*>(col);
+  const uint32_t a0 = v[0] | (static_cast<uint32_t>(v[WS]) << 16);
+  const uint32_t a1 = v[2 * WS] | (static_cast<uint32_t>(v[3 * WS]) << 16);
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_bits, uint2{a0, a1}),
+                                                    __builtin_bit_cast(bf16x4_bits, wb), acc, 0, 0, 0);
+}
+
 // Reductions over the four lane groups g (lanes c, c+16, c+32, c+48): each
 // swap leaves a lane's own value and its partner's (lane ^ 16, lane ^ 32)
 // in the two results.
@@ -702,23 +721,13 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
             l[e] += p[r];
           }
           if constexpr (sizeof(Tin) == 2) {
-            // bf16 inputs: P rounded to bf16 (O is returned in bf16) and one
-            // 16-deep bf16 step per output tile; lane (g, c) supplies
-            // V[keys 4g..4g+3][dim c] and its own P[query c][keys 4g..4g+3].
-            typedef __attribute__((ext_vector_type(2))) float f2;
-            typedef __attribute__((ext_vector_type(2))) __bf16 b2;
-            typedef __attribute__((ext_vector_type(4))) short s4;
-            const uint32_t pw0 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[0], p[1]}, b2));
-            const uint32_t pw1 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{p[2], p[3]}, b2));
-            const uint16_t* vb = reinterpret_cast<const uint16_t*>(st.Vs) + (k0 + 4 * g) * WS + hoff + c;
+            // bf16 inputs: P rounded to bf16 (O is returned in bf16), one
+            // 16-deep step per output tile: V[keys 4g..4g+3][dim c] against
+            // this lane's P[query c][keys 4g..4g+3].
+            const uint2 pw = pack_bf16(p);
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {
-              const uint32_t a0 = vb[kBlk * j] | (static_cast<uint32_t>(vb[kBlk * j + WS]) << 16);
-              const uint32_t a1 = vb[kBlk * j + 2 * WS] | (static_cast<uint32_t>(vb[kBlk * j + 3 * WS]) << 16);
-              o[e][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, uint2{a0, a1}),
-                                                                   __builtin_bit_cast(s4, uint2{pw0, pw1}), o[e][j],
-                                                                   0, 0, 0);
-            }
+            for (int j = 0; j < MT; ++j)
+              o[e][j] = mfma_rows_bf16(st.Vs + (k0 + 4 * g) * WS + hoff + kBlk * j + c, WS, pw, o[e][j]);
           } else {
 #pragma unroll
             for (int j = 0; j < MT; ++j)
@@ -865,11 +874,18 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           for (int r = 0; r < 4; ++r)
             ds[r] = live[r] ? fast_exp2(sv[r] - l2[e]) * (tv[r] - dl[e]) * scale : 0.0f;
           const int hoff = (h0 + e) * HD;
+          if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per tile
+            const uint2 dw = pack_bf16(ds);
 #pragma unroll
-          for (int j = 0; j < MT; ++j)
+            for (int j = 0; j < MT; ++j)
+              dq[e][j] = mfma_rows_bf16(st.Ks + (k0 + 4 * g) * WS + hoff + kBlk * j + c, WS, dw, dq[e][j]);
+          } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              dq[e][j] = mfma16(ld1(st.Ks + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), ds[r], dq[e][j]);
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                dq[e][j] = mfma16(ld1(st.Ks + (k0 + 4 * g + r) * WS + hoff + kBlk * j + c), ds[r], dq[e][j]);
+          }
         }
       }
       if (q < st.ntile) {
@@ -978,14 +994,24 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
             p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
             ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
           }
+          if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
+            const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
 #pragma unroll
-          for (int j = 0; j < MT; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = (q0 + r) * WS + hoff + kBlk * j + c;
-              dv[e][j] = mfma16(ld1(Gs + row), p[r], dv[e][j]);
-              dk[e][j] = mfma16(ld1(Qs + row), ds[r], dk[e][j]);
+            for (int j = 0; j < MT; ++j) {
+              const int col = q0 * WS + hoff + kBlk * j + c;
+              dv[e][j] = mfma_rows_bf16(Gs + col, WS, pw, dv[e][j]);
+              dk[e][j] = mfma_rows_bf16(Qs + col, WS, dw, dk[e][j]);
             }
+          } else {
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int row = (q0 + r) * WS + hoff + kBlk * j + c;
+                dv[e][j] = mfma16(ld1(Gs + row), p[r], dv[e][j]);
+                dk[e][j] = mfma16(ld1(Qs + row), ds[r], dk[e][j]);
+              }
+          }
         }
       }
       // Emit dims 16j+4g.. of key kslot.
