@@ -137,6 +137,13 @@ def test_long_subtrees(gpu):
     _check(tr.parent, 2, 16, seed=3, rope=True, acc=True, normwise=True)
 
 
+def test_long_subtrees_bf16(gpu):
+    """bf16 at head_dim 64 on the two-symbol trie: keys near the root sum
+    dK/dV over ~20K query rows whose P and dS go through bf16 products."""
+    tr = small_trie(n_tokens=4000, vocab=2, depth=20, seed=8)
+    _check(tr.parent, 2, 64, seed=13, dtype="bf16", rope=True, acc=True)
+
+
 def test_parity_c4_sample(gpu):
     """C4 shape (head_dim 64, bf16, tries to depth 128) on a reduced corpus."""
     from agpt_amd import trie
