@@ -1,5 +1,6 @@
-"""ctypes bindings of the two native libraries (include/agpt_attn.h and
-include/agpt_loss.h in libagpt_attn.so; include/agpt_trie.h).
+"""ctypes bindings of the two native libraries (include/agpt_attn.h,
+include/agpt_loss.h and include/agpt_block.h in libagpt_attn.so;
+include/agpt_trie.h in libagpt_trie.so).
 
 The attention library is the product path: if it is missing or fails to load,
 every call raises — there is no Python or CPU fallback.
@@ -78,6 +79,12 @@ LOSS_SYMBOLS = {
                                                        C.POINTER(C.c_float)]),
 }
 
+# include/agpt_block.h (same library as the attention entry points).
+BLOCK_SYMBOLS = {
+    "agpt_bias_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_int, C.c_int, _vp]),
+    "agpt_rmsprop": (C.c_int, [_vp, _vp, _vp, C.c_float, C.c_float, C.c_float, C.c_int64, _vp]),
+}
+
 TRIE_SYMBOLS = {
     "agpt_markov_corpus": (C.c_int, [C.c_uint64, C.c_int, C.c_int, C.c_double, C.c_double,
                                      C.c_int64, _i32p]),
@@ -87,6 +94,7 @@ TRIE_SYMBOLS = {
     "agpt_trie_stats": (C.c_int, [_vp, _i64p, _i64p, _i64p, _i32p, _i64p, _i64p]),
     "agpt_trie_export": (C.c_int, [_vp, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]),
     "agpt_trie_export_radix": (C.c_int, [_vp, _i32p, _i32p]),
+    "agpt_trie_next_counts": (C.c_int, [_vp, _i32p, _i64p, _i32p, _i32p, _i32p]),
     "agpt_trie_free": (None, [_vp]),
 }
 
@@ -110,7 +118,7 @@ def _load(name: str, symbols: dict) -> C.CDLL:
 def attn_lib() -> C.CDLL:
     global _attn
     if _attn is None:
-        _attn = _load("libagpt_attn.so", {**ATTN_SYMBOLS, **LOSS_SYMBOLS})
+        _attn = _load("libagpt_attn.so", {**ATTN_SYMBOLS, **LOSS_SYMBOLS, **BLOCK_SYMBOLS})
     return _attn
 
 

@@ -1,0 +1,45 @@
+"""Kernels around the trie-attention path in a training step
+(include/agpt_block.h): the projection epilogue (bias + RoPE, in place) and
+the RMSProp update. Torch CUDA tensors, current stream; no CPU fallback."""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import _native
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(t) -> C.c_void_p:
+    import torch
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def bias_rope_(x, bias=None, positions=None, cos_t=None, sin_t=None, n_heads: int = 1):
+    """In place on x [T, D] fp32: x += bias, then (cos_t given) RoPE of each
+    head at row position positions[t] (int32 [T]). Returns x."""
+    if not x.is_cuda or not x.is_contiguous() or x.dim() != 2:
+        raise ValueError("x must be a contiguous CUDA [T, D] tensor")
+    T, D = x.shape
+    if D % n_heads:
+        raise ValueError("D must be a multiple of n_heads")
+    seq = 0 if cos_t is None else cos_t.shape[0]
+    _native.check(_native.attn_lib().agpt_bias_rope(
+        _ptr(x), _ptr(bias), _ptr(positions), _ptr(cos_t), _ptr(sin_t), seq, T, n_heads, D // n_heads,
+        _stream(x)))
+    return x
+
+
+def rmsprop_(params, grads, sq_avg, lr: float, beta: float, eps: float = 1e-8):
+    """In place: sq_avg = beta sq_avg + (1-beta) g^2; params -= lr g / (sqrt(sq_avg) + eps)."""
+    for t in (params, grads, sq_avg):
+        if not t.is_cuda or not t.is_contiguous():
+            raise ValueError("params, grads and sq_avg must be contiguous CUDA tensors")
+    n = params.numel()
+    if grads.numel() != n or sq_avg.numel() != n:
+        raise ValueError("params, grads and sq_avg must have the same size")
+    _native.check(_native.attn_lib().agpt_rmsprop(
+        _ptr(params), _ptr(grads), _ptr(sq_avg), C.c_float(lr), C.c_float(beta), C.c_float(eps), n,
+        _stream(params)))

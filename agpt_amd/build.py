@@ -42,7 +42,7 @@ HIP_FLAGS = [
     "-Wno-unused-result",
 ]
 
-HIP_SOURCES = ["trie_attn.hip", "varlen_attn.hip", "agpt_loss.hip"]
+HIP_SOURCES = ["trie_attn.hip", "varlen_attn.hip", "agpt_loss.hip", "agpt_block.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -40,6 +40,10 @@ inline double std_normal(uint64_t key) {  // Box-Muller on two hashed uniforms
 
 struct Trie {
   std::vector<int32_t> parent, depth, token, end, radix_head, partition;
+  // Corpus observations (trie_corpus.cr:210-219): visits[n] = starts whose
+  // path passes n; a visit that ends at n (depth limit or corpus end) still
+  // observes the next token, kept in (end_node, end_tok) pairs.
+  std::vector<int32_t> visits, end_node, end_tok;
   int64_t n_radix = 0, sum_depth = 0, n_root_children = 0, n_parts = 0;
   int32_t max_depth = 0;
 };
@@ -191,7 +195,13 @@ extern "C" int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
       t.parent.push_back(stack[d - 1]);
       t.depth.push_back(static_cast<int32_t>(d));
       t.token.push_back(tokens[s + d - 1]);
+      t.visits.push_back(0);
       stack[d] = id;
+    }
+    for (int64_t d = 1; d <= len; ++d) ++t.visits[stack[d]];
+    if (len > 0) {  // the last step observes tokens[s + len] (index < total_starts)
+      t.end_node.push_back(stack[len]);
+      t.end_tok.push_back(tokens[s + len]);
     }
     prev = s;
   }
@@ -267,6 +277,51 @@ extern "C" int agpt_trie_export_radix(agpt_trie_handle h, int32_t* radix_parent,
     radix_of[i] = r;
     if (edge_len) edge_len[r]++;
   }
+  return 0;
+}
+
+extern "C" int agpt_trie_next_counts(agpt_trie_handle h, int32_t* visits, int64_t* n_entries,
+                                     int32_t* offsets, int32_t* tok, int32_t* val) {
+  if (!h || !n_entries) return 1;
+  const Trie& t = h->t;
+  const int64_t n = static_cast<int64_t>(t.parent.size());
+  if (t.visits.size() != static_cast<size_t>(n)) return 2;  // a chain trie has no corpus
+  if (visits) std::memcpy(visits, t.visits.data(), n * sizeof(int32_t));
+  // Per node: children (DFS order = ascending token) with their visits, then
+  // the ending observations merged by token, all in ascending token order.
+  std::vector<int32_t> end_first(n, -1), end_next(t.end_node.size(), -1);
+  for (int64_t i = static_cast<int64_t>(t.end_node.size()) - 1; i >= 0; --i) {
+    end_next[i] = end_first[t.end_node[i]];
+    end_first[t.end_node[i]] = static_cast<int32_t>(i);
+  }
+  std::vector<int32_t> first_child(n, -1), next_sib(n, -1);
+  for (int64_t i = n - 1; i >= 0; --i) {
+    const int32_t p = t.parent[i];
+    if (p >= 0) {
+      next_sib[i] = first_child[p];
+      first_child[p] = static_cast<int32_t>(i);
+    }
+  }
+  int64_t k = 0;
+  std::vector<std::pair<int32_t, int32_t>> hist;
+  for (int64_t i = 0; i < n; ++i) {
+    if (offsets) offsets[i] = static_cast<int32_t>(k);
+    hist.clear();
+    for (int32_t c = first_child[i]; c >= 0; c = next_sib[c]) hist.emplace_back(t.token[c], t.visits[c]);
+    for (int32_t e = end_first[i]; e >= 0; e = end_next[e]) hist.emplace_back(t.end_tok[e], 1);
+    std::sort(hist.begin(), hist.end());
+    for (size_t j = 0; j < hist.size(); ++j) {
+      if (j > 0 && hist[j].first == hist[j - 1].first) {  // same token: merge into the last entry
+        if (val) val[k - 1] += hist[j].second;
+        continue;
+      }
+      if (tok) tok[k] = hist[j].first;
+      if (val) val[k] = hist[j].second;
+      ++k;
+    }
+  }
+  if (offsets) offsets[n] = static_cast<int32_t>(k);
+  *n_entries = k;
   return 0;
 }
 

@@ -1,0 +1,248 @@
+"""µGPT-style transformer over one trie batch: the training step of config C3
+around the trie-attention path (the forward of agpt_train.cu:4640-4830 and
+its backward, one subtree batch).
+
+Per layer: x1 = x + Wo·attn(rope(Wq·n1(x) + bq), rope(Wk·n1(x) + bk),
+Wv·n1(x) + bv) + bo; x = x1 + W2·relu(W1·n2(x1) + b1) + b2. Then n_f, the
+output projection, the per-query AGPT loss (sum over queries), and an RMSProp
+update of every parameter (one flat fp32 buffer, as the reference's
+d_weights). X = tok_emb[token]; positions enter through RoPE at depth - 1.
+
+Native (libagpt_attn.so): trie attention fwd/bwd, the bias + RoPE epilogue,
+the loss and RMSProp. The plain GEMMs are torch's (hipBLASLt), the norms and
+ReLU torch's elementwise kernels; torch autograd strings them together.
+`norm="rms"` (BASELINE.json's C3 text) or `"layer"` (the reference code's
+LayerNorm, agpt_train.cu:4671). Norm eps is 1e-5: µGPT's is not in the
+reference (parity unpinned).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import block, loss as L
+from .attention import TrieAttention, rope_tables
+
+
+@dataclass
+class ModelConfig:
+    vocab: int = 65
+    d_model: int = 128
+    n_heads: int = 8
+    n_layers: int = 4
+    d_ff: int = 512
+    max_depth: int = 32
+    norm: str = "rms"
+    eps: float = 1e-5
+
+
+def param_shapes(cfg: ModelConfig) -> list[tuple[str, tuple[int, ...]]]:
+    """Names and shapes of the flat parameter buffer, in order."""
+    D, Fd, V = cfg.d_model, cfg.d_ff, cfg.vocab
+    out = [("tok_emb", (V, D))]
+    for l in range(cfg.n_layers):
+        out += [(f"n1_w{l}", (D,)), (f"n1_b{l}", (D,)),
+                (f"wq{l}", (D, D)), (f"bq{l}", (D,)), (f"wk{l}", (D, D)), (f"bk{l}", (D,)),
+                (f"wv{l}", (D, D)), (f"bv{l}", (D,)), (f"wo{l}", (D, D)), (f"bo{l}", (D,)),
+                (f"n2_w{l}", (D,)), (f"n2_b{l}", (D,)),
+                (f"w1{l}", (Fd, D)), (f"b1{l}", (Fd,)), (f"w2{l}", (D, Fd)), (f"b2{l}", (D,))]
+    out += [("nf_w", (D,)), ("nf_b", (D,)), ("w_out", (V, D)), ("b_out", (V,))]
+    return out
+
+
+def init_params(cfg: ModelConfig, seed: int = 0) -> np.ndarray:
+    """Flat fp32 buffer: projections N(0, 0.02^2), embeddings N(0, 1) * 0.02,
+    norm weights 1, biases 0 (seeded)."""
+    rng = np.random.default_rng(seed)
+    parts = []
+    for name, shape in param_shapes(cfg):
+        n = int(np.prod(shape))
+        if name.startswith(("n1_w", "n2_w", "nf_w")):
+            parts.append(np.ones(n, np.float32))
+        elif name.startswith(("b", "n1_b", "n2_b", "nf_b")) or name in ("b_out",):
+            parts.append(np.zeros(n, np.float32))
+        else:
+            parts.append((rng.standard_normal(n) * 0.02).astype(np.float32))
+    return np.concatenate(parts)
+
+
+def subtree_groups(tr, max_rows: int) -> list[tuple[int, int]]:
+    """Contiguous DFS row ranges of whole root-child subtrees, each at most
+    max_rows long unless one subtree alone is longer (the batching of the
+    reference's per-subtree trainer, agpt_train.cu:423-428)."""
+    roots = np.flatnonzero(tr.parent < 0)
+    bounds = np.append(roots, tr.n_nodes)
+    out, a = [], 0
+    for r in range(1, bounds.shape[0]):
+        if bounds[r] - a > max_rows and bounds[r - 1] > a:
+            out.append((a, int(bounds[r - 1])))
+            a = int(bounds[r - 1])
+    if tr.n_nodes > a:
+        out.append((a, tr.n_nodes))
+    return out
+
+
+class TrieBatch:
+    """The device tables of one batch (rows a..b of a trie, whole root-child
+    subtrees): DFS parents, RoPE positions, and the loss's radix query layout
+    (one query per node-token, radix nodes in DFS order, each endpoint's
+    next-token counts, edge_mass = visits of the edge's head). Mass weights
+    are normalised over the batch."""
+
+    def __init__(self, tr, cfg: ModelConfig, device, mass_mode: int = L.MASS_LINEAR, rows=None):
+        if tr.visits is None:
+            raise ValueError("the trie needs corpus counts (build_trie(..., counts=True))")
+        a0, b0 = rows if rows is not None else (0, tr.n_nodes)
+        self.T = b0 - a0
+        par = tr.parent[a0:b0]
+        self.parent = np.where(par < 0, -1, par - a0).astype(np.int32)
+        token = tr.token[a0:b0]
+        radix_head = tr.radix_head[a0:b0]
+        dev = device
+        self.tokens = torch.from_numpy(token.astype(np.int64)).to(dev)
+        self.positions = torch.from_numpy((tr.depth[a0:b0] - 1).astype(np.int32)).to(dev)
+        heads = np.flatnonzero(radix_head)
+        R = heads.shape[0]
+        q2n = (np.cumsum(radix_head) - 1).astype(np.int32)
+        qoff = np.append(heads, self.T).astype(np.int32)
+        ends = qoff[1:] - 1 + a0
+        a, b = tr.next_offsets[ends], tr.next_offsets[ends + 1]
+        cnt = (b - a).astype(np.int64)
+        coff = np.zeros(R + 1, np.int64)
+        np.cumsum(cnt, out=coff[1:])
+        sel = np.repeat(a.astype(np.int64) - coff[:-1], cnt) + np.arange(int(coff[-1]))
+        edge_len = np.diff(qoff).astype(np.int32)
+        edge_mass = tr.visits[heads + a0].astype(np.int32)
+        rid = np.arange(R, dtype=np.int32)
+        self.mass = None
+        if mass_mode != L.MASS_OFF:
+            self.mass = torch.from_numpy(L.mass_weights(rid, edge_mass, edge_len, qoff, self.T, mass_mode)).to(dev)
+        def to(x):
+            return torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(dev)
+        self.loss_args = [to(q2n), to(qoff), to(rid), to(token), to(coff), to(tr.next_tok[sel]),
+                          to(tr.next_val[sel])]
+        if int(token.max(initial=0)) >= cfg.vocab:
+            raise ValueError("trie tokens exceed the model vocabulary")
+
+
+class _Attn(torch.autograd.Function):
+    """Projection epilogue + trie attention; gradients come back pre-RoPE,
+    i.e. with respect to the projections' outputs (before their bias)."""
+
+    @staticmethod
+    def forward(ctx, ql, kl, vl, bq, bk, bv, m, grp):
+        att, batch = grp
+        q = block.bias_rope_(ql.detach().clone(), bq.detach(), batch.positions, m.cos, m.sin, m.cfg.n_heads)
+        k = block.bias_rope_(kl.detach().clone(), bk.detach(), batch.positions, m.cos, m.sin, m.cfg.n_heads)
+        v = block.bias_rope_(vl.detach().clone(), bv.detach(), n_heads=m.cfg.n_heads)
+        m._hook()
+        o, lse = att.forward(q, k, v)
+        m._hook()
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.m, ctx.att = m, att
+        return o
+
+    @staticmethod
+    def backward(ctx, d_o):
+        q, k, v, o, lse = ctx.saved_tensors
+        m = ctx.m
+        m._hook()
+        dq, dk, dv = ctx.att.backward(q, k, v, o, lse, d_o.contiguous(), rope=(m.cos, m.sin))
+        m._hook()
+        return dq, dk, dv, dq.sum(0), dk.sum(0), dv.sum(0), None, None
+
+
+class _Loss(torch.autograd.Function):
+    """Sum over queries of the per-query AGPT loss; the kernel's d_logits is
+    the gradient of that sum (agpt_train.cu:4810-4830)."""
+
+    @staticmethod
+    def forward(ctx, logits, batch):
+        d_logits, loss_q = L.loss_per_query(logits.detach().contiguous(), *batch.loss_args,
+                                            mass_weights=batch.mass)
+        ctx.save_for_backward(d_logits)
+        return loss_q.sum()
+
+    @staticmethod
+    def backward(ctx, g):
+        (d_logits,) = ctx.saved_tensors
+        return d_logits * g, None
+
+
+class TrieGPT:
+    def __init__(self, cfg: ModelConfig, device="cuda", seed: int = 0, lr: float = 1e-3,
+                 beta: float = 0.999, eps: float = 1e-8):
+        self.cfg = cfg
+        self.dev = torch.device(device)
+        self.flat = torch.from_numpy(init_params(cfg, seed)).to(self.dev).requires_grad_(True)
+        self.sq_avg = torch.zeros_like(self.flat, requires_grad=False)
+        self.lr, self.beta, self.eps = lr, beta, eps
+        hd = cfg.d_model // cfg.n_heads
+        self.cos, self.sin = rope_tables(cfg.max_depth, hd, device=self.dev)
+        self.groups = []  # (TrieAttention, TrieBatch) per batch of subtrees
+        self.attn_hook = None  # called before and after every attention fwd / bwd (timing)
+
+    def plan(self, tr, mass_mode: int = L.MASS_LINEAR, max_rows: int = 1 << 20) -> None:
+        """Splits the trie into batches of whole root-child subtrees (at most
+        max_rows rows each) and plans each batch's attention and loss tables."""
+        self.close()
+        hd = self.cfg.d_model // self.cfg.n_heads
+        for a, b in subtree_groups(tr, max_rows):
+            batch = TrieBatch(tr, self.cfg, self.dev, mass_mode, rows=(a, b))
+            att = TrieAttention(self.cfg.n_heads, hd, max_depth=self.cfg.max_depth)
+            att.plan(batch.parent)
+            self.groups.append((att, batch))
+
+    def _hook(self) -> None:
+        if self.attn_hook is not None:
+            self.attn_hook()
+
+    def params(self) -> dict[str, torch.Tensor]:
+        out, off = {}, 0
+        for name, shape in param_shapes(self.cfg):
+            n = int(np.prod(shape))
+            out[name] = self.flat[off:off + n].view(shape)
+            off += n
+        return out
+
+    def _norm(self, x, w, b):
+        if self.cfg.norm == "rms":
+            return F.rms_norm(x, (x.shape[-1],), w, self.cfg.eps)
+        return F.layer_norm(x, (x.shape[-1],), w, b, self.cfg.eps)
+
+    def loss(self, grp) -> torch.Tensor:
+        """Forward over one planned batch: the summed per-query loss."""
+        P, cfg = self.params(), self.cfg
+        batch = grp[1]
+        x = P["tok_emb"][batch.tokens]
+        for l in range(cfg.n_layers):
+            n1 = self._norm(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
+            o = _Attn.apply(F.linear(n1, P[f"wq{l}"]), F.linear(n1, P[f"wk{l}"]), F.linear(n1, P[f"wv{l}"]),
+                            P[f"bq{l}"], P[f"bk{l}"], P[f"bv{l}"], self, grp)
+            x = x + F.linear(o, P[f"wo{l}"], P[f"bo{l}"])
+            n2 = self._norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
+            x = x + F.linear(F.relu(F.linear(n2, P[f"w1{l}"], P[f"b1{l}"])), P[f"w2{l}"], P[f"b2{l}"])
+        logits = F.linear(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
+        return _Loss.apply(logits, batch)
+
+    def step(self) -> torch.Tensor:
+        """One training step over every planned batch: forward and backward
+        per batch (gradients accumulate in the flat buffer), then one
+        RMSProp update. Returns the summed loss as a device scalar."""
+        self.flat.grad = None
+        total = torch.zeros((), device=self.dev)
+        for grp in self.groups:
+            lv = self.loss(grp)
+            lv.backward()
+            total += lv.detach()
+        with torch.no_grad():
+            block.rmsprop_(self.flat.data, self.flat.grad, self.sq_avg, self.lr, self.beta, self.eps)
+        return total
+
+    def close(self) -> None:
+        for att, _ in self.groups:
+            att.close()
+        self.groups = []

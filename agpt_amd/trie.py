@@ -45,6 +45,12 @@ class Trie:
     n_radix: int
     n_root_children: int
     n_bigram_parts: int
+    # Corpus observations (build_trie(..., counts=True) only): visits per
+    # node and its next-token counts, CSR (offsets [T+1], tok, val).
+    visits: np.ndarray | None = None
+    next_offsets: np.ndarray | None = None
+    next_tok: np.ndarray | None = None
+    next_val: np.ndarray | None = None
 
     @property
     def n_nodes(self) -> int:
@@ -68,7 +74,7 @@ class Trie:
         return radix_parent, edge_len
 
 
-def _export(h) -> Trie:
+def _export(h, counts: bool = False) -> Trie:
     lib = trie_lib()
     n = C.c_int64()
     nr = C.c_int64()
@@ -81,17 +87,30 @@ def _export(h) -> Trie:
     T = n.value
     arrs = [np.empty(T, dtype=np.int32) for _ in range(6)]
     lib.agpt_trie_export(h, *[_ptr(a) for a in arrs])
+    extra = {}
+    if counts:
+        ne = C.c_int64()
+        vis = np.empty(T, np.int32)
+        if lib.agpt_trie_next_counts(h, _ptr(vis), C.byref(ne), None, None, None):
+            lib.agpt_trie_free(h)
+            raise ValueError("agpt_trie_next_counts: this trie has no corpus")
+        off = np.empty(T + 1, np.int32)
+        tk = np.empty(ne.value, np.int32)
+        vl = np.empty(ne.value, np.int32)
+        lib.agpt_trie_next_counts(h, None, C.byref(ne), _ptr(off), _ptr(tk), _ptr(vl))
+        extra = dict(visits=vis, next_offsets=off, next_tok=tk, next_val=vl)
     lib.agpt_trie_free(h)
-    return Trie(*arrs, n_radix=nr.value, n_root_children=nrc.value, n_bigram_parts=nbp.value)
+    return Trie(*arrs, n_radix=nr.value, n_root_children=nrc.value, n_bigram_parts=nbp.value, **extra)
 
 
-def build_trie(tokens: np.ndarray, max_depth: int, max_starts: int = 0) -> Trie:
-    """Leveled trie with TrieCorpus#ingest semantics (trie_corpus.cr:200-228)."""
+def build_trie(tokens: np.ndarray, max_depth: int, max_starts: int = 0, counts: bool = False) -> Trie:
+    """Leveled trie with TrieCorpus#ingest semantics (trie_corpus.cr:200-228);
+    counts=True also exports the corpus observations (visits, next-token counts)."""
     tok = np.ascontiguousarray(tokens, dtype=np.int32)
     h = C.c_void_p()
     if trie_lib().agpt_trie_build(_ptr(tok), tok.shape[0], max_depth, max_starts, C.byref(h)):
         raise ValueError("agpt_trie_build: bad arguments")
-    return _export(h)
+    return _export(h, counts)
 
 
 def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
@@ -115,7 +134,7 @@ CONFIGS = {
 }
 
 
-def config_trie(name: str, scale: float = 1.0) -> Trie:
+def config_trie(name: str, scale: float = 1.0, counts: bool = False) -> Trie:
     """The synthetic trie of a BASELINE config; scale < 1 shrinks the corpus."""
     c = CONFIGS[name]
     if "chains" in c:
@@ -124,4 +143,4 @@ def config_trie(name: str, scale: float = 1.0) -> Trie:
         return build_chains(tok, n_chains, c["chain_len"])
     n = max(2, int(c["n"] * scale))
     tok = markov_corpus(n, c["order"], c["vocab"], c["zipf"], c["seed"])
-    return build_trie(tok, c["depth"])
+    return build_trie(tok, c["depth"], counts=counts)

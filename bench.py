@@ -234,6 +234,69 @@ def bench_loss(args, tr, V: int) -> int:
     return 0
 
 
+C3_METRIC = "C3 training step node-tokens/sec (4-layer µGPT over the C1 trie: fwd+bwd+RMSProp, 1 GPU)"
+
+
+def bench_c3(args) -> int:
+    """One step = forward and backward of the 4-layer model over every
+    batch of whole root-child subtrees of the C1 trie (<= 1M rows each),
+    then one RMSProp update (agpt_amd.model). HIP events around every
+    trie-attention call give the attention share of the step."""
+    import torch
+    from agpt_amd import model, trie as trie_mod
+
+    dev = torch.device("cuda:0")
+    log(f"building C1 trie with counts (scale {args.scale})")
+    tr = trie_mod.config_trie("C1", args.scale, counts=True)
+    cfg = model.ModelConfig(vocab=65, d_model=128, n_heads=8, n_layers=4, d_ff=512, max_depth=32, norm="rms")
+    m = model.TrieGPT(cfg, device=dev, seed=1)
+    m.plan(tr, max_rows=1 << 20)
+    log(f"C3: {tr.n_nodes} node-tokens in {len(m.groups)} batches; {m.flat.numel()} parameters")
+    hev = HipEvents()
+    pool: list[int] = []
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def hook():
+        e = hev.create(1)[0]
+        hev.record(e, stream)
+        pool.append(e)
+
+    for _ in range(args.warmup):
+        m.step()
+    torch.cuda.synchronize()
+    m.attn_hook = hook
+    step_ms, attn_ms, losses = [], [], []
+    for _ in range(args.steps):
+        pool.clear()
+        t0 = time.perf_counter()
+        lv = m.step()
+        torch.cuda.synchronize()
+        step_ms.append((time.perf_counter() - t0) * 1e3)
+        attn_ms.append(sum(hev.ms(pool[i], pool[i + 1]) for i in range(0, len(pool), 2)))
+        hev.destroy(pool)
+        losses.append(float(lv))
+    m.attn_hook = None
+    ms = float(np.mean(step_ms))
+    am = float(np.mean(attn_ms))
+    log(f"C3 step {ms:.2f} ms, trie attention {am:.2f} ms ({am / ms:.1%}); loss {losses[0]:.4g} -> {losses[-1]:.4g}")
+    out = {
+        "metric": C3_METRIC, "value": tr.n_nodes * 1e3 / ms, "unit": "node-tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded order-3 Markov corpus -> C1 trie with counts; random-init weights)",
+        "config": {"workload": "C3: 4-layer training step on the C1 trie", "node_tokens": tr.n_nodes,
+                   "batches": len(m.groups), "d_model": 128, "heads": 8, "layers": 4, "d_ff": 512,
+                   "vocab": 65, "norm": "rms", "optimizer": "rmsprop(beta=0.999, lr=1e-3)",
+                   "loss": "per-query AGPT loss, linear mass weights"},
+        "attention_ms_per_step": am, "attention_share": am / ms,
+        "loss_first_last": [losses[0], losses[-1]],
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+    m.close()
+    return 0
+
+
 def load_traffic(name: str):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
@@ -252,8 +315,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C4", "C5"])
-    ap.add_argument("--path", default="attn", choices=["attn", "loss"],
-                    help="attn: trie attention fwd+bwd (the headline); loss: per-query AGPT loss")
+    ap.add_argument("--path", default="attn", choices=["attn", "loss", "c3"],
+                    help="attn: trie attention fwd+bwd (the headline); loss: per-query AGPT loss; "
+                         "c3: the 4-layer training step of config C3 (C1 trie)")
     ap.add_argument("--vocab", type=int, default=65, help="loss path: vocabulary size V")
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
@@ -286,6 +350,10 @@ def main() -> int:
     from agpt_amd import trie as trie_mod
     from agpt_amd.attention import TrieAttention
 
+    if args.path == "c3":
+        if args.scale is None:
+            args.scale = 1.0
+        return bench_c3(args)
     cfg = trie_mod.CONFIGS[args.workload]
     if args.scale is None:
         args.scale = cfg.get("one_gpu_scale", 1.0)

@@ -1,0 +1,47 @@
+/*
+ * agpt_block.h — C ABI of the kernels around the trie-attention path in one
+ * training step (libagpt_attn.so, gfx950): the projection epilogue (bias +
+ * RoPE) and the RMSProp update.
+ *
+ * Shares the conventions of agpt_attn.h: int status (AGPT_OK = 0) with the
+ * message in agpt_last_error(), DEVICE pointers owned by the caller, work
+ * ordered on the stream passed in (NULL = default stream), deterministic
+ * results.
+ */
+#ifndef AGPT_BLOCK_H
+#define AGPT_BLOCK_H
+
+#include <stdint.h>
+
+#include "agpt_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* In place on x [T, n_heads*head_dim] fp32 (a projection's output): adds
+ * bias [n_heads*head_dim] (NULL = none) to every row, then, when cos_t is
+ * not NULL, rotates each head's pairs (2i, 2i+1) by the angle of row t's
+ * position positions[t] (clamped to rope_seq_len-1):
+ *     x0' = x0 c - x1 s,  x1' = x0 s + x1 c,  c/s = table[pos, 2i].
+ * Replaces cuda_bias_add + launch_rope_batched (agpt_train.cu:4676-4687,
+ * kernel :1305-1326), fused into one pass over x. positions holds one entry
+ * per row t (the reference passes one per (row, head), all equal). */
+int agpt_bias_rope(float* x, const float* bias, const int32_t* positions, const float* cos_t,
+                   const float* sin_t, int rope_seq_len, int64_t T, int n_heads, int head_dim,
+                   void* stream);
+
+/* RMSProp without momentum over n fp32 parameters:
+ *     s = beta s + (1 - beta) g^2,   p -= lr g / (sqrt(s) + eps).
+ * Replaces cuda_rmsprop_bulk (the µGPT extern of agpt_train.cu:69, called at
+ * :5153-5156 with eps 1e-8); its body is not in the reference, so the update
+ * follows the textbook rule above (as torch.optim.RMSprop with alpha = beta,
+ * momentum 0, centered False). grads are read only. */
+int agpt_rmsprop(float* params, const float* grads, float* sq_avg, float lr, float beta, float eps,
+                 int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AGPT_BLOCK_H */

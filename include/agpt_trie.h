@@ -65,6 +65,16 @@ int agpt_trie_export(agpt_trie_handle t, int32_t* parent, int32_t* depth,
 int agpt_trie_export_radix(agpt_trie_handle t, int32_t* radix_parent,
                            int32_t* edge_len);
 
+/* Corpus observations of a trie built by agpt_trie_build (TrieCorpus#ingest
+ * + #observe, trie_corpus.cr:200-228): visits[i] = starts whose path passes
+ * node i; node i's next-token counts (every visit observes the token after
+ * its prefix, also where the path stops at the depth limit) as CSR over the
+ * T nodes: entries offsets[i] .. offsets[i+1]-1 of tok / val, tokens
+ * ascending, sum of val = visits[i]. Call first with tok = val = offsets =
+ * NULL to get n_entries. Returns 2 for a chain trie (no corpus). */
+int agpt_trie_next_counts(agpt_trie_handle t, int32_t* visits, int64_t* n_entries,
+                          int32_t* offsets, int32_t* tok, int32_t* val);
+
 void agpt_trie_free(agpt_trie_handle t);
 
 #ifdef __cplusplus

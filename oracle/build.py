@@ -17,7 +17,8 @@ HERE = Path(__file__).resolve().parent
 def build() -> Path:
     out = HERE / "liboracle.so"
     cmd = ["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-std=c99", "-shared", "-fPIC",
-           "-Wall", str(HERE / "trie_attn_oracle.c"), str(HERE / "loss_oracle.c"), "-o", str(out), "-lm"]
+           "-Wall", str(HERE / "trie_attn_oracle.c"), str(HERE / "loss_oracle.c"),
+           str(HERE / "block_oracle.c"), "-o", str(out), "-lm"]
     print("+", " ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     return out

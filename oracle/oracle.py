@@ -165,3 +165,23 @@ def loss_mass_weights(radix_ids, edge_mass, edge_lens, query_offsets, T_q, mode)
     out = np.empty(T_q, np.float32)
     lib().oracle_loss_mass_weights(*(_ip(x) for x in a), len(a[0]), T_q, mode, _fp(out))
     return out
+
+
+def bias_rope(x, bias, positions, cos_t, sin_t, n_heads, head_dim):
+    """cuda_bias_add + rope_batched_kernel restated (block_oracle.c); returns a copy."""
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    T = y.shape[0]
+    seq = 0 if cos_t is None else cos_t.shape[0]
+    lib().oracle_bias_rope(_fp(y), _fp(_f32(bias)), None if positions is None else _ip(_i32(positions)),
+                           _fp(_f32(cos_t)), _fp(_f32(sin_t)), seq, C.c_int64(T), n_heads, head_dim)
+    return y
+
+
+def rmsprop(params, grads, sq_avg, lr, beta, eps):
+    """Textbook RMSProp restated (block_oracle.c); returns (params, sq_avg) copies."""
+    p = np.array(params, dtype=np.float32, copy=True)
+    s = np.array(sq_avg, dtype=np.float32, copy=True)
+    g = _f32(grads)
+    lib().oracle_rmsprop(_fp(p), _fp(g), _fp(s), C.c_float(lr), C.c_float(beta), C.c_float(eps),
+                         C.c_int64(p.size))
+    return p, s

@@ -1,0 +1,89 @@
+"""GPU: the projection epilogue and RMSProp against the oracle, and one C3
+training step (agpt_amd.model: trie attention, epilogue, loss and RMSProp
+native; GEMMs and norms torch) against the float64 CPU reference model.
+
+Bars: epilogue and RMSProp within a few ulp of the oracle (fp32, fused
+multiply-adds on the GPU); the C3 step's loss within 1e-4 relative and every
+parameter's gradient within 2e-4 of its largest |value| (fp32 through two
+layers against float64)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import small_trie
+from oracle import oracle as ORC
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("H,hd,rope,bias", [(4, 16, True, True), (2, 64, True, False), (8, 16, False, True),
+                                            (3, 32, True, True)])
+def test_bias_rope_matches_oracle(gpu, H, hd, rope, bias):
+    import torch
+
+    from agpt_amd import block
+
+    rng = np.random.default_rng(H * hd)
+    T, seq = 1037, 24
+    x = rng.standard_normal((T, H * hd)).astype(np.float32)
+    b = rng.standard_normal(H * hd).astype(np.float32) if bias else None
+    pos = rng.integers(-2, seq + 5, T).astype(np.int32)  # clamped to [0, seq-1]
+    cos_t, sin_t = ORC.rope_table(seq, hd)
+    want = ORC.bias_rope(x, b, np.clip(pos, 0, seq - 1), cos_t if rope else None, sin_t if rope else None, H, hd)
+    xt = torch.from_numpy(x).to(gpu)
+    c, s = (torch.from_numpy(t).to(gpu) for t in (cos_t, sin_t))  # the same tables on both sides
+    block.bias_rope_(xt, None if b is None else torch.from_numpy(b).to(gpu),
+                     torch.from_numpy(pos).to(gpu), c if rope else None, s if rope else None, H)
+    np.testing.assert_allclose(xt.cpu().numpy(), want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [1, 4, 1001, 1 << 20])
+def test_rmsprop_matches_oracle(gpu, n):
+    import torch
+
+    from agpt_amd import block
+
+    rng = np.random.default_rng(n)
+    p = rng.standard_normal(n).astype(np.float32)
+    s = np.zeros(n, np.float32)
+    pt, st = torch.from_numpy(p).to(gpu), torch.from_numpy(s).to(gpu)
+    for _ in range(3):
+        g = rng.standard_normal(n).astype(np.float32)
+        p, s = ORC.rmsprop(p, g, s, 1e-3, 0.999, 1e-8)
+        block.rmsprop_(pt, torch.from_numpy(g).to(gpu), st, 1e-3, 0.999, 1e-8)
+    np.testing.assert_allclose(pt.cpu().numpy(), p, rtol=2e-6, atol=1e-6)
+    np.testing.assert_allclose(st.cpu().numpy(), s, rtol=2e-6)
+
+
+@pytest.mark.parametrize("norm,max_rows", [("rms", 1 << 20), ("layer", 1 << 20), ("rms", 400)])
+def test_c3_step_matches_float64(gpu, norm, max_rows):
+    import torch
+
+    from agpt_amd import model, trie
+    from c3_reference import step_f64
+
+    tok = trie.markov_corpus(260, 2, 7, 1.1, seed=5)
+    tr = trie.build_trie(tok, 10, counts=True)
+    cfg = model.ModelConfig(vocab=7, d_model=64, n_heads=4, n_layers=2, d_ff=128, max_depth=10, norm=norm)
+    m = model.TrieGPT(cfg, device=gpu, seed=3)
+    m.plan(tr, max_rows=max_rows)  # 400: several batches, gradients accumulated over them
+    assert len(m.groups) == (1 if max_rows > tr.n_nodes else len(model.subtree_groups(tr, max_rows)))
+    flat0 = m.flat.detach().cpu().numpy().copy()
+    loss = float(m.step())
+    torch.cuda.synchronize()
+    grad = m.flat.grad.detach().cpu().numpy()
+    mass = np.concatenate([b.mass.cpu().numpy() for _, b in m.groups])
+    want_loss, want_grad = step_f64(cfg, flat0, tr, mass)
+    assert abs(loss - want_loss) <= 1e-4 * abs(want_loss), (loss, want_loss)
+    off = 0
+    for name, shape in model.param_shapes(cfg):
+        k = int(np.prod(shape))
+        g, w = grad[off:off + k], want_grad[off:off + k]
+        bound = 2e-4 * max(np.abs(w).max(), 1e-6)
+        assert np.abs(g - w).max() <= bound, (name, np.abs(g - w).max(), np.abs(w).max())
+        off += k
+    # the update is RMSProp on the step's own gradient
+    p1, _ = ORC.rmsprop(flat0, grad, np.zeros_like(flat0), m.lr, m.beta, m.eps)
+    np.testing.assert_allclose(m.flat.detach().cpu().numpy(), p1, rtol=2e-6, atol=1e-6)
+    m.close()

@@ -24,6 +24,7 @@ def _declared(header: str) -> list[str]:
 @pytest.mark.parametrize("header,loader,table,n_min", [
     ("agpt_attn.h", _native.attn_lib, _native.ATTN_SYMBOLS, 8),
     ("agpt_loss.h", _native.attn_lib, _native.LOSS_SYMBOLS, 2),
+    ("agpt_block.h", _native.attn_lib, _native.BLOCK_SYMBOLS, 2),
     ("agpt_trie.h", _native.trie_lib, _native.TRIE_SYMBOLS, 8)])
 def test_abi_exports_every_declared_symbol(header, loader, table, n_min):
     lib = loader()
@@ -168,3 +169,30 @@ def test_create_fails_loudly_without_device():
     from agpt_amd.attention import TrieAttention
     with pytest.raises(_native.AgptError):
         TrieAttention(2, 8)
+
+
+@pytest.mark.parametrize("n,order,vocab,depth", [(300, 2, 5, 6), (500, 3, 7, 9)])
+def test_trie_next_counts_match_corpus_scan(n, order, vocab, depth):
+    """visits and next-token counts against a direct scan of the corpus with
+    TrieCorpus#ingest's loop (trie_corpus.cr:210-219): every step of every
+    start observes the token after its prefix."""
+    tok = trie.markov_corpus(n, order, vocab, 1.1, seed=4)
+    tr = trie.build_trie(tok, depth, counts=True)
+    hist, visits = {}, {}
+    for s in range(n - 1):
+        for d in range(1, min(depth, n - 1 - s) + 1):
+            key = tuple(tok[s:s + d])
+            visits[key] = visits.get(key, 0) + 1
+            h = hist.setdefault(key, {})
+            h[int(tok[s + d])] = h.get(int(tok[s + d]), 0) + 1
+    paths = []
+    for i in range(tr.n_nodes):
+        p = tr.parent[i]
+        paths.append((paths[p] if p >= 0 else ()) + (int(tr.token[i]),))
+    assert len(paths) == len(visits)
+    for i, key in enumerate(paths):
+        assert tr.visits[i] == visits[key]
+        a, b = tr.next_offsets[i], tr.next_offsets[i + 1]
+        got = dict(zip(tr.next_tok[a:b].tolist(), tr.next_val[a:b].tolist()))
+        assert got == hist[key]
+        assert list(tr.next_tok[a:b]) == sorted(got)
