@@ -152,7 +152,10 @@ class _Attn(torch.autograd.Function):
         m._hook()
         dq, dk, dv = ctx.att.backward(q, k, v, o, lse, d_o.contiguous(), rope=(m.cos, m.sin))
         m._hook()
-        return dq, dk, dv, dq.sum(0), dk.sum(0), dv.sum(0), None, None
+        # Bias gradients as one matrix-vector product each (a column sum over
+        # ~1M rows as a plain reduction keeps only D outputs in flight).
+        ones = torch.ones(1, dq.shape[0], device=dq.device, dtype=dq.dtype)
+        return dq, dk, dv, (ones @ dq)[0], (ones @ dk)[0], (ones @ dv)[0], None, None
 
 
 class _Loss(torch.autograd.Function):
@@ -173,7 +176,7 @@ class _Loss(torch.autograd.Function):
 
 
 class TrieGPT:
-    def __init__(self, cfg: ModelConfig, device="cuda", seed: int = 0, lr: float = 1e-3,
+    def __init__(self, cfg: ModelConfig, device="cuda", seed: int = 0, lr: float = 3e-4,
                  beta: float = 0.999, eps: float = 1e-8):
         self.cfg = cfg
         self.dev = torch.device(device)
@@ -217,7 +220,9 @@ class TrieGPT:
         """Forward over one planned batch: the summed per-query loss."""
         P, cfg = self.params(), self.cfg
         batch = grp[1]
-        x = P["tok_emb"][batch.tokens]
+        # X = onehot(token) · tok_emb: the backward is one product onehotᵀ · dX
+        # (the gather's backward would scatter-add 1M rows into 65).
+        x = F.one_hot(batch.tokens, cfg.vocab).to(torch.float32) @ P["tok_emb"]
         for l in range(cfg.n_layers):
             n1 = self._norm(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
             o = _Attn.apply(F.linear(n1, P[f"wq{l}"]), F.linear(n1, P[f"wk{l}"]), F.linear(n1, P[f"wv{l}"]),

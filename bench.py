@@ -286,7 +286,7 @@ def bench_c3(args) -> int:
         "data": "synthetic (seeded order-3 Markov corpus -> C1 trie with counts; random-init weights)",
         "config": {"workload": "C3: 4-layer training step on the C1 trie", "node_tokens": tr.n_nodes,
                    "batches": len(m.groups), "d_model": 128, "heads": 8, "layers": 4, "d_ff": 512,
-                   "vocab": 65, "norm": "rms", "optimizer": "rmsprop(beta=0.999, lr=1e-3)",
+                   "vocab": 65, "norm": "rms", "optimizer": "rmsprop(beta=0.999, lr=3e-4)",
                    "loss": "per-query AGPT loss, linear mass weights"},
         "attention_ms_per_step": am, "attention_share": am / ms,
         "loss_first_last": [losses[0], losses[-1]],
