@@ -247,6 +247,21 @@ class TrieGPT:
             block.rmsprop_(self.flat.data, self.flat.grad, self.sq_avg, self.lr, self.beta, self.eps)
         return total
 
+    def save(self, path: str) -> None:
+        """Writes the parameters as an MGPT checkpoint (agpt_train.cu:1262-1296)."""
+        from .checkpoint import save_mgpt
+        save_mgpt(path, self.cfg, self.flat.detach().cpu().numpy())
+
+    def load(self, path: str) -> None:
+        """Reads an MGPT checkpoint of this model's shape into the parameters."""
+        from .checkpoint import load_mgpt
+        cfg, flat = load_mgpt(path, norm=self.cfg.norm)
+        if (cfg.vocab, cfg.d_model, cfg.n_heads, cfg.n_layers, cfg.d_ff) != (
+                self.cfg.vocab, self.cfg.d_model, self.cfg.n_heads, self.cfg.n_layers, self.cfg.d_ff):
+            raise ValueError("checkpoint shape differs from the model's")
+        with torch.no_grad():
+            self.flat.copy_(torch.from_numpy(flat))
+
     def close(self) -> None:
         for att, _ in self.groups:
             att.close()

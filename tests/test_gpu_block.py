@@ -87,3 +87,14 @@ def test_c3_step_matches_float64(gpu, norm, max_rows):
     p1, _ = ORC.rmsprop(flat0, grad, np.zeros_like(flat0), m.lr, m.beta, m.eps)
     np.testing.assert_allclose(m.flat.detach().cpu().numpy(), p1, rtol=2e-6, atol=1e-6)
     m.close()
+
+
+def test_c3_checkpoint_round_trip_through_the_model(gpu, tmp_path):
+    from agpt_amd import model
+
+    cfg = model.ModelConfig(vocab=7, d_model=64, n_heads=4, n_layers=2, d_ff=128, max_depth=10, norm="layer")
+    a = model.TrieGPT(cfg, device=gpu, seed=1)
+    b = model.TrieGPT(cfg, device=gpu, seed=2)
+    a.save(str(tmp_path / "a.mgpt"))
+    b.load(str(tmp_path / "a.mgpt"))
+    assert (a.flat.detach() == b.flat.detach()).all()
