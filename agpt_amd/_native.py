@@ -95,6 +95,11 @@ TRIE_SYMBOLS = {
     "agpt_trie_export": (C.c_int, [_vp, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]),
     "agpt_trie_export_radix": (C.c_int, [_vp, _i32p, _i32p]),
     "agpt_trie_next_counts": (C.c_int, [_vp, _i32p, _i64p, _i32p, _i32p, _i32p]),
+    "agpt_radix_write_subtrees": (C.c_int, [_vp, C.c_char_p, C.c_int32]),
+    "agpt_radix_read_subtree": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "agpt_radix_info": (C.c_int, [_vp, _i64p, _i64p, _i64p, _i32p, _i32p]),
+    "agpt_radix_export": (C.c_int, [_vp] + [_i32p] * 9),
+    "agpt_radix_free": (None, [_vp]),
     "agpt_trie_free": (None, [_vp]),
 }
 

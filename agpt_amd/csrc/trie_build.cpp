@@ -12,6 +12,10 @@
 #include "../../include/agpt_trie.h"
 
 #include <algorithm>
+#include <array>
+#include <cstdio>
+#include <map>
+#include <string>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -324,5 +328,279 @@ extern "C" int agpt_trie_next_counts(agpt_trie_handle h, int32_t* visits, int64_
   *n_entries = k;
   return 0;
 }
+
+// ---- radix subtree files (streaming_radix_builder.cr:27-32, 100-330, 388-470;
+// read side agpt_train.cu:495-669) ---------------------------------------------
+
+namespace {
+
+constexpr uint32_t kRadixMagic = 0x52445841u;  // 'RDXA'
+constexpr int32_t kRadixVersion = 2;
+
+void put_i32(std::vector<uint8_t>& b, int32_t v) {
+  const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
+  b.insert(b.end(), p, p + 4);
+}
+void put_i64(std::vector<uint8_t>& b, int64_t v) {
+  const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
+  b.insert(b.end(), p, p + 8);
+}
+bool write_file(const std::string& path, const std::vector<uint8_t>& b) {
+  FILE* f = std::fopen(path.c_str(), "wb");
+  if (!f) return false;
+  const bool ok = std::fwrite(b.data(), 1, b.size(), f) == b.size();
+  return std::fclose(f) == 0 && ok;
+}
+
+}  // namespace
+
+struct agpt_radix_s {
+  int32_t root_child_id = 0, max_endpoint_depth = 0;
+  // radix nodes in DFS preorder (children by ascending first token)
+  std::vector<int32_t> radix_id, parent, first_char_depth, edge_len, edge_mass, edge_off;
+  std::vector<int32_t> tokens;  // edge tokens, DFS order
+  std::vector<int32_t> coff, ctok, cval;
+};
+
+extern "C" int agpt_radix_write_subtrees(agpt_trie_handle h, const char* out_dir, int32_t vocab_size) {
+  if (!h || !out_dir) return 1;
+  const Trie& t = h->t;
+  const int64_t n = static_cast<int64_t>(t.parent.size());
+  if (t.visits.size() != static_cast<size_t>(n)) return 2;  // no corpus counts
+  // next-token histograms (as agpt_trie_next_counts) and children lists
+  int64_t ne = 0;
+  if (agpt_trie_next_counts(h, nullptr, &ne, nullptr, nullptr, nullptr)) return 3;
+  std::vector<int32_t> off(n + 1), tok(ne), val(ne);
+  agpt_trie_next_counts(h, nullptr, &ne, off.data(), tok.data(), val.data());
+  std::vector<int32_t> first_child(n, -1), next_sib(n, -1), roots;
+  for (int64_t i = n - 1; i >= 0; --i) {
+    const int32_t p = t.parent[i];
+    if (p >= 0) {
+      next_sib[i] = first_child[p];
+      first_child[p] = static_cast<int32_t>(i);
+    }
+  }
+  for (int64_t i = 0; i < n; ++i)
+    if (t.parent[i] < 0) roots.push_back(static_cast<int32_t>(i));
+  struct Start {
+    int32_t parent_radix, node, depth;  // node = leveled parent (-1: root)
+  };
+  std::vector<Start> frontier{{0, -1, 1}};
+  std::map<int32_t, std::vector<uint8_t>> files;  // subtree key -> body
+  std::map<int32_t, std::array<int64_t, 3>> stats;  // key -> records, chars, max endpoint depth
+  std::vector<int32_t> subtree_of{0};
+  int32_t next_id = 1;
+  int64_t total_chars = 0;
+  int32_t max_ep = 0;
+  for (size_t fi = 0; fi < frontier.size(); ++fi) {  // FIFO: breadth first
+    const Start st = frontier[fi];
+    std::vector<int32_t> kids;
+    if (st.node < 0) kids = roots;
+    else
+      for (int32_t c = first_child[st.node]; c >= 0; c = next_sib[c]) kids.push_back(c);
+    for (int32_t c : kids) {
+      std::vector<int32_t> edge{t.token[c]};
+      int32_t cur = c;
+      // extend while the node has one next token and its one child exists
+      while (off[cur + 1] - off[cur] == 1 && first_child[cur] >= 0 && next_sib[first_child[cur]] < 0) {
+        cur = first_child[cur];
+        edge.push_back(t.token[cur]);
+      }
+      const int32_t rid = next_id++;
+      const int32_t key = st.parent_radix == 0 ? rid : subtree_of[st.parent_radix];
+      subtree_of.push_back(key);
+      const int32_t ep = t.depth[cur];
+      std::vector<uint8_t>& b = files[key];
+      put_i32(b, rid);
+      put_i32(b, st.parent_radix);
+      put_i32(b, st.depth);
+      put_i32(b, static_cast<int32_t>(edge.size()));
+      for (int32_t x : edge) put_i32(b, x);
+      put_i32(b, t.visits[c]);  // v2 edge mass: the head's count
+      put_i32(b, off[cur + 1] - off[cur]);
+      for (int32_t e = off[cur]; e < off[cur + 1]; ++e) {
+        put_i32(b, tok[e]);
+        put_i32(b, val[e]);
+      }
+      auto& sv = stats[key];
+      sv[0] += 1;
+      sv[1] += static_cast<int64_t>(edge.size());
+      sv[2] = std::max<int64_t>(sv[2], ep);
+      total_chars += static_cast<int64_t>(edge.size());
+      max_ep = std::max(max_ep, ep);
+      if (off[cur + 1] - off[cur] >= 2) frontier.push_back({rid, cur, ep + 1});
+    }
+  }
+  const std::string dir(out_dir);
+  std::vector<uint8_t> manifest;
+  put_i32(manifest, static_cast<int32_t>(kRadixMagic));
+  put_i32(manifest, kRadixVersion);
+  put_i32(manifest, static_cast<int32_t>(files.size()));
+  for (const auto& kv : files) {  // std::map: ascending root-child id
+    const auto& sv = stats[kv.first];
+    std::vector<uint8_t> b;
+    put_i32(b, static_cast<int32_t>(kRadixMagic));
+    put_i32(b, kRadixVersion);
+    put_i32(b, kv.first);
+    put_i32(b, static_cast<int32_t>(sv[0]));
+    put_i64(b, sv[1]);
+    put_i32(b, static_cast<int32_t>(sv[2]));
+    b.insert(b.end(), kv.second.begin(), kv.second.end());
+    char name[64];
+    std::snprintf(name, sizeof(name), "/subtrees/radix_subtree_%06d.bin", kv.first);
+    if (!write_file(dir + name, b)) return 4;
+    put_i32(manifest, kv.first);
+    put_i32(manifest, static_cast<int32_t>(sv[0]));
+    put_i64(manifest, sv[1]);
+    put_i32(manifest, static_cast<int32_t>(sv[2]));
+  }
+  if (!write_file(dir + "/manifest.bin", manifest)) return 4;
+  std::vector<uint8_t> meta;
+  put_i32(meta, static_cast<int32_t>(kRadixMagic));
+  put_i32(meta, kRadixVersion);
+  put_i32(meta, next_id);  // radix nodes + the virtual root
+  put_i32(meta, max_ep + 1);
+  put_i64(meta, total_chars);
+  put_i32(meta, 0);  // corpus token count: not kept by the trie
+  put_i32(meta, vocab_size);
+  put_i64(meta, 0);  // corpus hash
+  put_i32(meta, 4);
+  for (char ch : std::string("char")) meta.push_back(static_cast<uint8_t>(ch));
+  if (!write_file(dir + "/meta.bin", meta)) return 4;
+  return 0;
+}
+
+extern "C" int agpt_radix_read_subtree(const char* path, agpt_radix_handle* out) {
+  if (!path || !out) return 1;
+  *out = nullptr;
+  FILE* f = std::fopen(path, "rb");
+  if (!f) return 2;
+  std::vector<uint8_t> b;
+  uint8_t buf[1 << 16];
+  size_t got;
+  while ((got = std::fread(buf, 1, sizeof(buf), f)) > 0) b.insert(b.end(), buf, buf + got);
+  std::fclose(f);
+  size_t pos = 0;
+  bool ok = true;
+  auto i32 = [&]() -> int32_t {
+    if (pos + 4 > b.size()) { ok = false; return 0; }
+    int32_t v;
+    std::memcpy(&v, b.data() + pos, 4);
+    pos += 4;
+    return v;
+  };
+  auto i64 = [&]() -> int64_t {
+    if (pos + 8 > b.size()) { ok = false; return 0; }
+    int64_t v;
+    std::memcpy(&v, b.data() + pos, 8);
+    pos += 8;
+    return v;
+  };
+  if (static_cast<uint32_t>(i32()) != kRadixMagic || !ok) return 3;
+  if (i32() != kRadixVersion || !ok) return 4;
+  auto* r = new agpt_radix_s();
+  r->root_child_id = i32();
+  const int32_t count = i32();
+  const int64_t chars = i64();
+  r->max_endpoint_depth = i32();
+  if (!ok || count < 0 || chars < 0) { delete r; return 5; }
+  // records in file order (breadth first)
+  std::vector<int32_t> rid(count), gpar(count), fcd(count), elen(count), mass(count), eoff(count), cstart(count),
+      ccount(count);
+  std::vector<int32_t> toks, ct, cv;
+  for (int32_t i = 0; i < count && ok; ++i) {
+    rid[i] = i32();
+    gpar[i] = i32();
+    fcd[i] = i32();
+    elen[i] = i32();
+    if (elen[i] < 1 || pos + 4 * static_cast<size_t>(elen[i]) > b.size()) { ok = false; break; }
+    eoff[i] = static_cast<int32_t>(toks.size());
+    for (int32_t e = 0; e < elen[i]; ++e) toks.push_back(i32());
+    mass[i] = i32();
+    ccount[i] = i32();
+    if (ccount[i] < 0 || pos + 8 * static_cast<size_t>(ccount[i]) > b.size()) { ok = false; break; }
+    cstart[i] = static_cast<int32_t>(ct.size());
+    for (int32_t e = 0; e < ccount[i]; ++e) {
+      ct.push_back(i32());
+      cv.push_back(i32());
+    }
+  }
+  if (!ok || pos != b.size() || static_cast<int64_t>(toks.size()) != chars) { delete r; return 5; }
+  // global -> local ids; the subtree's root child has global parent 0
+  std::unordered_map<int32_t, int32_t> local;
+  local.reserve(static_cast<size_t>(count) * 2);
+  for (int32_t i = 0; i < count; ++i) local[rid[i]] = i;
+  std::vector<int32_t> lpar(count, -1);
+  std::vector<std::vector<int32_t>> kids(count);
+  std::vector<int32_t> tops;
+  for (int32_t i = 0; i < count; ++i) {
+    const auto it = gpar[i] == 0 ? local.end() : local.find(gpar[i]);
+    if (it == local.end()) tops.push_back(i);
+    else {
+      lpar[i] = it->second;
+      kids[it->second].push_back(i);
+    }
+  }
+  auto by_tok = [&](int32_t a, int32_t c) { return toks[eoff[a]] < toks[eoff[c]] || (toks[eoff[a]] == toks[eoff[c]] && a < c); };
+  std::sort(tops.begin(), tops.end(), by_tok);
+  for (auto& k : kids) std::sort(k.begin(), k.end(), by_tok);
+  // DFS preorder
+  std::vector<int32_t> order, newid(count, -1), stack(tops.rbegin(), tops.rend());
+  while (!stack.empty()) {
+    const int32_t i = stack.back();
+    stack.pop_back();
+    newid[i] = static_cast<int32_t>(order.size());
+    order.push_back(i);
+    for (auto it = kids[i].rbegin(); it != kids[i].rend(); ++it) stack.push_back(*it);
+  }
+  r->coff.push_back(0);
+  for (int32_t i : order) {
+    r->radix_id.push_back(rid[i]);
+    r->parent.push_back(lpar[i] < 0 ? -1 : newid[lpar[i]]);
+    r->first_char_depth.push_back(fcd[i]);
+    r->edge_len.push_back(elen[i]);
+    r->edge_mass.push_back(mass[i]);
+    r->edge_off.push_back(static_cast<int32_t>(r->tokens.size()));
+    r->tokens.insert(r->tokens.end(), toks.begin() + eoff[i], toks.begin() + eoff[i] + elen[i]);
+    r->ctok.insert(r->ctok.end(), ct.begin() + cstart[i], ct.begin() + cstart[i] + ccount[i]);
+    r->cval.insert(r->cval.end(), cv.begin() + cstart[i], cv.begin() + cstart[i] + ccount[i]);
+    r->coff.push_back(static_cast<int32_t>(r->ctok.size()));
+  }
+  *out = r;
+  return 0;
+}
+
+extern "C" int agpt_radix_info(agpt_radix_handle r, int64_t* n_radix, int64_t* n_chars, int64_t* n_entries,
+                               int32_t* root_child_id, int32_t* max_endpoint_depth) {
+  if (!r) return 1;
+  if (n_radix) *n_radix = static_cast<int64_t>(r->radix_id.size());
+  if (n_chars) *n_chars = static_cast<int64_t>(r->tokens.size());
+  if (n_entries) *n_entries = static_cast<int64_t>(r->ctok.size());
+  if (root_child_id) *root_child_id = r->root_child_id;
+  if (max_endpoint_depth) *max_endpoint_depth = r->max_endpoint_depth;
+  return 0;
+}
+
+extern "C" int agpt_radix_export(agpt_radix_handle r, int32_t* radix_id, int32_t* radix_parent,
+                                 int32_t* first_char_depth, int32_t* edge_len, int32_t* edge_mass,
+                                 int32_t* edge_tokens, int32_t* counts_offset, int32_t* counts_tok,
+                                 int32_t* counts_val) {
+  if (!r) return 1;
+  auto cp = [](int32_t* dst, const std::vector<int32_t>& src) {
+    if (dst && !src.empty()) std::memcpy(dst, src.data(), src.size() * sizeof(int32_t));
+  };
+  cp(radix_id, r->radix_id);
+  cp(radix_parent, r->parent);
+  cp(first_char_depth, r->first_char_depth);
+  cp(edge_len, r->edge_len);
+  cp(edge_mass, r->edge_mass);
+  cp(edge_tokens, r->tokens);
+  cp(counts_offset, r->coff);
+  cp(counts_tok, r->ctok);
+  cp(counts_val, r->cval);
+  return 0;
+}
+
+extern "C" void agpt_radix_free(agpt_radix_handle r) { delete r; }
 
 extern "C" void agpt_trie_free(agpt_trie_handle h) { delete h; }

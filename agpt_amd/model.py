@@ -86,46 +86,68 @@ def subtree_groups(tr, max_rows: int) -> list[tuple[int, int]]:
 
 
 class TrieBatch:
-    """The device tables of one batch (rows a..b of a trie, whole root-child
-    subtrees): DFS parents, RoPE positions, and the loss's radix query layout
-    (one query per node-token, radix nodes in DFS order, each endpoint's
-    next-token counts, edge_mass = visits of the edge's head). Mass weights
+    """The device tables of one batch of whole root-child subtrees: DFS
+    parents, RoPE positions, and the loss's radix query layout (one query
+    per node-token, radix nodes in DFS order, each endpoint's next-token
+    counts, edge_mass = the count of the edge's first node). Mass weights
     are normalised over the batch."""
 
     def __init__(self, tr, cfg: ModelConfig, device, mass_mode: int = L.MASS_LINEAR, rows=None):
+        """From a trie with corpus counts (build_trie(..., counts=True)),
+        rows a..b (whole root-child subtrees)."""
         if tr.visits is None:
             raise ValueError("the trie needs corpus counts (build_trie(..., counts=True))")
         a0, b0 = rows if rows is not None else (0, tr.n_nodes)
-        self.T = b0 - a0
         par = tr.parent[a0:b0]
-        self.parent = np.where(par < 0, -1, par - a0).astype(np.int32)
-        token = tr.token[a0:b0]
-        radix_head = tr.radix_head[a0:b0]
-        dev = device
-        self.tokens = torch.from_numpy(token.astype(np.int64)).to(dev)
-        self.positions = torch.from_numpy((tr.depth[a0:b0] - 1).astype(np.int32)).to(dev)
-        heads = np.flatnonzero(radix_head)
-        R = heads.shape[0]
-        q2n = (np.cumsum(radix_head) - 1).astype(np.int32)
-        qoff = np.append(heads, self.T).astype(np.int32)
+        heads = np.flatnonzero(tr.radix_head[a0:b0])
+        qoff = np.append(heads, b0 - a0).astype(np.int64)
         ends = qoff[1:] - 1 + a0
         a, b = tr.next_offsets[ends], tr.next_offsets[ends + 1]
         cnt = (b - a).astype(np.int64)
-        coff = np.zeros(R + 1, np.int64)
+        coff = np.zeros(heads.shape[0] + 1, np.int64)
         np.cumsum(cnt, out=coff[1:])
         sel = np.repeat(a.astype(np.int64) - coff[:-1], cnt) + np.arange(int(coff[-1]))
+        self._build(cfg, device, mass_mode, np.where(par < 0, -1, par - a0), tr.token[a0:b0],
+                    tr.depth[a0:b0], qoff, tr.visits[heads + a0], coff, tr.next_tok[sel], tr.next_val[sel])
+
+    @classmethod
+    def from_radix(cls, subtrees, cfg: ModelConfig, device, mass_mode: int = L.MASS_LINEAR):
+        """From radix subtree files read by trie.read_radix_subtree (the
+        reference's per-subtree loader, agpt_train.cu:495-669), concatenated."""
+        self = cls.__new__(cls)
+        parts = [st.rows() for st in subtrees]
+        base = np.cumsum([0] + [p[0].shape[0] for p in parts])
+        parent = np.concatenate([np.where(p < 0, -1, p + o) for (p, _, _), o in zip(parts, base)])
+        qoff = [np.zeros(1, np.int64)]
+        coff = [np.zeros(1, np.int64)]
+        for st, o in zip(subtrees, base):
+            qoff.append(np.cumsum(st.edge_len).astype(np.int64) + o)
+            coff.append(st.counts_offset[1:].astype(np.int64) + coff[-1][-1])
+        self._build(cfg, device, mass_mode, parent, np.concatenate([p[1] for p in parts]),
+                    np.concatenate([p[2] for p in parts]), np.concatenate(qoff),
+                    np.concatenate([st.edge_mass for st in subtrees]), np.concatenate(coff),
+                    np.concatenate([st.counts_tok for st in subtrees]),
+                    np.concatenate([st.counts_val for st in subtrees]))
+        return self
+
+    def _build(self, cfg, dev, mass_mode, parent, token, depth, qoff, edge_mass, coff, ctok, cval):
+        self.T = int(parent.shape[0])
+        self.parent = np.ascontiguousarray(parent, dtype=np.int32)
+        if int(token.max(initial=0)) >= cfg.vocab:
+            raise ValueError("trie tokens exceed the model vocabulary")
+        self.tokens = torch.from_numpy(token.astype(np.int64)).to(dev)
+        self.positions = torch.from_numpy((depth - 1).astype(np.int32)).to(dev)
+        R = qoff.shape[0] - 1
         edge_len = np.diff(qoff).astype(np.int32)
-        edge_mass = tr.visits[heads + a0].astype(np.int32)
+        q2n = np.repeat(np.arange(R, dtype=np.int32), edge_len)
         rid = np.arange(R, dtype=np.int32)
         self.mass = None
         if mass_mode != L.MASS_OFF:
             self.mass = torch.from_numpy(L.mass_weights(rid, edge_mass, edge_len, qoff, self.T, mass_mode)).to(dev)
+
         def to(x):
             return torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(dev)
-        self.loss_args = [to(q2n), to(qoff), to(rid), to(token), to(coff), to(tr.next_tok[sel]),
-                          to(tr.next_val[sel])]
-        if int(token.max(initial=0)) >= cfg.vocab:
-            raise ValueError("trie tokens exceed the model vocabulary")
+        self.loss_args = [to(q2n), to(qoff), to(rid), to(token), to(coff), to(ctok), to(cval)]
 
 
 class _Attn(torch.autograd.Function):
@@ -198,6 +220,33 @@ class TrieGPT:
             att = TrieAttention(self.cfg.n_heads, hd, max_depth=self.cfg.max_depth)
             att.plan(batch.parent)
             self.groups.append((att, batch))
+
+    def plan_radix_dir(self, radix_dir: str, mass_mode: int = L.MASS_LINEAR, max_rows: int = 1 << 20) -> None:
+        """Plans from the reference's radix files (manifest.bin +
+        subtrees/radix_subtree_%06d.bin): subtrees in manifest order, packed
+        into batches of at most max_rows node-tokens (a larger subtree alone)."""
+        import os
+
+        from . import trie as trie_mod
+        self.close()
+        hd = self.cfg.d_model // self.cfg.n_heads
+        man = trie_mod.read_radix_manifest(os.path.join(radix_dir, "manifest.bin"))
+        pending, rows = [], 0
+
+        def flush():
+            if pending:
+                batch = TrieBatch.from_radix(pending, self.cfg, self.dev, mass_mode)
+                att = TrieAttention(self.cfg.n_heads, hd, max_depth=self.cfg.max_depth)
+                att.plan(batch.parent)
+                self.groups.append((att, batch))
+        for rc, _, chars, _ in man:
+            if pending and rows + chars > max_rows:
+                flush()
+                pending, rows = [], 0
+            pending.append(trie_mod.read_radix_subtree(
+                os.path.join(radix_dir, "subtrees", f"radix_subtree_{rc:06d}.bin")))
+            rows += chars
+        flush()
 
     def _hook(self) -> None:
         if self.attn_hook is not None:

@@ -122,6 +122,80 @@ def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
     return _export(h)
 
 
+def write_radix_files(tokens: np.ndarray, max_depth: int, out_dir: str, vocab: int) -> None:
+    """Builds the leveled trie of `tokens` and writes the reference's radix
+    files (subtrees/radix_subtree_%06d.bin, manifest.bin, meta.bin, format v2)."""
+    import os
+    os.makedirs(os.path.join(out_dir, "subtrees"), exist_ok=True)
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    h = C.c_void_p()
+    lib = trie_lib()
+    if lib.agpt_trie_build(_ptr(tok), tok.shape[0], max_depth, 0, C.byref(h)):
+        raise ValueError("agpt_trie_build: bad arguments")
+    rc = lib.agpt_radix_write_subtrees(h, out_dir.encode(), vocab)
+    lib.agpt_trie_free(h)
+    if rc:
+        raise OSError(f"agpt_radix_write_subtrees failed ({rc})")
+
+
+@dataclass
+class RadixSubtree:
+    """One radix_subtree_%06d.bin, radix nodes in DFS preorder."""
+    root_child_id: int
+    max_endpoint_depth: int
+    radix_id: np.ndarray          # [R] global ids
+    radix_parent: np.ndarray      # [R] local, -1 for the root child
+    first_char_depth: np.ndarray  # [R]
+    edge_len: np.ndarray          # [R]
+    edge_mass: np.ndarray         # [R]
+    edge_tokens: np.ndarray       # [node-tokens], row order
+    counts_offset: np.ndarray     # [R+1]
+    counts_tok: np.ndarray
+    counts_val: np.ndarray
+
+    def rows(self) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """Node-token rows (one per edge char, DFS order): (parent, token,
+        depth), the input of TrieAttention.plan."""
+        qoff = np.zeros(self.edge_len.shape[0] + 1, np.int64)
+        np.cumsum(self.edge_len, out=qoff[1:])
+        T = int(qoff[-1])
+        parent = np.arange(-1, T - 1, dtype=np.int64)  # within an edge: the previous row
+        rp = self.radix_parent
+        first = qoff[:-1]
+        parent[first] = np.where(rp < 0, -1, qoff[np.maximum(rp, 0) + 1] - 1)
+        depth = np.repeat(self.first_char_depth.astype(np.int64) - first, self.edge_len) + np.arange(T)
+        return parent.astype(np.int32), self.edge_tokens.copy(), depth.astype(np.int32)
+
+
+def read_radix_subtree(path: str) -> RadixSubtree:
+    lib = trie_lib()
+    h = C.c_void_p()
+    rc = lib.agpt_radix_read_subtree(str(path).encode(), C.byref(h))
+    if rc:
+        raise ValueError(f"{path}: not a readable radix subtree file (code {rc})")
+    R, nc, ne = C.c_int64(), C.c_int64(), C.c_int64()
+    rcid, mx = C.c_int32(), C.c_int32()
+    lib.agpt_radix_info(h, C.byref(R), C.byref(nc), C.byref(ne), C.byref(rcid), C.byref(mx))
+    a = [np.empty(R.value, np.int32) for _ in range(5)]
+    et = np.empty(nc.value, np.int32)
+    co = np.empty(R.value + 1, np.int32)
+    ct = np.empty(ne.value, np.int32)
+    cv = np.empty(ne.value, np.int32)
+    lib.agpt_radix_export(h, *[_ptr(x) for x in a], _ptr(et), _ptr(co), _ptr(ct), _ptr(cv))
+    lib.agpt_radix_free(h)
+    return RadixSubtree(rcid.value, mx.value, *a, et, co, ct, cv)
+
+
+def read_radix_manifest(path: str) -> list[tuple[int, int, int, int]]:
+    """manifest.bin: (root_child_id, n_nodes, total_edge_chars, max_endpoint_depth) per subtree."""
+    import struct
+    data = open(path, "rb").read()
+    magic, ver, n = struct.unpack_from("<Iii", data, 0)
+    if magic != 0x52445841 or ver != 2:
+        raise ValueError(f"{path}: not a v2 radix manifest")
+    return [struct.unpack_from("<iiqi", data, 12 + 20 * i) for i in range(n)]
+
+
 # BASELINE.json configs (synthetic tries). Seeds are fixed and recorded.
 CONFIGS = {
     "C1": dict(n=200_000, order=3, vocab=65, zipf=1.1, depth=32, seed=1, H=4, hd=16, dtype="f32"),

@@ -75,6 +75,44 @@ int agpt_trie_export_radix(agpt_trie_handle t, int32_t* radix_parent,
 int agpt_trie_next_counts(agpt_trie_handle t, int32_t* visits, int64_t* n_entries,
                           int32_t* offsets, int32_t* tok, int32_t* val);
 
+/* ---- radix subtree files ---------------------------------------------------
+ * The reference's on-disk radix trie, format v2 (streaming_radix_builder.cr:
+ * 10-32, 388-470): out_dir/subtrees/radix_subtree_%06d.bin (one per root
+ * child, keyed by its radix id), out_dir/manifest.bin, out_dir/meta.bin.
+ * Record: radix_id, parent_radix_id (0 = virtual root), first_char_depth,
+ * edge_len, edge tokens, edge_mass (count of the edge's first node),
+ * entry_count, (token, count) entries of the endpoint's next-token counts. */
+typedef struct agpt_radix_s* agpt_radix_handle;
+
+/* Writes the radix files of a trie built with agpt_trie_build (needs its
+ * corpus counts) as the reference's builder does (streaming_radix_builder.cr:
+ * 100-330): edge starts breadth first from the root, radix ids in that order
+ * from 1, an edge extended while its end has exactly one next-token entry
+ * and that child exists. out_dir and out_dir/subtrees must exist. */
+int agpt_radix_write_subtrees(agpt_trie_handle t, const char* out_dir, int32_t vocab_size);
+
+/* Reads one radix_subtree_%06d.bin (agpt_train.cu:495-669 load_subtree):
+ * global ids mapped to local ones, radix nodes reordered to DFS preorder with
+ * children by ascending first token (what agpt_attn_plan_radix takes).
+ * Returns 2 (cannot open), 3 (bad magic), 4 (bad version), 5 (malformed). */
+int agpt_radix_read_subtree(const char* path, agpt_radix_handle* out);
+
+/* Sizes of a read subtree: radix nodes R, edge chars (node-tokens), count
+ * entries, the root child's radix id, the deepest endpoint. */
+int agpt_radix_info(agpt_radix_handle r, int64_t* n_radix, int64_t* n_chars, int64_t* n_entries,
+                    int32_t* root_child_id, int32_t* max_endpoint_depth);
+
+/* Copies the DFS-ordered tables (any pointer may be NULL): per radix node
+ * [R] its global radix id, local parent (-1 for the root child),
+ * first_char_depth, edge_len, edge_mass; edge_tokens [chars] in row order;
+ * the endpoint counts as CSR counts_offset [R+1], counts_tok, counts_val. */
+int agpt_radix_export(agpt_radix_handle r, int32_t* radix_id, int32_t* radix_parent,
+                      int32_t* first_char_depth, int32_t* edge_len, int32_t* edge_mass,
+                      int32_t* edge_tokens, int32_t* counts_offset, int32_t* counts_tok,
+                      int32_t* counts_val);
+
+void agpt_radix_free(agpt_radix_handle r);
+
 void agpt_trie_free(agpt_trie_handle t);
 
 #ifdef __cplusplus

@@ -98,3 +98,23 @@ def test_c3_checkpoint_round_trip_through_the_model(gpu, tmp_path):
     a.save(str(tmp_path / "a.mgpt"))
     b.load(str(tmp_path / "a.mgpt"))
     assert (a.flat.detach() == b.flat.detach()).all()
+
+
+def test_c3_step_from_radix_files(gpu, tmp_path):
+    """Planning from the reference's radix files gives the same step as
+    planning from the trie (loss and gradient bit for bit: same tables)."""
+    from agpt_amd import model, trie
+
+    tok = trie.markov_corpus(3000, 2, 7, 1.1, seed=3)
+    trie.write_radix_files(tok, 10, str(tmp_path), 7)
+    tr = trie.build_trie(tok, 10, counts=True)
+    cfg = model.ModelConfig(vocab=7, d_model=64, n_heads=4, n_layers=2, d_ff=128, max_depth=10)
+    a, b = model.TrieGPT(cfg, device=gpu, seed=3), model.TrieGPT(cfg, device=gpu, seed=3)
+    a.plan(tr, max_rows=2000)
+    b.plan_radix_dir(str(tmp_path), max_rows=2000)
+    assert [g[1].T for g in a.groups] == [g[1].T for g in b.groups]
+    la, lb = float(a.step()), float(b.step())
+    assert la == lb
+    assert (a.flat.grad == b.flat.grad).all()
+    a.close()
+    b.close()
