@@ -1,6 +1,7 @@
 """Kernels around the trie-attention path in a training step
-(include/agpt_block.h): the projection epilogue (bias + RoPE, in place) and
-the RMSProp update. Torch CUDA tensors, current stream; no CPU fallback."""
+(include/agpt_block.h): the projection epilogue (bias + RoPE, in place), the
+row norms and the RMSProp update. Torch CUDA tensors, current stream; no CPU
+fallback."""
 from __future__ import annotations
 
 import ctypes as C
@@ -43,3 +44,30 @@ def rmsprop_(params, grads, sq_avg, lr: float, beta: float, eps: float = 1e-8):
     _native.check(_native.attn_lib().agpt_rmsprop(
         _ptr(params), _ptr(grads), _ptr(sq_avg), C.c_float(lr), C.c_float(beta), C.c_float(eps), n,
         _stream(params)))
+
+
+def norm_fwd(x, w, b=None, eps: float = 1e-5):
+    """LayerNorm (b given) or RMSNorm of the rows of x [T, D]; returns
+    (y, mean or None, rstd)."""
+    import torch
+    T, D = x.shape
+    y = torch.empty_like(x)
+    rstd = torch.empty(T, device=x.device, dtype=torch.float32)
+    mean = torch.empty(T, device=x.device, dtype=torch.float32) if b is not None else None
+    _native.check(_native.attn_lib().agpt_norm_fwd(
+        _ptr(x), _ptr(w), _ptr(b), _ptr(y), _ptr(mean), _ptr(rstd), T, D, C.c_float(eps), _stream(x)))
+    return y, mean, rstd
+
+
+def norm_bwd(dy, x, w, mean, rstd, layer: bool):
+    """Returns (dx, dw, db or None) of norm_fwd."""
+    import torch
+    T, D = x.shape
+    lib = _native.attn_lib()
+    ws = torch.empty(lib.agpt_norm_workspace_floats(D), device=x.device, dtype=torch.float32)
+    dx = torch.empty_like(x)
+    dw = torch.empty(D, device=x.device, dtype=torch.float32)
+    db = torch.empty(D, device=x.device, dtype=torch.float32) if layer else None
+    _native.check(lib.agpt_norm_bwd(_ptr(dy), _ptr(x), _ptr(w), _ptr(mean), _ptr(rstd), _ptr(dx), _ptr(dw),
+                                    _ptr(db), _ptr(ws), ws.numel(), T, D, _stream(x)))
+    return dx, dw, db

@@ -12,6 +12,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <type_traits>
 
 namespace {
 
@@ -104,7 +105,222 @@ __global__ __launch_bounds__(kThreads) void rmsprop_kernel(float* __restrict__ p
 
 bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 
+// ---- RMSNorm / LayerNorm over rows of D = 16 * VPL floats -------------------
+// 16 lanes own a row; lane c holds columns 64k + 4c + e (k < VPL/4, e < 4), so
+// each 16-byte load of the 16 lanes covers 256 contiguous bytes. Row sums are
+// DPP butterflies (row mirror, half mirror, quad reverse, pair swap), which
+// leave the same bits in all 16 lanes. A wave works 4 rows at once.
+template <int kCtrl>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dppf<0x140>(v);
+  v += dppf<0x141>(v);
+  v += dppf<0x1B>(v);
+  return v + dppf<0xB1>(v);
+}
+
+constexpr int kNormBlocks = 1024;  // workgroups of the row kernels (and weight-gradient partials)
+
+template <int VPL>
+__device__ __forceinline__ void load_cols(const float* __restrict__ row, int c, float (&v)[VPL]) {
+#pragma unroll
+  for (int k = 0; k < VPL / 4; ++k) {
+    const float4 q = *reinterpret_cast<const float4*>(row + 64 * k + 4 * c);
+    v[4 * k] = q.x;
+    v[4 * k + 1] = q.y;
+    v[4 * k + 2] = q.z;
+    v[4 * k + 3] = q.w;
+  }
+}
+template <int VPL>
+__device__ __forceinline__ void store_cols(float* __restrict__ row, int c, const float (&v)[VPL]) {
+#pragma unroll
+  for (int k = 0; k < VPL / 4; ++k)
+    *reinterpret_cast<float4*>(row + 64 * k + 4 * c) = float4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+}
+
+// y = (x - mean) * rstd * w + b (LayerNorm) or x * rstd * w (RMSNorm, b
+// NULL), rstd = 1 / sqrt(var + eps) with var the mean of squares (of the
+// centred row for LayerNorm). mean (LayerNorm) and rstd per row are saved.
+template <int VPL, bool kLN>
+__global__ __launch_bounds__(kThreads) void norm_fwd_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            const float* __restrict__ b, float* __restrict__ y,
+                                                            float* __restrict__ mean, float* __restrict__ rstd,
+                                                            int64_t T, float eps) {
+  constexpr int D = 16 * VPL;
+  const int lane = threadIdx.x & 63, c = lane & 15;
+  float wv[VPL], bv[VPL];
+  load_cols<VPL>(w, c, wv);
+  if constexpr (kLN) load_cols<VPL>(b, c, bv);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * (kThreads / 16);
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4); t < T; t += stride) {
+    float v[VPL];
+    load_cols<VPL>(x + t * D, c, v);
+    float mu = 0.0f;
+    if constexpr (kLN) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) s += v[i];
+      mu = row16_sum(s) / static_cast<float>(D);
+    }
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const float d = v[i] - mu;
+      q += d * d;
+    }
+    const float r = 1.0f / sqrtf(row16_sum(q) / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      v[i] = (v[i] - mu) * r * wv[i];
+      if constexpr (kLN) v[i] += bv[i];
+    }
+    store_cols<VPL>(y + t * D, c, v);
+    if (c == 0) {
+      rstd[t] = r;
+      if constexpr (kLN) mean[t] = mu;
+    }
+  }
+}
+
+// dx = rstd (g - mean(g) - xh mean(g xh)) with g = dy w, xh the normalised
+// row (RMSNorm: no mean(g) term); per-workgroup partials of dw = sum dy xh
+// and db = sum dy, summed in a fixed order over the workgroup's rows.
+template <int VPL, bool kLN>
+__global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ mean,
+                                                            const float* __restrict__ rstd, float* __restrict__ dx,
+                                                            float* __restrict__ part, int64_t T) {
+  constexpr int D = 16 * VPL;
+  constexpr int G = kThreads / 16;  // row groups per workgroup
+  __shared__ float red[G][D];
+  const int lane = threadIdx.x & 63, c = lane & 15, grp = threadIdx.x >> 4;
+  float wv[VPL], dwa[VPL], dba[VPL];
+  load_cols<VPL>(w, c, wv);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) dwa[i] = dba[i] = 0.0f;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * G;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * G + grp; t < T; t += stride) {
+    float gy[VPL], xv[VPL];
+    load_cols<VPL>(dy + t * D, c, gy);
+    load_cols<VPL>(x + t * D, c, xv);
+    const float mu = kLN ? mean[t] : 0.0f, r = rstd[t];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      xv[i] = (xv[i] - mu) * r;  // xh
+      const float g = gy[i] * wv[i];
+      s1 += g;
+      s2 += g * xv[i];
+      dwa[i] += gy[i] * xv[i];
+      dba[i] += gy[i];
+    }
+    s2 = row16_sum(s2) / static_cast<float>(D);
+    s1 = kLN ? row16_sum(s1) / static_cast<float>(D) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) gy[i] = r * (gy[i] * wv[i] - s1 - xv[i] * s2);
+    store_cols<VPL>(dx + t * D, c, gy);
+  }
+  // the workgroup's G row groups, added in group order
+#pragma unroll
+  for (int k = 0; k < VPL / 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[grp][64 * k + 4 * c + e] = dwa[4 * k + e];
+  __syncthreads();
+  for (int j = threadIdx.x; j < D; j += kThreads) {
+    float a = 0.0f;
+    for (int q = 0; q < G; ++q) a += red[q][j];
+    part[static_cast<int64_t>(blockIdx.x) * D + j] = a;
+  }
+  if constexpr (kLN) {
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < VPL / 4; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[grp][64 * k + 4 * c + e] = dba[4 * k + e];
+    __syncthreads();
+    for (int j = threadIdx.x; j < D; j += kThreads) {
+      float a = 0.0f;
+      for (int q = 0; q < G; ++q) a += red[q][j];
+      part[static_cast<int64_t>(gridDim.x + blockIdx.x) * D + j] = a;
+    }
+  }
+}
+
+// out[j] = sum over n partial rows of part[., j], in row order.
+__global__ __launch_bounds__(kThreads) void col_sum_kernel(const float* __restrict__ part, int n, int D,
+                                                           float* __restrict__ out) {
+  const int j = blockIdx.x * kThreads + threadIdx.x;
+  if (j >= D) return;
+  float a = 0.0f;
+  for (int q = 0; q < n; ++q) a += part[static_cast<int64_t>(q) * D + j];
+  out[j] = a;
+}
+
+template <typename Fn>
+bool with_vpl(int D, Fn&& fn) {
+  switch (D) {
+    case 64: fn(std::integral_constant<int, 4>{}); return true;
+    case 128: fn(std::integral_constant<int, 8>{}); return true;
+    case 256: fn(std::integral_constant<int, 16>{}); return true;
+    case 512: fn(std::integral_constant<int, 32>{}); return true;
+    default: return false;
+  }
+}
+
 }  // namespace
+
+extern "C" int64_t agpt_norm_workspace_floats(int d_model) { return 2 * static_cast<int64_t>(kNormBlocks) * d_model; }
+
+extern "C" int agpt_norm_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
+                             int64_t T, int d_model, float eps, void* stream) {
+  if (T < 0) return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_fwd: T < 0");
+  if (T == 0) return AGPT_OK;
+  if (!x || !w || !y || !rstd || (b && !mean))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_fwd: null pointer");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || (b && !aligned16(b)))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_fwd: x, w, b, y must be 16-byte aligned");
+  const int64_t need = (T + kThreads / 16 - 1) / (kThreads / 16);
+  const int grid = static_cast<int>(need < kNormBlocks ? need : kNormBlocks);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool ok = with_vpl(d_model, [&](auto vc) {
+    constexpr int VPL = decltype(vc)::value;
+    if (b) hipLaunchKernelGGL((norm_fwd_kernel<VPL, true>), dim3(grid), dim3(kThreads), 0, st, x, w, b, y, mean, rstd, T, eps);
+    else hipLaunchKernelGGL((norm_fwd_kernel<VPL, false>), dim3(grid), dim3(kThreads), 0, st, x, w, b, y, mean, rstd, T, eps);
+  });
+  if (!ok) return agpt_internal_set_error(AGPT_ERR_UNSUPPORTED, "agpt_norm_fwd: d_model must be 64, 128, 256 or 512");
+  return launch_status("agpt_norm_fwd");
+}
+
+extern "C" int agpt_norm_bwd(const float* dy, const float* x, const float* w, const float* mean, const float* rstd,
+                             float* dx, float* dw, float* db, float* workspace, int64_t workspace_floats, int64_t T,
+                             int d_model, void* stream) {
+  if (T < 0) return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: T < 0");
+  if (!dy || !x || !w || !rstd || !dx || !dw || !workspace || (db && !mean))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: null pointer");
+  if (workspace_floats < agpt_norm_workspace_floats(d_model))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: workspace smaller than agpt_norm_workspace_floats");
+  if (!aligned16(dy) || !aligned16(x) || !aligned16(w) || !aligned16(dx))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: dy, x, w, dx must be 16-byte aligned");
+  const int64_t need = (T + kThreads / 16 - 1) / (kThreads / 16);
+  const int grid = static_cast<int>(need < 1 ? 1 : (need < kNormBlocks ? need : kNormBlocks));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool ok = with_vpl(d_model, [&](auto vc) {
+    constexpr int VPL = decltype(vc)::value;
+    if (db) hipLaunchKernelGGL((norm_bwd_kernel<VPL, true>), dim3(grid), dim3(kThreads), 0, st, dy, x, w, mean, rstd, dx, workspace, T);
+    else hipLaunchKernelGGL((norm_bwd_kernel<VPL, false>), dim3(grid), dim3(kThreads), 0, st, dy, x, w, mean, rstd, dx, workspace, T);
+  });
+  if (!ok) return agpt_internal_set_error(AGPT_ERR_UNSUPPORTED, "agpt_norm_bwd: d_model must be 64, 128, 256 or 512");
+  const int cgrid = (d_model + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(col_sum_kernel, dim3(cgrid), dim3(kThreads), 0, st, workspace, grid, d_model, dw);
+  if (db)
+    hipLaunchKernelGGL(col_sum_kernel, dim3(cgrid), dim3(kThreads), 0, st,
+                       workspace + static_cast<int64_t>(grid) * d_model, grid, d_model, db);
+  return launch_status("agpt_norm_bwd");
+}
 
 extern "C" int agpt_bias_rope(float* x, const float* bias, const int32_t* positions, const float* cos_t,
                               const float* sin_t, int rope_seq_len, int64_t T, int n_heads, int head_dim,

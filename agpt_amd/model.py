@@ -9,8 +9,9 @@ update of every parameter (one flat fp32 buffer, as the reference's
 d_weights). X = tok_emb[token]; positions enter through RoPE at depth - 1.
 
 Native (libagpt_attn.so): trie attention fwd/bwd, the bias + RoPE epilogue,
-the loss and RMSProp. The plain GEMMs are torch's (hipBLASLt), the norms and
-ReLU torch's elementwise kernels; torch autograd strings them together.
+the row norms, the loss and RMSProp. The plain GEMMs are torch's
+(hipBLASLt), ReLU and the residual adds torch's elementwise kernels; torch
+autograd strings them together.
 `norm="rms"` (BASELINE.json's C3 text) or `"layer"` (the reference code's
 LayerNorm, agpt_train.cu:4671). Norm eps is 1e-5: µGPT's is not in the
 reference (parity unpinned).
@@ -180,6 +181,24 @@ class _Attn(torch.autograd.Function):
         return dq, dk, dv, (ones @ dq)[0], (ones @ dk)[0], (ones @ dv)[0], None, None
 
 
+class _Norm(torch.autograd.Function):
+    """Row norm on the native kernels (agpt_norm_fwd / agpt_norm_bwd)."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, eps, layer):
+        x = x.contiguous()
+        y, mu, rs = block.norm_fwd(x, w.detach(), b.detach() if layer else None, eps)
+        ctx.save_for_backward(x, w, mu, rs)
+        ctx.layer = layer
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, mu, rs = ctx.saved_tensors
+        dx, dw, db = block.norm_bwd(dy.contiguous(), x, w.detach(), mu, rs, ctx.layer)
+        return dx, dw, db, None, None
+
+
 class _Loss(torch.autograd.Function):
     """Sum over queries of the per-query AGPT loss; the kernel's d_logits is
     the gradient of that sum (agpt_train.cu:4810-4830)."""
@@ -261,9 +280,7 @@ class TrieGPT:
         return out
 
     def _norm(self, x, w, b):
-        if self.cfg.norm == "rms":
-            return F.rms_norm(x, (x.shape[-1],), w, self.cfg.eps)
-        return F.layer_norm(x, (x.shape[-1],), w, b, self.cfg.eps)
+        return _Norm.apply(x, w, b, self.cfg.eps, self.cfg.norm == "layer")
 
     def loss(self, grp) -> torch.Tensor:
         """Forward over one planned batch: the summed per-query loss."""

@@ -1,7 +1,7 @@
 /*
  * agpt_block.h — C ABI of the kernels around the trie-attention path in one
  * training step (libagpt_attn.so, gfx950): the projection epilogue (bias +
- * RoPE) and the RMSProp update.
+ * RoPE), the row norms (RMSNorm / LayerNorm) and the RMSProp update.
  *
  * Shares the conventions of agpt_attn.h: int status (AGPT_OK = 0) with the
  * message in agpt_last_error(), DEVICE pointers owned by the caller, work
@@ -39,6 +39,28 @@ int agpt_bias_rope(float* x, const float* bias, const int32_t* positions, const 
  * momentum 0, centered False). grads are read only. */
 int agpt_rmsprop(float* params, const float* grads, float* sq_avg, float lr, float beta, float eps,
                  int64_t n, void* stream);
+
+/* Row norms over x [T, d_model] fp32 (d_model 64, 128, 256 or 512), the
+ * LN1 / LN2 / final-norm sites of agpt_train.cu:4671, 4826, 4800:
+ *   LayerNorm (b != NULL): y = (x - mean) rstd w + b, rstd = 1/sqrt(var + eps)
+ *   RMSNorm   (b == NULL): y = x rstd w,            rstd = 1/sqrt(mean(x^2) + eps)
+ * Saves mean [T] (LayerNorm only) and rstd [T] for the backward. Replaces
+ * µGPT's cuda_layer_norm_forward (extern, agpt_train.cu:50-52), which saves
+ * the normalised rows instead. */
+int agpt_norm_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
+                  int64_t T, int d_model, float eps, void* stream);
+
+/* Backward of agpt_norm_fwd: dx [T, d_model], dw [d_model], and db
+ * [d_model] when db != NULL (LayerNorm). dw / db are sums over rows in a
+ * fixed order (per-workgroup partials in `workspace`, at least
+ * agpt_norm_workspace_floats(d_model) floats, then a column sum): two calls
+ * give identical bytes. Replaces cuda_layer_norm_backward (agpt_train.cu:53-55). */
+int agpt_norm_bwd(const float* dy, const float* x, const float* w, const float* mean, const float* rstd,
+                  float* dx, float* dw, float* db, float* workspace, int64_t workspace_floats, int64_t T,
+                  int d_model, void* stream);
+
+/* Workspace floats agpt_norm_bwd needs for d_model. */
+int64_t agpt_norm_workspace_floats(int d_model);
 
 #ifdef __cplusplus
 }

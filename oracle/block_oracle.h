@@ -20,6 +20,14 @@ void oracle_bias_rope(float* x, const float* bias, const int32_t* positions, con
 void oracle_rmsprop(float* params, const float* grads, float* sq_avg, float lr, float beta, float eps,
                     int64_t n);
 
+/* LayerNorm (b != NULL) / RMSNorm (b == NULL) over rows of x [T, D]:
+ * two-pass mean and variance in double, rounded once to float for rstd. */
+void oracle_norm_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
+                     int64_t T, int D, float eps);
+/* The backward from the same saved mean / rstd, sums in double. */
+void oracle_norm_bwd(const float* dy, const float* x, const float* w, const float* mean, const float* rstd,
+                     float* dx, float* dw, float* db, int64_t T, int D);
+
 #ifdef __cplusplus
 }
 #endif

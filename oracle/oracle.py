@@ -185,3 +185,26 @@ def rmsprop(params, grads, sq_avg, lr, beta, eps):
     lib().oracle_rmsprop(_fp(p), _fp(g), _fp(s), C.c_float(lr), C.c_float(beta), C.c_float(eps),
                          C.c_int64(p.size))
     return p, s
+
+
+def norm_fwd(x, w, b, eps):
+    """LayerNorm (b given) / RMSNorm restated (block_oracle.c); returns (y, mean, rstd)."""
+    x = _f32(x)
+    T, D = x.shape
+    y = np.empty_like(x)
+    rs = np.empty(T, np.float32)
+    mu = np.empty(T, np.float32) if b is not None else None
+    lib().oracle_norm_fwd(_fp(x), _fp(_f32(w)), _fp(_f32(b)), _fp(y), _fp(mu), _fp(rs), C.c_int64(T), D,
+                          C.c_float(eps))
+    return y, mu, rs
+
+
+def norm_bwd(dy, x, w, mean, rstd, layer):
+    x = _f32(x)
+    T, D = x.shape
+    dx = np.empty_like(x)
+    dw = np.empty(D, np.float32)
+    db = np.empty(D, np.float32) if layer else None
+    lib().oracle_norm_bwd(_fp(_f32(dy)), _fp(x), _fp(_f32(w)), _fp(_f32(mean)), _fp(_f32(rstd)), _fp(dx),
+                          _fp(dw), _fp(db), C.c_int64(T), D)
+    return dx, dw, db

@@ -67,3 +67,30 @@ def test_rmsprop_matches_torch(beta, lr, eps):
         opt.step()
         np.testing.assert_allclose(p, pt.detach().numpy(), rtol=2e-6, atol=1e-6)  # a few ulp (fused forms)
         np.testing.assert_allclose(s, opt.state[pt]["square_avg"].numpy(), rtol=2e-6)
+
+
+@pytest.mark.parametrize("layer", [True, False])
+def test_norm_oracle_matches_torch_float64(layer):
+    """The row norms' restatement against torch's layer_norm / rms_norm and
+    autograd in float64 (library routines)."""
+    rng = np.random.default_rng(3)
+    T, D, eps = 37, 64, 1e-5
+    x = (rng.standard_normal((T, D)) * 2 + 0.5).astype(np.float32)
+    w = rng.standard_normal(D).astype(np.float32)
+    b = rng.standard_normal(D).astype(np.float32) if layer else None
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    y, mu, rs = ORC.norm_fwd(x, w, b, eps)
+    dx, dw, db = ORC.norm_bwd(dy, x, w, mu, rs, layer)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    if layer:
+        bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
+        yt = torch.nn.functional.layer_norm(xt, (D,), wt, bt, eps)
+    else:
+        yt = torch.nn.functional.rms_norm(xt, (D,), wt, eps)
+    yt.backward(torch.tensor(dy, dtype=torch.float64))
+    np.testing.assert_allclose(y, yt.detach().numpy(), rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(dw, wt.grad.numpy(), rtol=1e-5, atol=1e-5)
+    if layer:
+        np.testing.assert_allclose(db, bt.grad.numpy(), rtol=1e-6, atol=1e-6)

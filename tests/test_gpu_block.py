@@ -118,3 +118,31 @@ def test_c3_step_from_radix_files(gpu, tmp_path):
     assert (a.flat.grad == b.flat.grad).all()
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("D", [64, 128, 256, 512])
+@pytest.mark.parametrize("layer", [True, False])
+def test_norm_matches_oracle(gpu, D, layer):
+    import torch
+
+    from agpt_amd import block
+
+    rng = np.random.default_rng(D + layer)
+    T = 5003
+    x = (rng.standard_normal((T, D)) * 1.5 + 0.3).astype(np.float32)
+    w = rng.standard_normal(D).astype(np.float32)
+    b = rng.standard_normal(D).astype(np.float32) if layer else None
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    y0, mu0, rs0 = ORC.norm_fwd(x, w, b, 1e-5)
+    to = lambda a: None if a is None else torch.from_numpy(a).to(gpu)
+    y, mu, rs = block.norm_fwd(to(x), to(w), to(b), 1e-5)
+    np.testing.assert_allclose(y.cpu().numpy(), y0, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(rs.cpu().numpy(), rs0, rtol=1e-6)
+    dx0, dw0, db0 = ORC.norm_bwd(dy, x, w, mu0, rs0, layer)
+    dx, dw, db = block.norm_bwd(to(dy), to(x), to(w), mu, rs, layer)
+    np.testing.assert_allclose(dx.cpu().numpy(), dx0, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(dw.cpu().numpy(), dw0, rtol=1e-4, atol=1e-3)  # sums of 5003 rows
+    if layer:
+        np.testing.assert_allclose(db.cpu().numpy(), db0, rtol=1e-4, atol=1e-3)
+    dx2, dw2, _ = block.norm_bwd(to(dy), to(x), to(w), mu, rs, layer)
+    assert torch.equal(dx, dx2) and torch.equal(dw, dw2)  # fixed-order sums
