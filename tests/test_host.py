@@ -196,3 +196,32 @@ def test_trie_next_counts_match_corpus_scan(n, order, vocab, depth):
         got = dict(zip(tr.next_tok[a:b].tolist(), tr.next_val[a:b].tolist()))
         assert got == hist[key]
         assert list(tr.next_tok[a:b]) == sorted(got)
+
+
+def test_new_entry_points_reject_bad_arguments_without_a_device():
+    """The loss, epilogue, norm and RMSProp entry points check their
+    arguments before any device call: bad sizes and null pointers come back
+    as AGPT_ERR_INVALID_ARG / AGPT_ERR_UNSUPPORTED with a message."""
+    lib = _native.attn_lib()
+    nul = [None] * 11
+
+    def msg():
+        return lib.agpt_last_error().decode()
+
+    assert lib.agpt_loss_per_query(*nul, -1, 65, 0.0, 1.0, 0, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_loss_per_query(*nul, 5, 0, 0.0, 1.0, 0, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_loss_per_query(*nul, 5, 65, 0.0, 1.0, 0, None) == _native.AGPT_ERR_INVALID_ARG
+    assert "null pointer" in msg()
+    assert lib.agpt_loss_per_query(*nul, 0, 65, 0.0, 1.0, 0, None) == _native.AGPT_OK  # empty batch
+    assert lib.agpt_bias_rope(None, None, None, None, None, 0, 4, 2, 6, None) == _native.AGPT_ERR_INVALID_ARG
+    assert "multiple of 4" in msg()
+    assert lib.agpt_bias_rope(None, None, None, None, None, 0, 4, 2, 8, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_rmsprop(None, None, None, 1e-3, 0.9, 1e-8, 10, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_rmsprop(None, None, None, 1e-3, 0.9, 1e-8, 0, None) == _native.AGPT_OK
+    assert lib.agpt_norm_fwd(None, None, None, None, None, None, 3, 128, 1e-5, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_norm_workspace_floats(128) == 2 * 1024 * 128
+    assert lib.agpt_norm_bwd(*[None] * 9, 0, 3, 128, None) == _native.AGPT_ERR_INVALID_ARG
+    mass = np.zeros(3, np.float32)
+    i = lambda *v: np.array(v, np.int32).ctypes.data_as(C.POINTER(C.c_int32))
+    assert lib.agpt_loss_mass_weights(i(0), i(5), i(2), i(0, 2), 1, 2, 9,
+                                      mass.ctypes.data_as(C.POINTER(C.c_float))) == _native.AGPT_ERR_INVALID_ARG
