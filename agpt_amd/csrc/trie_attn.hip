@@ -433,7 +433,43 @@ __global__ __launch_bounds__(256) void trie_bwd_chunk_kernel(PlanDev pl, const f
 // Σ over tiles u in (t, tile(end_a - 1)] of slot depth(a)-1, in tile order,
 // using chunk sums for whole chunks. Then seeds, inverse RoPE, final write.
 // ---------------------------------------------------------------------------
-template <int HD>
+// VW consecutive columns per lane: one walk over the tiles covers 64 * VW
+// columns (D = 512 in one walk with VW = 8, 16-byte loads).
+template <int VW>
+__device__ __forceinline__ void ld_cols(const float* __restrict__ p, float (&x)[VW]) {
+  if constexpr (VW == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    x[0] = v.x;
+    x[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VW; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(p + i);
+      x[i] = v.x;
+      x[i + 1] = v.y;
+      x[i + 2] = v.z;
+      x[i + 3] = v.w;
+    }
+  }
+}
+template <int VW>
+__device__ __forceinline__ void st_cols(float* __restrict__ p, const float (&x)[VW]) {
+  if constexpr (VW == 2) {
+    *reinterpret_cast<float2*>(p) = float2{x[0], x[1]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < VW; i += 4) *reinterpret_cast<float4*>(p + i) = float4{x[i], x[i + 1], x[i + 2], x[i + 3]};
+  }
+}
+template <int VW>
+__device__ __forceinline__ void add_cols(float (&x)[VW], const float* __restrict__ p) {
+  float y[VW];
+  ld_cols<VW>(p, y);
+#pragma unroll
+  for (int i = 0; i < VW; ++i) x[i] += y[i];
+}
+
+template <int HD, int VW>
 __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
     PlanDev pl, float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ Pk,
     const float* __restrict__ Pv, const float* __restrict__ Ck, const float* __restrict__ Cv,
@@ -451,52 +487,40 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
     if (a < s) break;  // deeper-first scan: everything above is outside tile t
     const int u_last = static_cast<int>((pl.end[a] - 1) / pl.tile);
     const int pos = rope.cos_t ? rope_pos(k + 1, rope.seq_len) : 0;
-    for (int col0 = lane * 2; col0 < D; col0 += 128) {
-      float2 sk = *reinterpret_cast<const float2*>(dK + a * D + col0);
-      float2 sv = *reinterpret_cast<const float2*>(dV + a * D + col0);
+    for (int col0 = lane * VW; col0 < D; col0 += 64 * VW) {
+      float sk[VW], sv[VW];
+      ld_cols<VW>(dK + a * D + col0, sk);
+      ld_cols<VW>(dV + a * D + col0, sv);
       int u = t + 1;
       while (u <= u_last) {
         const int c = u / kChunkTiles;
         if (u == c * kChunkTiles && u + kChunkTiles - 1 <= u_last) {
           const int64_t o = (static_cast<int64_t>(c) * pl.max_depth + k) * D + col0;
-          const float2 ck = *reinterpret_cast<const float2*>(Ck + o);
-          const float2 cv = *reinterpret_cast<const float2*>(Cv + o);
-          sk.x += ck.x;
-          sk.y += ck.y;
-          sv.x += cv.x;
-          sv.y += cv.y;
+          add_cols<VW>(sk, Ck + o);
+          add_cols<VW>(sv, Cv + o);
           u += kChunkTiles;
         } else {
           const int64_t o = (static_cast<int64_t>(pl.pref_off[u]) + k) * D + col0;
-          const float2 pk = *reinterpret_cast<const float2*>(Pk + o);
-          const float2 pv = *reinterpret_cast<const float2*>(Pv + o);
-          sk.x += pk.x;
-          sk.y += pk.y;
-          sv.x += pv.x;
-          sv.y += pv.y;
+          add_cols<VW>(sk, Pk + o);
+          add_cols<VW>(sv, Pv + o);
           ++u;
         }
       }
-      if (acc_dk) {
-        const float2 x = *reinterpret_cast<const float2*>(acc_dk + a * D + col0);
-        sk.x += x.x;
-        sk.y += x.y;
-      }
-      if (acc_dv) {
-        const float2 x = *reinterpret_cast<const float2*>(acc_dv + a * D + col0);
-        sv.x += x.x;
-        sv.y += x.y;
-      }
+      if (acc_dk) add_cols<VW>(sk, acc_dk + a * D + col0);
+      if (acc_dv) add_cols<VW>(sv, acc_dv + a * D + col0);
       if (rope.cos_t) {
-        const int j = col0 % HD;  // even: pair (j, j+1) of the head
-        const float c = rope.cos_t[pos * HD + j];
-        const float sn = rope.sin_t[pos * HD + j];
-        const float x0 = sk.x, x1 = sk.y;
-        sk.x = x0 * c + x1 * sn;
-        sk.y = -x0 * sn + x1 * c;
+#pragma unroll
+        for (int p = 0; p < VW; p += 2) {
+          const int j = (col0 + p) % HD;  // even: pair (j, j+1) of the head
+          const float c = rope.cos_t[pos * HD + j];
+          const float sn = rope.sin_t[pos * HD + j];
+          const float x0 = sk[p], x1 = sk[p + 1];
+          sk[p] = x0 * c + x1 * sn;
+          sk[p + 1] = -x0 * sn + x1 * c;
+        }
       }
-      *reinterpret_cast<float2*>(dK + a * D + col0) = sk;
-      *reinterpret_cast<float2*>(dV + a * D + col0) = sv;
+      st_cols<VW>(dK + a * D + col0, sk);
+      st_cols<VW>(dV + a * D + col0, sv);
     }
   }
 }
@@ -1301,9 +1325,15 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
     hipLaunchKernelGGL(trie_bwd_chunk_kernel, dim3(h->n_chunks), dim3(256), 0, st, plan_dev(h), h->d_Pk,
                        h->d_Pv, h->d_Ck, h->d_Cv, D);
     pm.mark(3);
-    hipLaunchKernelGGL((trie_bwd_reduce_kernel<HD>), dim3(h->n_tiles - 1), dim3(256), 0, st, plan_dev(h),
-                       dk, dv, h->d_Pk, h->d_Pv, h->d_Ck, h->d_Cv, acc_dk, acc_dv, rope,
-                       h->cfg.n_heads);
+    auto reduce = [&](auto vw) {
+      constexpr int VW = decltype(vw)::value;
+      hipLaunchKernelGGL((trie_bwd_reduce_kernel<HD, VW>), dim3(h->n_tiles - 1), dim3(256), 0, st, plan_dev(h),
+                         dk, dv, h->d_Pk, h->d_Pv, h->d_Ck, h->d_Cv, acc_dk, acc_dv, rope, h->cfg.n_heads);
+    };
+    // the widest column group that divides D (16-byte loads need VW >= 4)
+    if (D % 512 == 0) reduce(std::integral_constant<int, 8>{});
+    else if (D % 256 == 0) reduce(std::integral_constant<int, 4>{});
+    else reduce(std::integral_constant<int, 2>{});
   } else {
     pm.mark(3);
   }
