@@ -45,9 +45,10 @@ def param_shapes(cfg: ModelConfig) -> list[tuple[str, tuple[int, ...]]]:
     D, Fd, V = cfg.d_model, cfg.d_ff, cfg.vocab
     out = [("tok_emb", (V, D))]
     for l in range(cfg.n_layers):
+        # wq, wk, wv (and bq, bk, bv) adjacent: one [3D, D] projection
         out += [(f"n1_w{l}", (D,)), (f"n1_b{l}", (D,)),
-                (f"wq{l}", (D, D)), (f"bq{l}", (D,)), (f"wk{l}", (D, D)), (f"bk{l}", (D,)),
-                (f"wv{l}", (D, D)), (f"bv{l}", (D,)), (f"wo{l}", (D, D)), (f"bo{l}", (D,)),
+                (f"wq{l}", (D, D)), (f"wk{l}", (D, D)), (f"wv{l}", (D, D)),
+                (f"bq{l}", (D,)), (f"bk{l}", (D,)), (f"bv{l}", (D,)), (f"wo{l}", (D, D)), (f"bo{l}", (D,)),
                 (f"n2_w{l}", (D,)), (f"n2_b{l}", (D,)),
                 (f"w1{l}", (Fd, D)), (f"b1{l}", (Fd,)), (f"w2{l}", (D, Fd)), (f"b2{l}", (D,))]
     out += [("nf_w", (D,)), ("nf_b", (D,)), ("w_out", (V, D)), ("b_out", (V,))]
@@ -156,11 +157,16 @@ class _Attn(torch.autograd.Function):
     i.e. with respect to the projections' outputs (before their bias)."""
 
     @staticmethod
-    def forward(ctx, ql, kl, vl, bq, bk, bv, m, grp):
+    def forward(ctx, qkv, bqkv, m, grp):
         att, batch = grp
-        q = block.bias_rope_(ql.detach().clone(), bq.detach(), batch.positions, m.cos, m.sin, m.cfg.n_heads)
-        k = block.bias_rope_(kl.detach().clone(), bk.detach(), batch.positions, m.cos, m.sin, m.cfg.n_heads)
-        v = block.bias_rope_(vl.detach().clone(), bv.detach(), n_heads=m.cfg.n_heads)
+        D = m.cfg.d_model
+        qkv, bqkv = qkv.detach(), bqkv.detach()
+
+        def col(i):  # a contiguous copy of column block i of the [T, 3D] projection
+            return qkv[:, i * D:(i + 1) * D].clone(memory_format=torch.contiguous_format)
+        q = block.bias_rope_(col(0), bqkv[:D], batch.positions, m.cos, m.sin, m.cfg.n_heads)
+        k = block.bias_rope_(col(1), bqkv[D:2 * D], batch.positions, m.cos, m.sin, m.cfg.n_heads)
+        v = block.bias_rope_(col(2), bqkv[2 * D:], n_heads=m.cfg.n_heads)
         m._hook()
         o, lse = att.forward(q, k, v)
         m._hook()
@@ -175,10 +181,11 @@ class _Attn(torch.autograd.Function):
         m._hook()
         dq, dk, dv = ctx.att.backward(q, k, v, o, lse, d_o.contiguous(), rope=(m.cos, m.sin))
         m._hook()
-        # Bias gradients as one matrix-vector product each (a column sum over
-        # ~1M rows as a plain reduction keeps only D outputs in flight).
-        ones = torch.ones(1, dq.shape[0], device=dq.device, dtype=dq.dtype)
-        return dq, dk, dv, (ones @ dq)[0], (ones @ dk)[0], (ones @ dv)[0], None, None
+        dqkv = torch.cat((dq, dk, dv), dim=1)
+        # The bias gradient as one matrix-vector product (a column sum over
+        # ~1M rows as a plain reduction keeps only 3D outputs in flight).
+        ones = torch.ones(1, dqkv.shape[0], device=dq.device, dtype=dq.dtype)
+        return dqkv, (ones @ dqkv)[0], None, None
 
 
 class _Norm(torch.autograd.Function):
@@ -272,11 +279,18 @@ class TrieGPT:
             self.attn_hook()
 
     def params(self) -> dict[str, torch.Tensor]:
-        out, off = {}, 0
+        """Views into the flat buffer by name, plus wqkv{l} [3D, D] and
+        bqkv{l} [3D] over the adjacent q, k, v blocks."""
+        out, off, at = {}, 0, {}
         for name, shape in param_shapes(self.cfg):
             n = int(np.prod(shape))
             out[name] = self.flat[off:off + n].view(shape)
+            at[name] = off
             off += n
+        D = self.cfg.d_model
+        for l in range(self.cfg.n_layers):
+            out[f"wqkv{l}"] = self.flat[at[f"wq{l}"]:at[f"wq{l}"] + 3 * D * D].view(3 * D, D)
+            out[f"bqkv{l}"] = self.flat[at[f"bq{l}"]:at[f"bq{l}"] + 3 * D]
         return out
 
     def _norm(self, x, w, b):
@@ -291,8 +305,7 @@ class TrieGPT:
         x = F.one_hot(batch.tokens, cfg.vocab).to(torch.float32) @ P["tok_emb"]
         for l in range(cfg.n_layers):
             n1 = self._norm(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
-            o = _Attn.apply(F.linear(n1, P[f"wq{l}"]), F.linear(n1, P[f"wk{l}"]), F.linear(n1, P[f"wv{l}"]),
-                            P[f"bq{l}"], P[f"bk{l}"], P[f"bv{l}"], self, grp)
+            o = _Attn.apply(F.linear(n1, P[f"wqkv{l}"]), P[f"bqkv{l}"], self, grp)
             x = x + F.linear(o, P[f"wo{l}"], P[f"bo{l}"])
             n2 = self._norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
             x = x + F.linear(F.relu(F.linear(n2, P[f"w1{l}"], P[f"b1{l}"])), P[f"w2{l}"], P[f"b2{l}"])
