@@ -188,6 +188,31 @@ class _Attn(torch.autograd.Function):
         return dqkv, (ones @ dqkv)[0], None, None
 
 
+def _col_sum(dy: torch.Tensor, rows: int = 64) -> torch.Tensor:
+    """Sum over the rows of dy [T, V] in two wide stages: [T/rows, rows*V]
+    summed over its first dimension, then the rows blocks (a plain column
+    sum of a narrow matrix, V = 65, leaves the reduction nearly serial)."""
+    T, V = dy.shape
+    m = T // rows * rows
+    out = dy[:m].view(-1, rows * V).sum(0).view(rows, V).sum(0)
+    return out + dy[m:].sum(0) if m < T else out
+
+
+class _OutProj(torch.autograd.Function):
+    """The output projection x·Woutᵀ + b_out (hipBLASLt's fused bias) whose
+    backward sums the narrow bias gradient with _col_sum."""
+
+    @staticmethod
+    def forward(ctx, x, w, b):
+        ctx.save_for_backward(x, w)
+        return F.linear(x, w, b)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        return dy @ w, dy.t() @ x, _col_sum(dy)
+
+
 class _Norm(torch.autograd.Function):
     """Row norm on the native kernels (agpt_norm_fwd / agpt_norm_bwd)."""
 
@@ -309,7 +334,7 @@ class TrieGPT:
             x = x + F.linear(o, P[f"wo{l}"], P[f"bo{l}"])
             n2 = self._norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
             x = x + F.linear(F.relu(F.linear(n2, P[f"w1{l}"], P[f"b1{l}"])), P[f"w2{l}"], P[f"b2{l}"])
-        logits = F.linear(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
+        logits = _OutProj.apply(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
         return _Loss.apply(logits, batch)
 
     def step(self) -> torch.Tensor:
