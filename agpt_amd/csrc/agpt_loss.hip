@@ -12,10 +12,9 @@
 //     (1 + lambda H/log V) (x mass_weights[q]); an endpoint without counts
 //     gets loss 0 and grad = p.
 //
-// Layout: LPR lanes own one row (4 for V <= 128, 16 for V <= 512, else 64)
-// of the rows staged in LDS. The row
-// is read once and written once: the loss is HBM-bound at 8V bytes per
-// query. The count entries of an endpoint are applied one at a time in
+// Layout: LPR lanes own one row (4 for V <= 32, 8 for V <= 128, 16 for
+// V <= 512, else 64) of the rows staged in LDS. The row is read once and
+// written once: the loss is HBM-bound at 8V bytes per query. The count entries of an endpoint are applied one at a time in
 // their stored order (as the reference's single thread does), so repeated
 // tokens and the loss sum come out in the same order.
 
@@ -51,19 +50,15 @@ constexpr int kRowMirror = 0x140, kRowHalfMirror = 0x141, kQuadRev = 0x1B, kQuad
 
 template <int LPR, typename T>
 __device__ __forceinline__ T row_sum(T v) {
-  if constexpr (LPR >= 16) {
-    v += dpp<kRowMirror>(v);
-    v += dpp<kRowHalfMirror>(v);
-  }
+  if constexpr (LPR >= 16) v += dpp<kRowMirror>(v);
+  if constexpr (LPR >= 8) v += dpp<kRowHalfMirror>(v);
   v += dpp<kQuadRev>(v);
   return v + dpp<kQuadSwap>(v);
 }
 template <int LPR>
 __device__ __forceinline__ float row_max(float v) {
-  if constexpr (LPR >= 16) {
-    v = fmaxf(v, dpp<kRowMirror>(v));
-    v = fmaxf(v, dpp<kRowHalfMirror>(v));
-  }
+  if constexpr (LPR >= 16) v = fmaxf(v, dpp<kRowMirror>(v));
+  if constexpr (LPR >= 8) v = fmaxf(v, dpp<kRowHalfMirror>(v));
   v = fmaxf(v, dpp<kQuadRev>(v));
   return fmaxf(v, dpp<kQuadSwap>(v));
 }
@@ -104,15 +99,16 @@ __device__ __forceinline__ T group_sum(T v) {
   return v;
 }
 
-// Columns of a row over its LPR lanes: 4-lane rows give each lane VPL
-// consecutive columns; wider rows interleave them (lane c: c, c + LPR, ...),
-// which keeps the LDS reads of rows whose length is a multiple of 64 off a
-// shared bank.
+// Columns of a row over its LPR lanes: rows of 4 or 8 lanes give each lane
+// VPL consecutive columns; wider rows interleave them (lane c: c, c + LPR,
+// ...), which keeps the LDS reads of rows whose length is a multiple of 64
+// off a shared bank.
 template <int LPR, int VPL>
 struct Cols {
-  static __device__ __forceinline__ int col(int c, int i) { return LPR == 4 ? c * VPL + i : c + LPR * i; }
-  static __device__ __forceinline__ int owner(int j) { return LPR == 4 ? j / VPL : j % LPR; }
-  static __device__ __forceinline__ int slot(int j) { return LPR == 4 ? j % VPL : j / LPR; }
+  static constexpr bool kSlice = LPR <= 8;
+  static __device__ __forceinline__ int col(int c, int i) { return kSlice ? c * VPL + i : c + LPR * i; }
+  static __device__ __forceinline__ int owner(int j) { return kSlice ? j / VPL : j % LPR; }
+  static __device__ __forceinline__ int slot(int j) { return kSlice ? j % VPL : j / LPR; }
 };
 
 // Value of column j of the row held by this lane's group (j uniform over the
@@ -378,18 +374,19 @@ void launch(const float* logits, const int* q2n, const int* qoff, const int* rid
                      qoff, rids, toks, coff, ctok, cval, mass, dl, lo, T_q, V, RB, lambda, iw, ce);
 }
 
-// Lanes per row: 4 up to 128 columns, 16 up to 512, a wave up to 1024; VPL
-// columns per lane.
+// Lanes per row: 4 up to 32 columns, 8 up to 128, 16 up to 512, a wave up
+// to 1024; VPL columns per lane.
 template <typename... A>
 bool dispatch(int V, A... a) {
   if (V <= 16) launch<4, 4>(a...);
   else if (V <= 32) launch<4, 8>(a...);
-  else if (V <= 48) launch<4, 12>(a...);
-  else if (V <= 64) launch<4, 16>(a...);
-  else if (V <= 68) launch<4, 17>(a...);
-  else if (V <= 80) launch<4, 20>(a...);
-  else if (V <= 96) launch<4, 24>(a...);
-  else if (V <= 128) launch<4, 32>(a...);
+  else if (V <= 40) launch<8, 5>(a...);
+  else if (V <= 48) launch<8, 6>(a...);
+  else if (V <= 64) launch<8, 8>(a...);
+  else if (V <= 72) launch<8, 9>(a...);
+  else if (V <= 80) launch<8, 10>(a...);
+  else if (V <= 96) launch<8, 12>(a...);
+  else if (V <= 128) launch<8, 16>(a...);
   else if (V <= 192) launch<16, 12>(a...);
   else if (V <= 256) launch<16, 16>(a...);
   else if (V <= 384) launch<16, 24>(a...);
