@@ -198,19 +198,53 @@ def _col_sum(dy: torch.Tensor, rows: int = 64) -> torch.Tensor:
     return out + dy[m:].sum(0) if m < T else out
 
 
-class _OutProj(torch.autograd.Function):
-    """The output projection x·Woutᵀ + b_out (hipBLASLt's fused bias) whose
-    backward sums the narrow bias gradient with _col_sum."""
+def _wgrad(dy: torch.Tensor, x: torch.Tensor, splits: int = 64) -> torch.Tensor:
+    """dyᵀ·x [out, in] over T ≈ 1M rows, split along the rows into `splits`
+    batched products summed in order: a single product has only out·in/1024
+    output tiles (16 for 128 x 128) to spread over 256 CUs."""
+    T = dy.shape[0]
+    m = T // splits * splits
+    if m == 0:
+        return dy.t() @ x
+    a = dy[:m].view(splits, m // splits, dy.shape[1]).transpose(1, 2)  # [S, out, T/S]
+    b = x[:m].contiguous().view(splits, m // splits, x.shape[1])       # [S, T/S, in]
+    w = torch.bmm(a, b).sum(0)
+    return w + dy[m:].t() @ x[m:] if m < T else w
+
+
+class _Lin(torch.autograd.Function):
+    """x·Wᵀ (+ b, hipBLASLt's fused bias epilogue). Backward: dx = dy·W, the
+    weight gradient by _wgrad, the bias gradient by _col_sum when the output
+    is narrow (the vocabulary) and a plain column sum otherwise."""
 
     @staticmethod
     def forward(ctx, x, w, b):
         ctx.save_for_backward(x, w)
+        ctx.has_b = b is not None
         return F.linear(x, w, b)
 
     @staticmethod
     def backward(ctx, dy):
         x, w = ctx.saved_tensors
-        return dy @ w, dy.t() @ x, _col_sum(dy)
+        db = None
+        if ctx.has_b:
+            db = _col_sum(dy) if dy.shape[1] < 128 else dy.sum(0)
+        return dy @ w, _wgrad(dy, x), db
+
+
+class _Embed(torch.autograd.Function):
+    """X = onehot(token)·E; dE = onehotᵀ·dX by _wgrad (V x D outputs)."""
+
+    @staticmethod
+    def forward(ctx, tokens, emb):
+        oh = F.one_hot(tokens, emb.shape[0]).to(emb.dtype)
+        ctx.save_for_backward(oh)
+        return oh @ emb
+
+    @staticmethod
+    def backward(ctx, dx):
+        (oh,) = ctx.saved_tensors
+        return None, _wgrad(oh, dx)
 
 
 class _Norm(torch.autograd.Function):
@@ -325,16 +359,17 @@ class TrieGPT:
         """Forward over one planned batch: the summed per-query loss."""
         P, cfg = self.params(), self.cfg
         batch = grp[1]
-        # X = onehot(token) · tok_emb: the backward is one product onehotᵀ · dX
+        # X = onehot(token) · tok_emb: the backward is a product onehotᵀ · dX
         # (the gather's backward would scatter-add 1M rows into 65).
-        x = F.one_hot(batch.tokens, cfg.vocab).to(torch.float32) @ P["tok_emb"]
+        x = _Embed.apply(batch.tokens, P["tok_emb"])
         for l in range(cfg.n_layers):
             n1 = self._norm(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
-            o = _Attn.apply(F.linear(n1, P[f"wqkv{l}"]), P[f"bqkv{l}"], self, grp)
-            x = x + F.linear(o, P[f"wo{l}"], P[f"bo{l}"])
+            o = _Attn.apply(_Lin.apply(n1, P[f"wqkv{l}"], None), P[f"bqkv{l}"], self, grp)
+            x = x + _Lin.apply(o, P[f"wo{l}"], P[f"bo{l}"])
             n2 = self._norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
-            x = x + F.linear(F.relu(F.linear(n2, P[f"w1{l}"], P[f"b1{l}"])), P[f"w2{l}"], P[f"b2{l}"])
-        logits = _OutProj.apply(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
+            h = F.relu(_Lin.apply(n2, P[f"w1{l}"], P[f"b1{l}"]))
+            x = x + _Lin.apply(h, P[f"w2{l}"], P[f"b2{l}"])
+        logits = _Lin.apply(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
         return _Loss.apply(logits, batch)
 
     def step(self) -> torch.Tensor:
