@@ -82,6 +82,7 @@ LOSS_SYMBOLS = {
 # include/agpt_block.h (same library as the attention entry points).
 BLOCK_SYMBOLS = {
     "agpt_bias_rope": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_int, C.c_int, _vp]),
+    "agpt_bias_rope_split": (C.c_int, [_vp] * 5 + [C.c_int, C.c_int64, C.c_int, C.c_int, _vp, _vp, _vp, _vp]),
     "agpt_rmsprop": (C.c_int, [_vp, _vp, _vp, C.c_float, C.c_float, C.c_float, C.c_int64, _vp]),
     "agpt_norm_fwd": (C.c_int, [_vp] * 6 + [C.c_int64, C.c_int, C.c_float, _vp]),
     "agpt_norm_bwd": (C.c_int, [_vp] * 9 + [C.c_int64, C.c_int64, C.c_int, _vp]),

@@ -33,6 +33,23 @@ def bias_rope_(x, bias=None, positions=None, cos_t=None, sin_t=None, n_heads: in
     return x
 
 
+def bias_rope_split(qkv, bias=None, positions=None, cos_t=None, sin_t=None, n_heads: int = 1):
+    """qkv [T, 3D] -> contiguous (q, k, v) [T, D]: bias on all, RoPE on q, k."""
+    import torch
+    if not qkv.is_cuda or not qkv.is_contiguous() or qkv.dim() != 2 or qkv.shape[1] % 3:
+        raise ValueError("qkv must be a contiguous CUDA [T, 3D] tensor")
+    T, D3 = qkv.shape
+    D = D3 // 3
+    if D % n_heads:
+        raise ValueError("D must be a multiple of n_heads")
+    q, k, v = (torch.empty(T, D, device=qkv.device, dtype=qkv.dtype) for _ in range(3))
+    seq = 0 if cos_t is None else cos_t.shape[0]
+    _native.check(_native.attn_lib().agpt_bias_rope_split(
+        _ptr(qkv), _ptr(bias), _ptr(positions), _ptr(cos_t), _ptr(sin_t), seq, T, n_heads, D // n_heads,
+        _ptr(q), _ptr(k), _ptr(v), _stream(qkv)))
+    return q, k, v
+
+
 def rmsprop_(params, grads, sq_avg, lr: float, beta: float, eps: float = 1e-8):
     """In place: sq_avg = beta sq_avg + (1-beta) g^2; params -= lr g / (sqrt(sq_avg) + eps)."""
     for t in (params, grads, sq_avg):

@@ -72,6 +72,44 @@ __global__ __launch_bounds__(kThreads) void bias_rope_kernel(float* __restrict__
   }
 }
 
+// The [T, 3D] projection (q | k | v column blocks) split into contiguous
+// [T, D] outputs: bias added to all three, RoPE on q and k.
+__global__ __launch_bounds__(kThreads) void bias_rope_split_kernel(
+    const float* __restrict__ x, const float* __restrict__ bias, const int32_t* __restrict__ pos,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int seq, int64_t T, int D, int hd,
+    float* __restrict__ q, float* __restrict__ k, float* __restrict__ v) {
+  const int qpr = 3 * D / 4;  // quads per input row
+  const int64_t n = T * qpr;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int64_t t = i / qpr;
+    const int col3 = static_cast<int>(i - t * qpr) * 4;
+    const int part = col3 / D, col = col3 - part * D;
+    float4 w = *reinterpret_cast<const float4*>(x + t * 3 * D + col3);
+    if (bias != nullptr) {
+      const float4 b = *reinterpret_cast<const float4*>(bias + col3);
+      w.x += b.x;
+      w.y += b.y;
+      w.z += b.z;
+      w.w += b.w;
+    }
+    if (part < 2 && cos_t != nullptr) {
+      int p = pos[t];
+      p = p < 0 ? 0 : (p > seq - 1 ? seq - 1 : p);
+      const int j = col % hd;
+      const float c0 = cos_t[static_cast<int64_t>(p) * hd + j], s0 = sin_t[static_cast<int64_t>(p) * hd + j];
+      const float c1 = cos_t[static_cast<int64_t>(p) * hd + j + 2], s1 = sin_t[static_cast<int64_t>(p) * hd + j + 2];
+      const float x0 = w.x, x1 = w.y, x2 = w.z, x3 = w.w;
+      w.x = x0 * c0 - x1 * s0;
+      w.y = x0 * s0 + x1 * c0;
+      w.z = x2 * c1 - x3 * s1;
+      w.w = x2 * s1 + x3 * c1;
+    }
+    float* out = part == 0 ? q : (part == 1 ? k : v);
+    *reinterpret_cast<float4*>(out + t * D + col) = w;
+  }
+}
+
 __device__ __forceinline__ void rms_one(float& p, float g, float& s, float lr, float beta, float eps) {
   s = beta * s + (1.0f - beta) * (g * g);
   p -= lr * (g / (sqrtf(s) + eps));
@@ -337,6 +375,24 @@ extern "C" int agpt_bias_rope(float* x, const float* bias, const int32_t* positi
                      static_cast<hipStream_t>(stream), x, bias, positions, cos_t, sin_t, rope_seq_len, T, D,
                      head_dim);
   return launch_status("agpt_bias_rope");
+}
+
+extern "C" int agpt_bias_rope_split(const float* qkv, const float* bias, const int32_t* positions,
+                                    const float* cos_t, const float* sin_t, int rope_seq_len, int64_t T,
+                                    int n_heads, int head_dim, float* q, float* k, float* v, void* stream) {
+  if (T < 0 || n_heads < 1 || head_dim < 4 || head_dim % 4 != 0)
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG,
+                                   "agpt_bias_rope_split: T < 0, n_heads < 1 or head_dim not a multiple of 4");
+  if (T == 0) return AGPT_OK;
+  if (!qkv || !q || !k || !v || (cos_t && (!sin_t || !positions || rope_seq_len < 1)))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_bias_rope_split: null pointer or rope_seq_len < 1");
+  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v) || (bias && !aligned16(bias)))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_bias_rope_split: buffers must be 16-byte aligned");
+  const int D = n_heads * head_dim;
+  hipLaunchKernelGGL(bias_rope_split_kernel, dim3(grid_for(T * (3 * D / 4))), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), qkv, bias, positions, cos_t, sin_t, rope_seq_len, T, D,
+                     head_dim, q, k, v);
+  return launch_status("agpt_bias_rope_split");
 }
 
 extern "C" int agpt_rmsprop(float* params, const float* grads, float* sq_avg, float lr, float beta, float eps,

@@ -159,14 +159,8 @@ class _Attn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, qkv, bqkv, m, grp):
         att, batch = grp
-        D = m.cfg.d_model
-        qkv, bqkv = qkv.detach(), bqkv.detach()
-
-        def col(i):  # a contiguous copy of column block i of the [T, 3D] projection
-            return qkv[:, i * D:(i + 1) * D].clone(memory_format=torch.contiguous_format)
-        q = block.bias_rope_(col(0), bqkv[:D], batch.positions, m.cos, m.sin, m.cfg.n_heads)
-        k = block.bias_rope_(col(1), bqkv[D:2 * D], batch.positions, m.cos, m.sin, m.cfg.n_heads)
-        v = block.bias_rope_(col(2), bqkv[2 * D:], n_heads=m.cfg.n_heads)
+        q, k, v = block.bias_rope_split(qkv.detach().contiguous(), bqkv.detach(), batch.positions, m.cos, m.sin,
+                                        m.cfg.n_heads)
         m._hook()
         o, lse = att.forward(q, k, v)
         m._hook()

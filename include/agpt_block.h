@@ -31,6 +31,15 @@ int agpt_bias_rope(float* x, const float* bias, const int32_t* positions, const 
                    const float* sin_t, int rope_seq_len, int64_t T, int n_heads, int head_dim,
                    void* stream);
 
+/* The same epilogue over a fused projection: qkv [T, 3D] holds the q | k | v
+ * column blocks of one GEMM (D = n_heads*head_dim), bias [3D] or NULL.
+ * Writes contiguous q, k, v [T, D]: bias on all three, RoPE (as
+ * agpt_bias_rope) on q and k. One pass instead of three copies and three
+ * in-place passes. */
+int agpt_bias_rope_split(const float* qkv, const float* bias, const int32_t* positions,
+                         const float* cos_t, const float* sin_t, int rope_seq_len, int64_t T,
+                         int n_heads, int head_dim, float* q, float* k, float* v, void* stream);
+
 /* RMSProp without momentum over n fp32 parameters:
  *     s = beta s + (1 - beta) g^2,   p -= lr g / (sqrt(s) + eps).
  * Replaces cuda_rmsprop_bulk (the µGPT extern of agpt_train.cu:69, called at

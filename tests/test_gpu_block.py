@@ -38,6 +38,28 @@ def test_bias_rope_matches_oracle(gpu, H, hd, rope, bias):
     np.testing.assert_allclose(xt.cpu().numpy(), want, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("H,hd,bias", [(8, 16, True), (2, 64, False)])
+def test_bias_rope_split_matches_oracle(gpu, H, hd, bias):
+    import torch
+
+    from agpt_amd import block
+
+    rng = np.random.default_rng(7 * H + hd)
+    T, seq, D = 2049, 32, H * hd
+    x = rng.standard_normal((T, 3 * D)).astype(np.float32)
+    b = rng.standard_normal(3 * D).astype(np.float32) if bias else None
+    pos = rng.integers(0, seq + 3, T).astype(np.int32)
+    cos_t, sin_t = ORC.rope_table(seq, hd)
+    p = np.clip(pos, 0, seq - 1)
+    want = [ORC.bias_rope(np.ascontiguousarray(x[:, i * D:(i + 1) * D]), None if b is None else b[i * D:(i + 1) * D],
+                          p, cos_t if i < 2 else None, sin_t if i < 2 else None, H, hd) for i in range(3)]
+    c, s = (torch.from_numpy(t).to(gpu) for t in (cos_t, sin_t))
+    got = block.bias_rope_split(torch.from_numpy(x).to(gpu), None if b is None else torch.from_numpy(b).to(gpu),
+                                torch.from_numpy(pos).to(gpu), c, s, H)
+    for g_, w_ in zip(got, want):
+        np.testing.assert_allclose(g_.cpu().numpy(), w_, rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("n", [1, 4, 1001, 1 << 20])
 def test_rmsprop_matches_oracle(gpu, n):
     import torch
