@@ -226,6 +226,23 @@ class _Lin(torch.autograd.Function):
         return dy @ w, _wgrad(dy, x), db
 
 
+class _LinRelu(torch.autograd.Function):
+    """relu(x·Wᵀ + b) with bias and ReLU in the GEMM's epilogue; backward
+    masks dy by the saved output (> 0), then as _Lin."""
+
+    @staticmethod
+    def forward(ctx, x, w, b):
+        h = torch._addmm_activation(b, x, w.t(), use_gelu=False)
+        ctx.save_for_backward(x, w, h)
+        return h
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, h = ctx.saved_tensors
+        dh = torch.where(h > 0, dy, torch.zeros((), device=dy.device, dtype=dy.dtype))
+        return dh @ w, _wgrad(dh, x), dh.sum(0)
+
+
 class _Embed(torch.autograd.Function):
     """X = onehot(token)·E; dE = onehotᵀ·dX by _wgrad (V x D outputs)."""
 
@@ -361,7 +378,7 @@ class TrieGPT:
             o = _Attn.apply(_Lin.apply(n1, P[f"wqkv{l}"], None), P[f"bqkv{l}"], self, grp)
             x = x + _Lin.apply(o, P[f"wo{l}"], P[f"bo{l}"])
             n2 = self._norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
-            h = F.relu(_Lin.apply(n2, P[f"w1{l}"], P[f"b1{l}"]))
+            h = _LinRelu.apply(n2, P[f"w1{l}"], P[f"b1{l}"])
             x = x + _Lin.apply(h, P[f"w2{l}"], P[f"b2{l}"])
         logits = _Lin.apply(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
         return _Loss.apply(logits, batch)
