@@ -393,8 +393,9 @@ class TrieGPT:
             lv = self.loss(grp)
             lv.backward()
             total += lv.detach()
-        with torch.no_grad():
-            block.rmsprop_(self.flat.data, self.flat.grad, self.sq_avg, self.lr, self.beta, self.eps)
+        if self.flat.grad is not None:  # no planned rows: nothing to update
+            with torch.no_grad():
+                block.rmsprop_(self.flat.data, self.flat.grad, self.sq_avg, self.lr, self.beta, self.eps)
         return total
 
     def save(self, path: str) -> None:

@@ -116,3 +116,19 @@ def test_model_batch_from_files_equals_batch_from_trie(tmp_path):
     assert (b1.parent == b2.parent).all()
     assert all(torch.equal(x, y) for x, y in zip(b1.loss_args, b2.loss_args))
     assert torch.equal(b1.mass, b2.mass) and torch.equal(b1.positions, b2.positions)
+
+
+def test_subtree_groups_cover_the_rows_in_order():
+    from agpt_amd import model
+
+    tok = trie.markov_corpus(4000, 2, 6, 1.1, seed=11)
+    tr = trie.build_trie(tok, 12, counts=True)
+    roots = set(np.flatnonzero(tr.parent < 0).tolist()) | {tr.n_nodes}
+    for max_rows in (1, 100, 1000, 1 << 30):
+        g = model.subtree_groups(tr, max_rows)
+        assert g[0][0] == 0 and g[-1][1] == tr.n_nodes
+        assert all(a < b and b == c for (a, b), (c, _) in zip(g, g[1:] + [(tr.n_nodes, 0)]))
+        assert all(a in roots and b in roots for a, b in g)  # whole root-child subtrees
+        assert all(b - a <= max_rows or len([r for r in roots if a < r < b]) == 0 for a, b in g)
+    empty = trie.build_trie(np.zeros(1, np.int32), 4, counts=True)
+    assert model.subtree_groups(empty, 10) == []
