@@ -994,7 +994,13 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
   }
   if (h->variant == 6) {
     HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_sched), kSchedBytes));
-    h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", 24));
+    // Up to 24 tiles per claim (the carry's reach), but at least ~8 chunks
+    // per CU: a plan of few tiles (C5: 2048) would otherwise leave most
+    // workgroups without a chunk.
+    int cus = 256;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
+    const int dflt = static_cast<int>(std::min<int64_t>(24, std::max<int64_t>(1, n_tiles / (8 * std::max(cus, 1)))));
+    h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", dflt));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
   }
   if (h->carry) {

@@ -23,6 +23,7 @@ VARIANTS = {
     "block_split": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUSED": "0"},
     "block_no_carry_chunk2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CARRY": "0", "AGPT_ATTN_CHUNK": "2"},
     "block_chunk2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHUNK": "2"},
+    "block_chunk24": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHUNK": "24"},
     "block_hg4_all_heads_chunk1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4", "AGPT_ATTN_UH": "4",
                                    "AGPT_ATTN_FUH": "4", "AGPT_ATTN_CHUNK": "1"},
     "block_fwd_one_head_units": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUH": "1"},
