@@ -289,13 +289,32 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
 }
 
 // out[j] = sum over n partial rows of part[., j], in row order.
+// out[j] = sum over q of part[q][j], D a multiple of 64. One workgroup per 64
+// columns: 16 lanes x float4 across the columns, 16 row slots down the rows
+// (slot s sums rows s, s+16, ...), then slot 0 folds the 16 slot sums in
+// order, so the result does not depend on timing.
+constexpr int kColSlots = kThreads / 16;
 __global__ __launch_bounds__(kThreads) void col_sum_kernel(const float* __restrict__ part, int n, int D,
                                                            float* __restrict__ out) {
-  const int j = blockIdx.x * kThreads + threadIdx.x;
-  if (j >= D) return;
-  float a = 0.0f;
-  for (int q = 0; q < n; ++q) a += part[static_cast<int64_t>(q) * D + j];
-  out[j] = a;
+  __shared__ float4 red[kColSlots][16];
+  const int c4 = threadIdx.x & 15, slot = threadIdx.x >> 4;
+  const float4* p = reinterpret_cast<const float4*>(part) + blockIdx.x * 16 + c4;
+  const int D4 = D / 4;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+  for (int q = slot; q < n; q += kColSlots) {
+    const float4 v = p[static_cast<int64_t>(q) * D4];
+    a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+  }
+  red[slot][c4] = a;
+  __syncthreads();
+  if (slot == 0) {
+    for (int t = 1; t < kColSlots; ++t) {
+      const float4 v = red[t][c4];
+      a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+    }
+    reinterpret_cast<float4*>(out)[blockIdx.x * 16 + c4] = a;
+  }
 }
 
 template <typename Fn>
@@ -341,8 +360,10 @@ extern "C" int agpt_norm_bwd(const float* dy, const float* x, const float* w, co
     return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: null pointer");
   if (workspace_floats < agpt_norm_workspace_floats(d_model))
     return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: workspace smaller than agpt_norm_workspace_floats");
-  if (!aligned16(dy) || !aligned16(x) || !aligned16(w) || !aligned16(dx))
-    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: dy, x, w, dx must be 16-byte aligned");
+  if (!aligned16(dy) || !aligned16(x) || !aligned16(w) || !aligned16(dx) || !aligned16(dw) ||
+      (db && !aligned16(db)) || !aligned16(workspace))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG,
+                                   "agpt_norm_bwd: dy, x, w, dx, dw, db and workspace must be 16-byte aligned");
   const int64_t need = (T + kThreads / 16 - 1) / (kThreads / 16);
   const int grid = static_cast<int>(need < 1 ? 1 : (need < kNormBlocks ? need : kNormBlocks));
   const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -352,7 +373,7 @@ extern "C" int agpt_norm_bwd(const float* dy, const float* x, const float* w, co
     else hipLaunchKernelGGL((norm_bwd_kernel<VPL, false>), dim3(grid), dim3(kThreads), 0, st, dy, x, w, mean, rstd, dx, workspace, T);
   });
   if (!ok) return agpt_internal_set_error(AGPT_ERR_UNSUPPORTED, "agpt_norm_bwd: d_model must be 64, 128, 256 or 512");
-  const int cgrid = (d_model + kThreads - 1) / kThreads;
+  const int cgrid = d_model / 64;
   hipLaunchKernelGGL(col_sum_kernel, dim3(cgrid), dim3(kThreads), 0, st, workspace, grid, d_model, dw);
   if (db)
     hipLaunchKernelGGL(col_sum_kernel, dim3(cgrid), dim3(kThreads), 0, st,

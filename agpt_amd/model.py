@@ -228,7 +228,7 @@ class _Lin(torch.autograd.Function):
 
 class _LinRelu(torch.autograd.Function):
     """relu(x·Wᵀ + b) with bias and ReLU in the GEMM's epilogue; backward
-    masks dy by the saved output (> 0), then as _Lin."""
+    masks dy by the saved output (> 0, one pass), then as _Lin."""
 
     @staticmethod
     def forward(ctx, x, w, b):
@@ -239,7 +239,7 @@ class _LinRelu(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x, w, h = ctx.saved_tensors
-        dh = torch.where(h > 0, dy, torch.zeros((), device=dy.device, dtype=dy.dtype))
+        dh = torch.ops.aten.threshold_backward(dy, h, 0.0)
         return dh @ w, _wgrad(dh, x), dh.sum(0)
 
 

@@ -63,7 +63,8 @@ int agpt_norm_fwd(const float* x, const float* w, const float* b, float* y, floa
  * [d_model] when db != NULL (LayerNorm). dw / db are sums over rows in a
  * fixed order (per-workgroup partials in `workspace`, at least
  * agpt_norm_workspace_floats(d_model) floats, then a column sum): two calls
- * give identical bytes. Replaces cuda_layer_norm_backward (agpt_train.cu:53-55). */
+ * give identical bytes. All pointers 16-byte aligned. Replaces
+ * cuda_layer_norm_backward (agpt_train.cu:53-55). */
 int agpt_norm_bwd(const float* dy, const float* x, const float* w, const float* mean, const float* rstd,
                   float* dx, float* dw, float* db, float* workspace, int64_t workspace_floats, int64_t T,
                   int d_model, void* stream);
