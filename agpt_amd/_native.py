@@ -85,7 +85,7 @@ BLOCK_SYMBOLS = {
     "agpt_bias_rope_split": (C.c_int, [_vp] * 5 + [C.c_int, C.c_int64, C.c_int, C.c_int, _vp, _vp, _vp, _vp]),
     "agpt_rmsprop": (C.c_int, [_vp, _vp, _vp, C.c_float, C.c_float, C.c_float, C.c_int64, _vp]),
     "agpt_norm_fwd": (C.c_int, [_vp] * 6 + [C.c_int64, C.c_int, C.c_float, _vp]),
-    "agpt_norm_bwd": (C.c_int, [_vp] * 9 + [C.c_int64, C.c_int64, C.c_int, _vp]),
+    "agpt_norm_bwd": (C.c_int, [_vp] * 10 + [C.c_int64, C.c_int64, C.c_int, _vp]),
     "agpt_norm_workspace_floats": (C.c_int64, [C.c_int]),
 }
 

@@ -76,15 +76,18 @@ def norm_fwd(x, w, b=None, eps: float = 1e-5):
     return y, mean, rstd
 
 
-def norm_bwd(dy, x, w, mean, rstd, layer: bool):
-    """Returns (dx, dw, db or None) of norm_fwd."""
+def norm_bwd(dy, x, w, mean, rstd, layer: bool, dres=None):
+    """Returns (dx, dw, db or None) of norm_fwd; dres [T, D] (a residual
+    stream's gradient at x) is added into dx in the same pass."""
     import torch
     T, D = x.shape
+    if dres is not None and (not dres.is_cuda or not dres.is_contiguous() or dres.shape != x.shape):
+        raise ValueError("dres must be a contiguous CUDA tensor shaped as x")
     lib = _native.attn_lib()
     ws = torch.empty(lib.agpt_norm_workspace_floats(D), device=x.device, dtype=torch.float32)
     dx = torch.empty_like(x)
     dw = torch.empty(D, device=x.device, dtype=torch.float32)
     db = torch.empty(D, device=x.device, dtype=torch.float32) if layer else None
-    _native.check(lib.agpt_norm_bwd(_ptr(dy), _ptr(x), _ptr(w), _ptr(mean), _ptr(rstd), _ptr(dx), _ptr(dw),
+    _native.check(lib.agpt_norm_bwd(_ptr(dy), _ptr(dres), _ptr(x), _ptr(w), _ptr(mean), _ptr(rstd), _ptr(dx), _ptr(dw),
                                     _ptr(db), _ptr(ws), ws.numel(), T, D, _stream(x)))
     return dx, dw, db

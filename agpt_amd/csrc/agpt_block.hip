@@ -225,9 +225,12 @@ __global__ __launch_bounds__(kThreads) void norm_fwd_kernel(const float* __restr
 
 // dx = rstd (g - mean(g) - xh mean(g xh)) with g = dy w, xh the normalised
 // row (RMSNorm: no mean(g) term); per-workgroup partials of dw = sum dy xh
-// and db = sum dy, summed in a fixed order over the workgroup's rows.
-template <int VPL, bool kLN>
-__global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+// and db = sum dy, summed in a fixed order over the workgroup's rows. kRes:
+// dx also adds dres (the gradient the residual stream brings to x).
+template <int VPL, bool kLN, bool kRes>
+__global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restrict__ dy,
+                                                            const float* __restrict__ dres,
+                                                            const float* __restrict__ x,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ mean,
                                                             const float* __restrict__ rstd, float* __restrict__ dx,
@@ -260,6 +263,12 @@ __global__ __launch_bounds__(kThreads) void norm_bwd_kernel(const float* __restr
     s1 = kLN ? row16_sum(s1) / static_cast<float>(D) : 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) gy[i] = r * (gy[i] * wv[i] - s1 - xv[i] * s2);
+    if constexpr (kRes) {
+      float rv[VPL];
+      load_cols<VPL>(dres + t * D, c, rv);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) gy[i] += rv[i];
+    }
     store_cols<VPL>(dx + t * D, c, gy);
   }
   // the workgroup's G row groups, added in group order
@@ -352,7 +361,7 @@ extern "C" int agpt_norm_fwd(const float* x, const float* w, const float* b, flo
   return launch_status("agpt_norm_fwd");
 }
 
-extern "C" int agpt_norm_bwd(const float* dy, const float* x, const float* w, const float* mean, const float* rstd,
+extern "C" int agpt_norm_bwd(const float* dy, const float* dres, const float* x, const float* w, const float* mean, const float* rstd,
                              float* dx, float* dw, float* db, float* workspace, int64_t workspace_floats, int64_t T,
                              int d_model, void* stream) {
   if (T < 0) return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: T < 0");
@@ -360,17 +369,20 @@ extern "C" int agpt_norm_bwd(const float* dy, const float* x, const float* w, co
     return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: null pointer");
   if (workspace_floats < agpt_norm_workspace_floats(d_model))
     return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_norm_bwd: workspace smaller than agpt_norm_workspace_floats");
-  if (!aligned16(dy) || !aligned16(x) || !aligned16(w) || !aligned16(dx) || !aligned16(dw) ||
+  if (!aligned16(dy) || (dres && !aligned16(dres)) || !aligned16(x) || !aligned16(w) || !aligned16(dx) || !aligned16(dw) ||
       (db && !aligned16(db)) || !aligned16(workspace))
     return agpt_internal_set_error(AGPT_ERR_INVALID_ARG,
-                                   "agpt_norm_bwd: dy, x, w, dx, dw, db and workspace must be 16-byte aligned");
+                                   "agpt_norm_bwd: dy, dres, x, w, dx, dw, db and workspace must be 16-byte aligned");
   const int64_t need = (T + kThreads / 16 - 1) / (kThreads / 16);
   const int grid = static_cast<int>(need < 1 ? 1 : (need < kNormBlocks ? need : kNormBlocks));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const bool ok = with_vpl(d_model, [&](auto vc) {
     constexpr int VPL = decltype(vc)::value;
-    if (db) hipLaunchKernelGGL((norm_bwd_kernel<VPL, true>), dim3(grid), dim3(kThreads), 0, st, dy, x, w, mean, rstd, dx, workspace, T);
-    else hipLaunchKernelGGL((norm_bwd_kernel<VPL, false>), dim3(grid), dim3(kThreads), 0, st, dy, x, w, mean, rstd, dx, workspace, T);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, st, dy, dres, x, w, mean, rstd, dx, workspace, T);
+    };
+    if (db) dres ? go(norm_bwd_kernel<VPL, true, true>) : go(norm_bwd_kernel<VPL, true, false>);
+    else dres ? go(norm_bwd_kernel<VPL, false, true>) : go(norm_bwd_kernel<VPL, false, false>);
   });
   if (!ok) return agpt_internal_set_error(AGPT_ERR_UNSUPPORTED, "agpt_norm_bwd: d_model must be 64, 128, 256 or 512");
   const int cgrid = d_model / 64;

@@ -276,6 +276,30 @@ class _Norm(torch.autograd.Function):
         return dx, dw, db, None, None
 
 
+class _NormRes(torch.autograd.Function):
+    """(norm(x), x) for an x that also continues as the residual stream: the
+    backward adds the stream's gradient into dx inside the norm kernel
+    (agpt_norm_bwd's dres), so autograd has no add of its own at x."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, eps, layer):
+        ctx.set_materialize_grads(False)
+        x = x.contiguous()
+        y, mu, rs = block.norm_fwd(x, w.detach(), b.detach() if layer else None, eps)
+        ctx.save_for_backward(x, w, mu, rs)
+        ctx.layer = layer
+        return y, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dy, dres):
+        x, w, mu, rs = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(x)
+        dx, dw, db = block.norm_bwd(dy.contiguous(), x, w.detach(), mu, rs, ctx.layer,
+                                    None if dres is None else dres.contiguous())
+        return dx, dw, db, None, None
+
+
 class _Loss(torch.autograd.Function):
     """Sum over queries of the per-query AGPT loss; the kernel's d_logits is
     the gradient of that sum (agpt_train.cu:4810-4830)."""
@@ -366,6 +390,9 @@ class TrieGPT:
     def _norm(self, x, w, b):
         return _Norm.apply(x, w, b, self.cfg.eps, self.cfg.norm == "layer")
 
+    def _norm_res(self, x, w, b):
+        return _NormRes.apply(x, w, b, self.cfg.eps, self.cfg.norm == "layer")
+
     def loss(self, grp) -> torch.Tensor:
         """Forward over one planned batch: the summed per-query loss."""
         P, cfg = self.params(), self.cfg
@@ -374,10 +401,12 @@ class TrieGPT:
         # (the gather's backward would scatter-add 1M rows into 65).
         x = _Embed.apply(batch.tokens, P["tok_emb"])
         for l in range(cfg.n_layers):
-            n1 = self._norm(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
+            # x feeds the norm and the residual add: _NormRes passes it on so
+            # both gradients meet inside the norm backward.
+            n1, x = self._norm_res(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
             o = _Attn.apply(_Lin.apply(n1, P[f"wqkv{l}"], None), P[f"bqkv{l}"], self, grp)
             x = x + _Lin.apply(o, P[f"wo{l}"], P[f"bo{l}"])
-            n2 = self._norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
+            n2, x = self._norm_res(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
             h = _LinRelu.apply(n2, P[f"w1{l}"], P[f"b1{l}"])
             x = x + _Lin.apply(h, P[f"w2{l}"], P[f"b2{l}"])
         logits = _Lin.apply(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])

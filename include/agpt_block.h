@@ -60,12 +60,14 @@ int agpt_norm_fwd(const float* x, const float* w, const float* b, float* y, floa
                   int64_t T, int d_model, float eps, void* stream);
 
 /* Backward of agpt_norm_fwd: dx [T, d_model], dw [d_model], and db
- * [d_model] when db != NULL (LayerNorm). dw / db are sums over rows in a
+ * [d_model] when db != NULL (LayerNorm). dres [T, d_model] (NULL = none) is
+ * added into dx: the gradient a residual stream brings to the same x, so the
+ * caller needs no separate add where x also feeds a residual connection. dw / db are sums over rows in a
  * fixed order (per-workgroup partials in `workspace`, at least
  * agpt_norm_workspace_floats(d_model) floats, then a column sum): two calls
  * give identical bytes. All pointers 16-byte aligned. Replaces
  * cuda_layer_norm_backward (agpt_train.cu:53-55). */
-int agpt_norm_bwd(const float* dy, const float* x, const float* w, const float* mean, const float* rstd,
+int agpt_norm_bwd(const float* dy, const float* dres, const float* x, const float* w, const float* mean, const float* rstd,
                   float* dx, float* dw, float* db, float* workspace, int64_t workspace_floats, int64_t T,
                   int d_model, void* stream);
 

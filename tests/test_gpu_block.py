@@ -168,3 +168,8 @@ def test_norm_matches_oracle(gpu, D, layer):
         np.testing.assert_allclose(db.cpu().numpy(), db0, rtol=1e-4, atol=1e-3)
     dx2, dw2, _ = block.norm_bwd(to(dy), to(x), to(w), mu, rs, layer)
     assert torch.equal(dx, dx2) and torch.equal(dw, dw2)  # fixed-order sums
+    # dres (a residual stream's gradient at x) is added into dx only
+    r = rng.standard_normal((T, D)).astype(np.float32)
+    dxr, dwr, dbr = block.norm_bwd(to(dy), to(x), to(w), mu, rs, layer, dres=to(r))
+    np.testing.assert_allclose(dxr.cpu().numpy(), dx0 + r, rtol=1e-4, atol=1e-5)
+    assert torch.equal(dwr, dw) and (not layer or torch.equal(dbr, db))

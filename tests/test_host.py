@@ -220,7 +220,7 @@ def test_new_entry_points_reject_bad_arguments_without_a_device():
     assert lib.agpt_rmsprop(None, None, None, 1e-3, 0.9, 1e-8, 0, None) == _native.AGPT_OK
     assert lib.agpt_norm_fwd(None, None, None, None, None, None, 3, 128, 1e-5, None) == _native.AGPT_ERR_INVALID_ARG
     assert lib.agpt_norm_workspace_floats(128) == 2 * 1024 * 128
-    assert lib.agpt_norm_bwd(*[None] * 9, 0, 3, 128, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_norm_bwd(*[None] * 10, 0, 3, 128, None) == _native.AGPT_ERR_INVALID_ARG
     mass = np.zeros(3, np.float32)
     i = lambda *v: np.array(v, np.int32).ctypes.data_as(C.POINTER(C.c_int32))
     assert lib.agpt_loss_mass_weights(i(0), i(5), i(2), i(0, 2), 1, 2, 9,
