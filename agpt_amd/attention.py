@@ -153,6 +153,10 @@ class TrieAttention:
         if out is None:
             out = tuple(torch.empty(self.n_nodes, self.d_model, device=q.device,
                                     dtype=torch.float32) for _ in range(3))
+        for t in out:
+            if (not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous()
+                    or tuple(t.shape) != (self.n_nodes, self.d_model)):
+                raise ValueError("out must be three contiguous float32 CUDA [n_nodes, d_model] tensors")
         dq, dk, dv = out
         opts = self._opts(scale, rope, stream, events)
         N.check(self._lib.agpt_attn_bwd(self._h, q.data_ptr(), k.data_ptr(), v.data_ptr(),

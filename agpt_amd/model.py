@@ -152,34 +152,45 @@ class TrieBatch:
         self.loss_args = [to(q2n), to(qoff), to(rid), to(token), to(coff), to(ctok), to(cval)]
 
 
-class _Attn(torch.autograd.Function):
-    """Projection epilogue + trie attention; gradients come back pre-RoPE,
-    i.e. with respect to the projections' outputs (before their bias)."""
+class _QKVAttn(torch.autograd.Function):
+    """x -> fused Q|K|V projection x·Wᵀ ([T, 3D]) -> bias + RoPE epilogue ->
+    trie attention. The backward writes dq, dk, dv (pre-RoPE, i.e. gradients
+    of the projection's output before its bias) into one [3, T, D] buffer and
+    forms dx as three accumulating products dq·Wq + dk·Wk + dv·Wv, so the
+    three gradients are never concatenated into [T, 3D]."""
 
     @staticmethod
-    def forward(ctx, qkv, bqkv, m, grp):
+    def forward(ctx, x, w, b, m, grp):
         att, batch = grp
-        q, k, v = block.bias_rope_split(qkv.detach().contiguous(), bqkv.detach(), batch.positions, m.cos, m.sin,
-                                        m.cfg.n_heads)
+        qkv = F.linear(x, w)
+        q, k, v = block.bias_rope_split(qkv, b.detach(), batch.positions, m.cos, m.sin, m.cfg.n_heads)
+        del qkv
         m._hook()
         o, lse = att.forward(q, k, v)
         m._hook()
-        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.save_for_backward(x, w, q, k, v, o, lse)
         ctx.m, ctx.att = m, att
         return o
 
     @staticmethod
     def backward(ctx, d_o):
-        q, k, v, o, lse = ctx.saved_tensors
+        x, w, q, k, v, o, lse = ctx.saved_tensors
         m = ctx.m
+        T, D = q.shape
+        d3 = torch.empty(3, T, D, device=q.device, dtype=q.dtype)
         m._hook()
-        dq, dk, dv = ctx.att.backward(q, k, v, o, lse, d_o.contiguous(), rope=(m.cos, m.sin))
+        ctx.att.backward(q, k, v, o, lse, d_o.contiguous(), rope=(m.cos, m.sin), out=(d3[0], d3[1], d3[2]))
         m._hook()
-        dqkv = torch.cat((dq, dk, dv), dim=1)
-        # The bias gradient as one matrix-vector product (a column sum over
-        # ~1M rows as a plain reduction keeps only 3D outputs in flight).
-        ones = torch.ones(1, dqkv.shape[0], device=dq.device, dtype=dq.dtype)
-        return dqkv, (ones @ dqkv)[0], None, None
+        w = w.detach()
+        dx = d3[0] @ w[:D]
+        dx.addmm_(d3[1], w[D:2 * D])
+        dx.addmm_(d3[2], w[2 * D:])
+        dw = torch.cat([_wgrad(d3[j], x) for j in range(3)])
+        # The bias gradient as matrix-vector products (a column sum over ~1M
+        # rows as a plain reduction keeps only D outputs in flight).
+        ones = torch.ones(1, T, device=q.device, dtype=q.dtype)
+        db = torch.matmul(ones, d3).view(3 * D)
+        return dx, dw, db, None, None
 
 
 def _col_sum(dy: torch.Tensor, rows: int = 64) -> torch.Tensor:
@@ -404,7 +415,7 @@ class TrieGPT:
             # x feeds the norm and the residual add: _NormRes passes it on so
             # both gradients meet inside the norm backward.
             n1, x = self._norm_res(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
-            o = _Attn.apply(_Lin.apply(n1, P[f"wqkv{l}"], None), P[f"bqkv{l}"], self, grp)
+            o = _QKVAttn.apply(n1, P[f"wqkv{l}"], P[f"bqkv{l}"], self, grp)
             x = x + _Lin.apply(o, P[f"wo{l}"], P[f"bo{l}"])
             n2, x = self._norm_res(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
             h = _LinRelu.apply(n2, P[f"w1{l}"], P[f"b1{l}"])
