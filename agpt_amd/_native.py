@@ -87,6 +87,7 @@ BLOCK_SYMBOLS = {
     "agpt_norm_fwd": (C.c_int, [_vp] * 6 + [C.c_int64, C.c_int, C.c_float, _vp]),
     "agpt_norm_bwd": (C.c_int, [_vp] * 10 + [C.c_int64, C.c_int64, C.c_int, _vp]),
     "agpt_norm_workspace_floats": (C.c_int64, [C.c_int]),
+    "agpt_relu_bwd": (C.c_int, [_vp] * 5 + [C.c_int64, C.c_int64, C.c_int, _vp]),
 }
 
 TRIE_SYMBOLS = {

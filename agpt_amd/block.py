@@ -63,6 +63,25 @@ def rmsprop_(params, grads, sq_avg, lr: float, beta: float, eps: float = 1e-8):
         _stream(params)))
 
 
+def relu_bwd(dy, h):
+    """Returns (dh, db): dh = dy where h > 0 else 0 ([T, width]), db = its
+    column sum [width] (fixed order), in one pass."""
+    import torch
+    for t in (dy, h):
+        if not t.is_cuda or not t.is_contiguous() or t.dim() != 2 or t.dtype != torch.float32:
+            raise ValueError("dy and h must be contiguous float32 CUDA [T, width] tensors")
+    if dy.shape != h.shape:
+        raise ValueError("dy and h must have the same shape")
+    T, W = dy.shape
+    lib = _native.attn_lib()
+    ws = torch.empty(lib.agpt_norm_workspace_floats(W), device=dy.device, dtype=torch.float32)
+    dh = torch.empty_like(dy)
+    db = torch.empty(W, device=dy.device, dtype=torch.float32)
+    _native.check(lib.agpt_relu_bwd(_ptr(dy), _ptr(h), _ptr(dh), _ptr(db), _ptr(ws), ws.numel(), T, W,
+                                    _stream(dy)))
+    return dh, db
+
+
 def norm_fwd(x, w, b=None, eps: float = 1e-5):
     """LayerNorm (b given) or RMSNorm of the rows of x [T, D]; returns
     (y, mean or None, rstd)."""

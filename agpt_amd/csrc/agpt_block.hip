@@ -326,6 +326,43 @@ __global__ __launch_bounds__(kThreads) void col_sum_kernel(const float* __restri
   }
 }
 
+// dh = dy where h > 0, else 0 (the ReLU's backward through its output h);
+// per-workgroup partials of db = sum over rows of dh, in a fixed order. dh
+// may alias dy (each thread reads a row's slice before it writes it).
+template <int VPL>
+__global__ __launch_bounds__(kThreads) void relu_bwd_kernel(const float* dy, const float* __restrict__ h, float* dh,
+                                                            float* __restrict__ part, int64_t T) {
+  constexpr int D = 16 * VPL;
+  constexpr int G = kThreads / 16;  // row groups per workgroup
+  __shared__ float red[G][D];
+  const int c = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  float dba[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) dba[i] = 0.0f;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * G;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * G + grp; t < T; t += stride) {
+    float gy[VPL], hv[VPL];
+    load_cols<VPL>(dy + t * D, c, gy);
+    load_cols<VPL>(h + t * D, c, hv);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      gy[i] = hv[i] > 0.0f ? gy[i] : 0.0f;
+      dba[i] += gy[i];
+    }
+    store_cols<VPL>(dh + t * D, c, gy);
+  }
+#pragma unroll
+  for (int k = 0; k < VPL / 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[grp][64 * k + 4 * c + e] = dba[4 * k + e];
+  __syncthreads();
+  for (int j = threadIdx.x; j < D; j += kThreads) {
+    float a = 0.0f;
+    for (int q = 0; q < G; ++q) a += red[q][j];
+    part[static_cast<int64_t>(blockIdx.x) * D + j] = a;
+  }
+}
+
 template <typename Fn>
 bool with_vpl(int D, Fn&& fn) {
   switch (D) {
@@ -391,6 +428,27 @@ extern "C" int agpt_norm_bwd(const float* dy, const float* dres, const float* x,
     hipLaunchKernelGGL(col_sum_kernel, dim3(cgrid), dim3(kThreads), 0, st,
                        workspace + static_cast<int64_t>(grid) * d_model, grid, d_model, db);
   return launch_status("agpt_norm_bwd");
+}
+
+extern "C" int agpt_relu_bwd(const float* dy, const float* h, float* dh, float* db, float* workspace,
+                             int64_t workspace_floats, int64_t T, int width, void* stream) {
+  if (T < 0) return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_relu_bwd: T < 0");
+  if (!dy || !h || !dh || !db || !workspace)
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_relu_bwd: null pointer");
+  if (workspace_floats < agpt_norm_workspace_floats(width))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_relu_bwd: workspace smaller than agpt_norm_workspace_floats");
+  if (!aligned16(dy) || !aligned16(h) || !aligned16(dh) || !aligned16(db) || !aligned16(workspace))
+    return agpt_internal_set_error(AGPT_ERR_INVALID_ARG, "agpt_relu_bwd: dy, h, dh, db and workspace must be 16-byte aligned");
+  const int64_t need = (T + kThreads / 16 - 1) / (kThreads / 16);
+  const int grid = static_cast<int>(need < 1 ? 1 : (need < kNormBlocks ? need : kNormBlocks));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool ok = with_vpl(width, [&](auto vc) {
+    constexpr int VPL = decltype(vc)::value;
+    hipLaunchKernelGGL((relu_bwd_kernel<VPL>), dim3(grid), dim3(kThreads), 0, st, dy, h, dh, workspace, T);
+  });
+  if (!ok) return agpt_internal_set_error(AGPT_ERR_UNSUPPORTED, "agpt_relu_bwd: width must be 64, 128, 256 or 512");
+  hipLaunchKernelGGL(col_sum_kernel, dim3(width / 64), dim3(kThreads), 0, st, workspace, grid, width, db);
+  return launch_status("agpt_relu_bwd");
 }
 
 extern "C" int agpt_bias_rope(float* x, const float* bias, const int32_t* positions, const float* cos_t,

@@ -239,7 +239,8 @@ class _Lin(torch.autograd.Function):
 
 class _LinRelu(torch.autograd.Function):
     """relu(x·Wᵀ + b) with bias and ReLU in the GEMM's epilogue; backward
-    masks dy by the saved output (> 0, one pass), then as _Lin."""
+    masks dy by the saved output (> 0) and sums the bias gradient in one
+    native pass (agpt_relu_bwd), then dx and dW as _Lin."""
 
     @staticmethod
     def forward(ctx, x, w, b):
@@ -250,8 +251,8 @@ class _LinRelu(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x, w, h = ctx.saved_tensors
-        dh = torch.ops.aten.threshold_backward(dy, h, 0.0)
-        return dh @ w, _wgrad(dh, x), dh.sum(0)
+        dh, db = block.relu_bwd(dy.contiguous(), h)
+        return dh @ w, _wgrad(dh, x), db
 
 
 class _Embed(torch.autograd.Function):
@@ -331,6 +332,8 @@ class _Loss(torch.autograd.Function):
 class TrieGPT:
     def __init__(self, cfg: ModelConfig, device="cuda", seed: int = 0, lr: float = 3e-4,
                  beta: float = 0.999, eps: float = 1e-8):
+        if cfg.d_model not in (64, 128, 256, 512) or cfg.d_ff not in (64, 128, 256, 512):
+            raise ValueError("the native row kernels take d_model and d_ff of 64, 128, 256 or 512")
         self.cfg = cfg
         self.dev = torch.device(device)
         self.flat = torch.from_numpy(init_params(cfg, seed)).to(self.dev).requires_grad_(True)

@@ -71,7 +71,20 @@ int agpt_norm_bwd(const float* dy, const float* dres, const float* x, const floa
                   float* dx, float* dw, float* db, float* workspace, int64_t workspace_floats, int64_t T,
                   int d_model, void* stream);
 
-/* Workspace floats agpt_norm_bwd needs for d_model. */
+/* Backward of the FFN's ReLU and its bias gradient in one pass over
+ * [T, width] fp32 (width 64, 128, 256 or 512): dh = dy where h > 0 else 0
+ * (h = the ReLU's output), db [width] = sum over rows of dh in a fixed order
+ * (per-workgroup partials in `workspace`, at least
+ * agpt_norm_workspace_floats(width) floats, then a column sum). dh may be dy
+ * (in place, as the reference). All pointers 16-byte aligned. Replaces
+ * cuda_relu_backward (µGPT extern, agpt_train.cu:59; called at :4893) plus
+ * launch_bias_grad_accum over its output (:1774-1796, called at :4903),
+ * which the reference scales and adds into the bias gradient: the caller
+ * scales / accumulates db. */
+int agpt_relu_bwd(const float* dy, const float* h, float* dh, float* db, float* workspace,
+                  int64_t workspace_floats, int64_t T, int width, void* stream);
+
+/* Workspace floats agpt_norm_bwd and agpt_relu_bwd need for d_model / width. */
 int64_t agpt_norm_workspace_floats(int d_model);
 
 #ifdef __cplusplus

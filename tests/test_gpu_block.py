@@ -173,3 +173,34 @@ def test_norm_matches_oracle(gpu, D, layer):
     dxr, dwr, dbr = block.norm_bwd(to(dy), to(x), to(w), mu, rs, layer, dres=to(r))
     np.testing.assert_allclose(dxr.cpu().numpy(), dx0 + r, rtol=1e-4, atol=1e-5)
     assert torch.equal(dwr, dw) and (not layer or torch.equal(dbr, db))
+
+
+@pytest.mark.parametrize("W", [128, 512])
+def test_relu_bwd(gpu, W):
+    """agpt_relu_bwd against torch fp32: dh exact, db = the column sum of dh
+    (fixed order: two calls give identical bytes); in place allowed."""
+    import ctypes
+
+    import torch
+
+    from agpt_amd import _native, block
+
+    g = torch.Generator().manual_seed(W)
+    T = 7001
+    dy = torch.randn(T, W, generator=g).to(gpu)
+    h = torch.relu(torch.randn(T, W, generator=g)).to(gpu)
+    h[3, :] = 0.0  # a row with no live units
+    dh, db = block.relu_bwd(dy, h)
+    ref = torch.where(h > 0, dy, torch.zeros((), device=gpu))
+    assert torch.equal(dh, ref)
+    torch.testing.assert_close(db.double().cpu(), ref.double().sum(0).cpu(), rtol=1e-5, atol=1e-3)
+    dh2, db2 = block.relu_bwd(dy, h)
+    assert torch.equal(dh, dh2) and torch.equal(db, db2)
+    lib = _native.attn_lib()
+    ws = torch.empty(lib.agpt_norm_workspace_floats(W), device=gpu)
+    d3 = torch.empty(W, device=gpu)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    y = dy.clone()
+    assert lib.agpt_relu_bwd(p(y), p(h), p(y), p(d3), p(ws), ws.numel(), T, W, None) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref) and torch.equal(d3, db)

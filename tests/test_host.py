@@ -221,6 +221,7 @@ def test_new_entry_points_reject_bad_arguments_without_a_device():
     assert lib.agpt_norm_fwd(None, None, None, None, None, None, 3, 128, 1e-5, None) == _native.AGPT_ERR_INVALID_ARG
     assert lib.agpt_norm_workspace_floats(128) == 2 * 1024 * 128
     assert lib.agpt_norm_bwd(*[None] * 10, 0, 3, 128, None) == _native.AGPT_ERR_INVALID_ARG
+    assert lib.agpt_relu_bwd(*[None] * 5, 0, 3, 512, None) == _native.AGPT_ERR_INVALID_ARG
     mass = np.zeros(3, np.float32)
     i = lambda *v: np.array(v, np.int32).ctypes.data_as(C.POINTER(C.c_int32))
     assert lib.agpt_loss_mass_weights(i(0), i(5), i(2), i(0, 2), 1, 2, 9,
