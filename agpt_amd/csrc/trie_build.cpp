@@ -44,15 +44,18 @@ inline double std_normal(uint64_t key) {  // Box-Muller on two hashed uniforms
 
 struct Trie {
   std::vector<int32_t> parent, depth, token, end, radix_head, partition;
-  // Corpus observations (trie_corpus.cr:210-219): visits[n] = starts whose
-  // path passes n; a visit that ends at n (depth limit or corpus end) still
-  // observes the next token, kept in (end_node, end_tok) pairs.
-  std::vector<int32_t> visits, end_node, end_tok;
+  // Corpus observations: visits[n] = starts whose path passes n; the
+  // next-token counts of n as CSR (coff [T+1], ctok, cval; tokens
+  // ascending). Empty for a chain trie (no corpus).
+  std::vector<int32_t> visits, coff, ctok, cval;
+  int64_t n_corpus = 0;
   int64_t n_radix = 0, sum_depth = 0, n_root_children = 0, n_parts = 0;
   int32_t max_depth = 0;
 };
 
-void finish(Trie* t) {
+// Tables derived from parent / depth / token (and radix_head when
+// `heads_set`: a corpus trie decides its radix heads from counts).
+void finish(Trie* t, bool heads_set) {
   const int64_t n = static_cast<int64_t>(t->parent.size());
   t->end.resize(n);
   for (int64_t i = 0; i < n; ++i) t->end[i] = static_cast<int32_t>(i + 1);
@@ -66,7 +69,14 @@ void finish(Trie* t) {
     if (t->parent[i] >= 0) nchild[t->parent[i]]++;
     else t->n_root_children++;
   }
-  t->radix_head.resize(n);
+  if (!heads_set) {
+    // No corpus: a chain continues through a parent with exactly one child.
+    t->radix_head.resize(n);
+    for (int64_t i = 0; i < n; ++i) {
+      const int32_t p = t->parent[i];
+      t->radix_head[i] = (p < 0 || nchild[p] != 1) ? 1 : 0;
+    }
+  }
   t->partition.resize(n);
   t->n_radix = 0;
   t->sum_depth = 0;
@@ -74,11 +84,7 @@ void finish(Trie* t) {
   std::vector<int32_t> first_tok(n), second_tok(n);
   for (int64_t i = 0; i < n; ++i) {
     const int32_t p = t->parent[i];
-    // A chain continues through a parent with exactly one child
-    // (streaming_radix_builder.cr:159-170); root children always start one.
-    const int head = (p < 0 || nchild[p] != 1) ? 1 : 0;
-    t->radix_head[i] = head;
-    t->n_radix += head;
+    t->n_radix += t->radix_head[i];
     t->sum_depth += t->depth[i];
     t->max_depth = std::max(t->max_depth, t->depth[i]);
     if (p < 0) {
@@ -93,6 +99,149 @@ void finish(Trie* t) {
   }
   std::unordered_set<int32_t> keys(t->partition.begin(), t->partition.end());
   t->n_parts = static_cast<int64_t>(keys.size());
+}
+
+// Path length of a start: how many tokens from `s` become nodes.
+//   ingest (TrieCorpus#ingest, trie_corpus.cr:200-228): every inserted token
+//     has a next token, so the path stops before the corpus' last token;
+//   streaming (StreamingLeveledBuilder#build, streaming_leveled_builder.cr:
+//     48-108): a cursor advances while cursor + 1 < n, so a path runs onto
+//     the corpus' last token, whose node observes no next token.
+enum class Paths { kIngest, kStreaming };
+
+// Builds the nodes of the given starts in DFS preorder (children by
+// ascending token) with their visits and next-token counts.
+void build_nodes(Trie& t, const int32_t* tokens, int64_t n, int max_depth, std::vector<int64_t>& starts,
+                 Paths mode) {
+  auto len_of = [&](int64_t s) -> int64_t {
+    const int64_t room = mode == Paths::kIngest ? n - 1 - s : n - s;
+    return std::min<int64_t>(max_depth, room);
+  };
+  // Sorted by path string, every prefix first appears where a DFS preorder
+  // with ascending child tokens visits it.
+  std::sort(starts.begin(), starts.end(), [&](int64_t a, int64_t b) {
+    const int64_t la = len_of(a), lb = len_of(b), m = std::min(la, lb);
+    for (int64_t i = 0; i < m; ++i) {
+      const int32_t x = tokens[a + i], y = tokens[b + i];
+      if (x != y) return x < y;
+    }
+    if (la != lb) return la < lb;
+    return a < b;
+  });
+  // A visit that ends at a node (depth limit) still observes the token
+  // after its prefix, when there is one: (node, token) pairs.
+  std::vector<int32_t> end_node, end_tok;
+  std::vector<int32_t> stack(static_cast<size_t>(max_depth) + 1, -1);  // stack[d] = node at depth d
+  int64_t prev = -1;
+  for (int64_t s : starts) {
+    const int64_t len = len_of(s);
+    int64_t lcp = 0;
+    if (prev >= 0) {
+      const int64_t m = std::min(len, len_of(prev));
+      while (lcp < m && tokens[s + lcp] == tokens[prev + lcp]) ++lcp;
+    }
+    for (int64_t d = lcp + 1; d <= len; ++d) {
+      const int32_t id = static_cast<int32_t>(t.parent.size());
+      t.parent.push_back(stack[d - 1]);
+      t.depth.push_back(static_cast<int32_t>(d));
+      t.token.push_back(tokens[s + d - 1]);
+      t.visits.push_back(0);
+      stack[d] = id;
+    }
+    for (int64_t d = 1; d <= len; ++d) ++t.visits[stack[d]];
+    if (len > 0 && s + len < n) {
+      end_node.push_back(stack[len]);
+      end_tok.push_back(tokens[s + len]);
+    }
+    prev = s;
+  }
+  // Next-token counts: the children (each child's visits observed its
+  // token) merged with the ending observations, ascending by token.
+  const int64_t T = static_cast<int64_t>(t.parent.size());
+  std::vector<int32_t> end_first(T, -1), end_next(end_node.size(), -1);
+  for (int64_t i = static_cast<int64_t>(end_node.size()) - 1; i >= 0; --i) {
+    end_next[i] = end_first[end_node[i]];
+    end_first[end_node[i]] = static_cast<int32_t>(i);
+  }
+  std::vector<int32_t> first_child(T, -1), next_sib(T, -1);
+  for (int64_t i = T - 1; i >= 0; --i) {
+    const int32_t p = t.parent[i];
+    if (p >= 0) {
+      next_sib[i] = first_child[p];
+      first_child[p] = static_cast<int32_t>(i);
+    }
+  }
+  t.coff.assign(static_cast<size_t>(T) + 1, 0);
+  std::vector<std::pair<int32_t, int32_t>> hist;
+  for (int64_t i = 0; i < T; ++i) {
+    t.coff[i] = static_cast<int32_t>(t.ctok.size());
+    hist.clear();
+    for (int32_t c = first_child[i]; c >= 0; c = next_sib[c]) hist.emplace_back(t.token[c], t.visits[c]);
+    for (int32_t e = end_first[i]; e >= 0; e = end_next[e]) hist.emplace_back(end_tok[e], 1);
+    std::sort(hist.begin(), hist.end());
+    for (size_t j = 0; j < hist.size(); ++j) {
+      if (j > 0 && hist[j].first == hist[j - 1].first) {  // same token: merge into the last entry
+        t.cval.back() += hist[j].second;
+        continue;
+      }
+      t.ctok.push_back(hist[j].first);
+      t.cval.push_back(hist[j].second);
+    }
+  }
+  t.coff[T] = static_cast<int32_t>(t.ctok.size());
+  t.n_corpus = n;
+}
+
+// Radix heads by the reference's rule (streaming_radix_builder.cr:155-170):
+// an edge runs on through a node with exactly one next-token entry, so a
+// node starts an edge when it is a root child or its parent's count list
+// does not have exactly one entry.
+void count_heads(Trie& t) {
+  const int64_t T = static_cast<int64_t>(t.parent.size());
+  t.radix_head.resize(T);
+  for (int64_t i = 0; i < T; ++i) {
+    const int32_t p = t.parent[i];
+    t.radix_head[i] = (p < 0 || t.coff[p + 1] - t.coff[p] != 1) ? 1 : 0;
+  }
+}
+
+// Drops every radix edge whose endpoint has no next-token entry (the
+// end-of-corpus leaf, streaming_radix_builder.cr:177-180): the edge's rows
+// form the head's whole subtree (each inner node has one child, the
+// endpoint none), so removing them keeps a DFS-preorder forest. The counts
+// of the remaining nodes are kept as they are (a parent still lists the
+// dropped child's token, as the reference's endpoint records do).
+void drop_dead_edges(Trie& t) {
+  const int64_t T = static_cast<int64_t>(t.parent.size());
+  std::vector<uint8_t> keep(T, 1);
+  for (int64_t h = 0; h < T;) {
+    int64_t e = h;  // last row of the edge that starts at h
+    while (e + 1 < T && !t.radix_head[e + 1] && t.parent[e + 1] == e) ++e;
+    if (t.coff[e + 1] == t.coff[e])
+      for (int64_t i = h; i <= e; ++i) keep[i] = 0;
+    h = e + 1;
+  }
+  std::vector<int32_t> nid(T, -1);
+  int64_t m = 0;
+  for (int64_t i = 0; i < T; ++i)
+    if (keep[i]) nid[i] = static_cast<int32_t>(m++);
+  if (m == T) return;
+  Trie u;
+  u.n_corpus = t.n_corpus;
+  u.coff.push_back(0);
+  for (int64_t i = 0; i < T; ++i) {
+    if (!keep[i]) continue;
+    const int32_t p = t.parent[i];
+    u.parent.push_back(p < 0 ? -1 : nid[p]);
+    u.depth.push_back(t.depth[i]);
+    u.token.push_back(t.token[i]);
+    u.visits.push_back(t.visits[i]);
+    u.radix_head.push_back(t.radix_head[i]);
+    u.ctok.insert(u.ctok.end(), t.ctok.begin() + t.coff[i], t.ctok.begin() + t.coff[i + 1]);
+    u.cval.insert(u.cval.end(), t.cval.begin() + t.coff[i], t.cval.begin() + t.coff[i + 1]);
+    u.coff.push_back(static_cast<int32_t>(u.ctok.size()));
+  }
+  t = std::move(u);
 }
 
 }  // namespace
@@ -158,13 +307,10 @@ extern "C" int agpt_uniform_tokens(uint64_t seed, int vocab, int64_t n, int32_t*
   return 0;
 }
 
-extern "C" int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
-                               int64_t max_starts, agpt_trie_handle* out) {
-  if (!out || (!tokens && n > 0) || max_depth < 1) return 1;
-  *out = nullptr;
-  auto* h = new agpt_trie_s();
-  Trie& t = h->t;
-  const int64_t total_starts = n - 1;  // trie_corpus.cr:203
+namespace {
+
+std::vector<int64_t> starts_of(int64_t n, int64_t max_starts) {
+  const int64_t total_starts = n - 1;  // trie_corpus.cr:203, streaming_leveled_builder.cr:43
   std::vector<int64_t> starts;
   if (total_starts > 0) {
     const int64_t count = (max_starts > 0) ? std::min(total_starts, max_starts) : total_starts;
@@ -175,41 +321,36 @@ extern "C" int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
       for (int64_t i = 0; i < count; ++i) starts[i] = (i * total_starts / count) % total_starts;
     }
   }
-  auto len_of = [&](int64_t s) -> int64_t { return std::min<int64_t>(max_depth, total_starts - s); };
-  std::sort(starts.begin(), starts.end(), [&](int64_t a, int64_t b) {
-    const int64_t la = len_of(a), lb = len_of(b), m = std::min(la, lb);
-    for (int64_t i = 0; i < m; ++i) {
-      const int32_t x = tokens[a + i], y = tokens[b + i];
-      if (x != y) return x < y;
-    }
-    if (la != lb) return la < lb;
-    return a < b;
-  });
-  std::vector<int32_t> stack(static_cast<size_t>(max_depth) + 1, -1);  // stack[d] = node at depth d
-  int64_t prev = -1;
-  for (int64_t s : starts) {
-    const int64_t len = len_of(s);
-    int64_t lcp = 0;
-    if (prev >= 0) {
-      const int64_t m = std::min(len, len_of(prev));
-      while (lcp < m && tokens[s + lcp] == tokens[prev + lcp]) ++lcp;
-    }
-    for (int64_t d = lcp + 1; d <= len; ++d) {
-      const int32_t id = static_cast<int32_t>(t.parent.size());
-      t.parent.push_back(stack[d - 1]);
-      t.depth.push_back(static_cast<int32_t>(d));
-      t.token.push_back(tokens[s + d - 1]);
-      t.visits.push_back(0);
-      stack[d] = id;
-    }
-    for (int64_t d = 1; d <= len; ++d) ++t.visits[stack[d]];
-    if (len > 0) {  // the last step observes tokens[s + len] (index < total_starts)
-      t.end_node.push_back(stack[len]);
-      t.end_tok.push_back(tokens[s + len]);
-    }
-    prev = s;
-  }
-  finish(&t);
+  return starts;
+}
+
+}  // namespace
+
+extern "C" int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
+                               int64_t max_starts, agpt_trie_handle* out) {
+  if (!out || (!tokens && n > 0) || max_depth < 1) return 1;
+  *out = nullptr;
+  auto* h = new agpt_trie_s();
+  Trie& t = h->t;
+  std::vector<int64_t> starts = starts_of(n, max_starts);
+  build_nodes(t, tokens, n, max_depth, starts, Paths::kIngest);
+  count_heads(t);
+  finish(&t, true);
+  *out = h;
+  return 0;
+}
+
+extern "C" int agpt_trie_build_radix(const int32_t* tokens, int64_t n, int max_depth,
+                                     agpt_trie_handle* out) {
+  if (!out || (!tokens && n > 0) || max_depth < 1) return 1;
+  *out = nullptr;
+  auto* h = new agpt_trie_s();
+  Trie& t = h->t;
+  std::vector<int64_t> starts = starts_of(n, 0);
+  build_nodes(t, tokens, n, max_depth, starts, Paths::kStreaming);
+  count_heads(t);
+  drop_dead_edges(t);
+  finish(&t, true);
   *out = h;
   return 0;
 }
@@ -230,7 +371,7 @@ extern "C" int agpt_trie_build_chains(const int32_t* tokens, int64_t n_chains, i
       t.depth[i] = j + 1;
       t.token[i] = tokens[i];
     }
-  finish(&t);
+  finish(&t, false);
   *out = h;
   return 0;
 }
@@ -291,41 +432,10 @@ extern "C" int agpt_trie_next_counts(agpt_trie_handle h, int32_t* visits, int64_
   const int64_t n = static_cast<int64_t>(t.parent.size());
   if (t.visits.size() != static_cast<size_t>(n)) return 2;  // a chain trie has no corpus
   if (visits) std::memcpy(visits, t.visits.data(), n * sizeof(int32_t));
-  // Per node: children (DFS order = ascending token) with their visits, then
-  // the ending observations merged by token, all in ascending token order.
-  std::vector<int32_t> end_first(n, -1), end_next(t.end_node.size(), -1);
-  for (int64_t i = static_cast<int64_t>(t.end_node.size()) - 1; i >= 0; --i) {
-    end_next[i] = end_first[t.end_node[i]];
-    end_first[t.end_node[i]] = static_cast<int32_t>(i);
-  }
-  std::vector<int32_t> first_child(n, -1), next_sib(n, -1);
-  for (int64_t i = n - 1; i >= 0; --i) {
-    const int32_t p = t.parent[i];
-    if (p >= 0) {
-      next_sib[i] = first_child[p];
-      first_child[p] = static_cast<int32_t>(i);
-    }
-  }
-  int64_t k = 0;
-  std::vector<std::pair<int32_t, int32_t>> hist;
-  for (int64_t i = 0; i < n; ++i) {
-    if (offsets) offsets[i] = static_cast<int32_t>(k);
-    hist.clear();
-    for (int32_t c = first_child[i]; c >= 0; c = next_sib[c]) hist.emplace_back(t.token[c], t.visits[c]);
-    for (int32_t e = end_first[i]; e >= 0; e = end_next[e]) hist.emplace_back(t.end_tok[e], 1);
-    std::sort(hist.begin(), hist.end());
-    for (size_t j = 0; j < hist.size(); ++j) {
-      if (j > 0 && hist[j].first == hist[j - 1].first) {  // same token: merge into the last entry
-        if (val) val[k - 1] += hist[j].second;
-        continue;
-      }
-      if (tok) tok[k] = hist[j].first;
-      if (val) val[k] = hist[j].second;
-      ++k;
-    }
-  }
-  if (offsets) offsets[n] = static_cast<int32_t>(k);
-  *n_entries = k;
+  if (offsets) std::memcpy(offsets, t.coff.data(), (n + 1) * sizeof(int32_t));
+  if (tok && !t.ctok.empty()) std::memcpy(tok, t.ctok.data(), t.ctok.size() * sizeof(int32_t));
+  if (val && !t.cval.empty()) std::memcpy(val, t.cval.data(), t.cval.size() * sizeof(int32_t));
+  *n_entries = static_cast<int64_t>(t.ctok.size());
   return 0;
 }
 
@@ -367,11 +477,9 @@ extern "C" int agpt_radix_write_subtrees(agpt_trie_handle h, const char* out_dir
   const Trie& t = h->t;
   const int64_t n = static_cast<int64_t>(t.parent.size());
   if (t.visits.size() != static_cast<size_t>(n)) return 2;  // no corpus counts
-  // next-token histograms (as agpt_trie_next_counts) and children lists
-  int64_t ne = 0;
-  if (agpt_trie_next_counts(h, nullptr, &ne, nullptr, nullptr, nullptr)) return 3;
-  std::vector<int32_t> off(n + 1), tok(ne), val(ne);
-  agpt_trie_next_counts(h, nullptr, &ne, off.data(), tok.data(), val.data());
+  const std::vector<int32_t>& off = t.coff;
+  const std::vector<int32_t>& tok = t.ctok;
+  const std::vector<int32_t>& val = t.cval;
   std::vector<int32_t> first_child(n, -1), next_sib(n, -1), roots;
   for (int64_t i = n - 1; i >= 0; --i) {
     const int32_t p = t.parent[i];
@@ -401,8 +509,9 @@ extern "C" int agpt_radix_write_subtrees(agpt_trie_handle h, const char* out_dir
     for (int32_t c : kids) {
       std::vector<int32_t> edge{t.token[c]};
       int32_t cur = c;
-      // extend while the node has one next token and its one child exists
-      while (off[cur + 1] - off[cur] == 1 && first_child[cur] >= 0 && next_sib[first_child[cur]] < 0) {
+      // extend while the node has one next-token entry and its child
+      // exists (the child then continues the edge: it is no radix head)
+      while (first_child[cur] >= 0 && !t.radix_head[first_child[cur]]) {
         cur = first_child[cur];
         edge.push_back(t.token[cur]);
       }
@@ -416,7 +525,9 @@ extern "C" int agpt_radix_write_subtrees(agpt_trie_handle h, const char* out_dir
       put_i32(b, st.depth);
       put_i32(b, static_cast<int32_t>(edge.size()));
       for (int32_t x : edge) put_i32(b, x);
-      put_i32(b, t.visits[c]);  // v2 edge mass: the head's count
+      int32_t mass = 0;  // v2 edge mass: the sum of the head's counts
+      for (int32_t e = off[c]; e < off[c + 1]; ++e) mass += val[e];
+      put_i32(b, mass);
       put_i32(b, off[cur + 1] - off[cur]);
       for (int32_t e = off[cur]; e < off[cur + 1]; ++e) {
         put_i32(b, tok[e]);
@@ -461,7 +572,7 @@ extern "C" int agpt_radix_write_subtrees(agpt_trie_handle h, const char* out_dir
   put_i32(meta, next_id);  // radix nodes + the virtual root
   put_i32(meta, max_ep + 1);
   put_i64(meta, total_chars);
-  put_i32(meta, 0);  // corpus token count: not kept by the trie
+  put_i32(meta, static_cast<int32_t>(t.n_corpus));
   put_i32(meta, vocab_size);
   put_i64(meta, 0);  // corpus hash
   put_i32(meta, 4);

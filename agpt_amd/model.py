@@ -91,12 +91,12 @@ class TrieBatch:
     """The device tables of one batch of whole root-child subtrees: DFS
     parents, RoPE positions, and the loss's radix query layout (one query
     per node-token, radix nodes in DFS order, each endpoint's next-token
-    counts, edge_mass = the count of the edge's first node). Mass weights
+    counts, edge_mass = the sum of the edge head's counts). Mass weights
     are normalised over the batch."""
 
     def __init__(self, tr, cfg: ModelConfig, device, mass_mode: int = L.MASS_LINEAR, rows=None):
-        """From a trie with corpus counts (build_trie(..., counts=True)),
-        rows a..b (whole root-child subtrees)."""
+        """From a trie with corpus counts (build_radix_trie or build_trie
+        with counts=True), rows a..b (whole root-child subtrees)."""
         if tr.visits is None:
             raise ValueError("the trie needs corpus counts (build_trie(..., counts=True))")
         a0, b0 = rows if rows is not None else (0, tr.n_nodes)
@@ -109,8 +109,12 @@ class TrieBatch:
         coff = np.zeros(heads.shape[0] + 1, np.int64)
         np.cumsum(cnt, out=coff[1:])
         sel = np.repeat(a.astype(np.int64) - coff[:-1], cnt) + np.arange(int(coff[-1]))
+        # edge_mass: the sum of the edge head's counts (streaming_radix_builder.cr:150-153)
+        csum = np.concatenate([[0], np.cumsum(tr.next_val, dtype=np.int64)])
+        h = heads + a0
+        mass = (csum[tr.next_offsets[h + 1]] - csum[tr.next_offsets[h]]).astype(np.int32)
         self._build(cfg, device, mass_mode, np.where(par < 0, -1, par - a0), tr.token[a0:b0],
-                    tr.depth[a0:b0], qoff, tr.visits[heads + a0], coff, tr.next_tok[sel], tr.next_val[sel])
+                    tr.depth[a0:b0], qoff, mass, coff, tr.next_tok[sel], tr.next_val[sel])
 
     @classmethod
     def from_radix(cls, subtrees, cfg: ModelConfig, device, mass_mode: int = L.MASS_LINEAR):

@@ -113,6 +113,18 @@ def build_trie(tokens: np.ndarray, max_depth: int, max_starts: int = 0, counts: 
     return _export(h, counts)
 
 
+def build_radix_trie(tokens: np.ndarray, max_depth: int, counts: bool = False) -> Trie:
+    """The node-tokens the reference's on-disk radix pipeline trains on
+    (StreamingLeveledBuilder + StreamingRadixBuilder: paths run onto the
+    corpus' last token, edges are cut on next-token entries, edges ending at
+    the end-of-corpus leaf are dropped; see include/agpt_trie.h)."""
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    h = C.c_void_p()
+    if trie_lib().agpt_trie_build_radix(_ptr(tok), tok.shape[0], max_depth, C.byref(h)):
+        raise ValueError("agpt_trie_build_radix: bad arguments")
+    return _export(h, counts)
+
+
 def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
     tok = np.ascontiguousarray(tokens, dtype=np.int32)
     assert tok.shape[0] >= n_chains * chain_len
@@ -122,16 +134,25 @@ def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
     return _export(h)
 
 
-def write_radix_files(tokens: np.ndarray, max_depth: int, out_dir: str, vocab: int) -> None:
-    """Builds the leveled trie of `tokens` and writes the reference's radix
-    files (subtrees/radix_subtree_%06d.bin, manifest.bin, meta.bin, format v2)."""
+def write_radix_files(tokens: np.ndarray, max_depth: int, out_dir: str, vocab: int,
+                      pipeline: str = "radix") -> None:
+    """Builds the trie of `tokens` and writes the reference's radix files
+    (subtrees/radix_subtree_%06d.bin, manifest.bin, meta.bin, format v2).
+    pipeline "radix": the reference's on-disk builders (build_radix_trie);
+    "ingest": the in-memory TrieCorpus trie (build_trie)."""
     import os
     os.makedirs(os.path.join(out_dir, "subtrees"), exist_ok=True)
     tok = np.ascontiguousarray(tokens, dtype=np.int32)
     h = C.c_void_p()
     lib = trie_lib()
-    if lib.agpt_trie_build(_ptr(tok), tok.shape[0], max_depth, 0, C.byref(h)):
-        raise ValueError("agpt_trie_build: bad arguments")
+    if pipeline == "radix":
+        rc = lib.agpt_trie_build_radix(_ptr(tok), tok.shape[0], max_depth, C.byref(h))
+    elif pipeline == "ingest":
+        rc = lib.agpt_trie_build(_ptr(tok), tok.shape[0], max_depth, 0, C.byref(h))
+    else:
+        raise ValueError(f"pipeline {pipeline!r}: 'radix' or 'ingest'")
+    if rc:
+        raise ValueError("trie build: bad arguments")
     rc = lib.agpt_radix_write_subtrees(h, out_dir.encode(), vocab)
     lib.agpt_trie_free(h)
     if rc:
@@ -217,4 +238,6 @@ def config_trie(name: str, scale: float = 1.0, counts: bool = False) -> Trie:
         return build_chains(tok, n_chains, c["chain_len"])
     n = max(2, int(c["n"] * scale))
     tok = markov_corpus(n, c["order"], c["vocab"], c["zipf"], c["seed"])
-    return build_trie(tok, c["depth"], counts=counts)
+    # "Build the leveled trie at max depth D, then radix-compress it":
+    # the reference's on-disk pipeline.
+    return build_radix_trie(tok, c["depth"], counts=counts)

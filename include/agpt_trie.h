@@ -40,12 +40,28 @@ int agpt_uniform_tokens(uint64_t seed, int vocab, int64_t n, int32_t* out_tokens
 int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
                     int64_t max_starts, agpt_trie_handle* out);
 
+/* The trie the reference's on-disk radix pipeline trains on
+ * (src/tools/build_index.cr + build_radix.cr): StreamingLeveledBuilder#build
+ * (streaming_leveled_builder.cr:48-108) inserts every start 0..n-2 with a
+ * path that runs while the next position is inside the corpus, so paths
+ * near the end reach the corpus' last token (a node with no next-token
+ * observation); StreamingRadixBuilder#build (streaming_radix_builder.cr:
+ * 149-180) then runs an edge on through nodes with exactly one next-token
+ * entry and drops every edge whose endpoint has none (the end-of-corpus
+ * leaf). The result holds the node-tokens of the kept radix edges, DFS
+ * preorder, children by ascending token; its counts are the leveled
+ * nodes' own (a parent keeps the entry of a dropped child). */
+int agpt_trie_build_radix(const int32_t* tokens, int64_t n, int max_depth,
+                          agpt_trie_handle* out);
+
 /* `n_chains` independent unary chains of `chain_len` nodes each (never
  * merged); chain c takes tokens[c*chain_len ...]. The dense-causal control. */
 int agpt_trie_build_chains(const int32_t* tokens, int64_t n_chains, int chain_len,
                            agpt_trie_handle* out);
 
-/* Node-token count T, radix-node count (chain heads, streaming_radix_builder.cr:149-175),
+/* Node-token count T, radix-node count (edge heads: a root child, or a node
+ * whose parent has not exactly one next-token entry, streaming_radix_builder.cr:
+ * 155-170; a chain trie: a parent without exactly one child),
  * Σ depth, max depth, number of root children, number of bigram partitions. */
 int agpt_trie_stats(agpt_trie_handle t, int64_t* n_nodes, int64_t* n_radix,
                     int64_t* sum_depth, int32_t* max_depth, int64_t* n_root_children,
@@ -66,12 +82,13 @@ int agpt_trie_export_radix(agpt_trie_handle t, int32_t* radix_parent,
                            int32_t* edge_len);
 
 /* Corpus observations of a trie built by agpt_trie_build (TrieCorpus#ingest
- * + #observe, trie_corpus.cr:200-228): visits[i] = starts whose path passes
- * node i; node i's next-token counts (every visit observes the token after
- * its prefix, also where the path stops at the depth limit) as CSR over the
- * T nodes: entries offsets[i] .. offsets[i+1]-1 of tok / val, tokens
- * ascending, sum of val = visits[i]. Call first with tok = val = offsets =
- * NULL to get n_entries. Returns 2 for a chain trie (no corpus). */
+ * + #observe, trie_corpus.cr:200-228) or agpt_trie_build_radix:
+ * visits[i] = starts whose path passes node i; node i's next-token counts
+ * (every visit observes the token after its prefix, also where the path
+ * stops at the depth limit, except a visit ending on the corpus' last
+ * token) as CSR over the T nodes: entries offsets[i] .. offsets[i+1]-1 of
+ * tok / val, tokens ascending. Call first with tok = val = offsets = NULL
+ * to get n_entries. Returns 2 for a chain trie (no corpus). */
 int agpt_trie_next_counts(agpt_trie_handle t, int32_t* visits, int64_t* n_entries,
                           int32_t* offsets, int32_t* tok, int32_t* val);
 
@@ -84,11 +101,13 @@ int agpt_trie_next_counts(agpt_trie_handle t, int32_t* visits, int64_t* n_entrie
  * entry_count, (token, count) entries of the endpoint's next-token counts. */
 typedef struct agpt_radix_s* agpt_radix_handle;
 
-/* Writes the radix files of a trie built with agpt_trie_build (needs its
- * corpus counts) as the reference's builder does (streaming_radix_builder.cr:
+/* Writes the radix files of a trie built with agpt_trie_build or
+ * agpt_trie_build_radix (needs its corpus counts) as the reference's builder does (streaming_radix_builder.cr:
  * 100-330): edge starts breadth first from the root, radix ids in that order
  * from 1, an edge extended while its end has exactly one next-token entry
- * and that child exists. out_dir and out_dir/subtrees must exist. */
+ * and that child exists, edge_mass = the sum of the head's counts, meta's
+ * corpus_token_count = the corpus length. out_dir and out_dir/subtrees must
+ * exist. */
 int agpt_radix_write_subtrees(agpt_trie_handle t, const char* out_dir, int32_t vocab_size);
 
 /* Reads one radix_subtree_%06d.bin (agpt_train.cu:495-669 load_subtree):

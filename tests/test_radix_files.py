@@ -59,11 +59,15 @@ def test_hand_built_subtree_file(tmp_path):
             trie.read_radix_subtree(str(q))
 
 
+@pytest.mark.parametrize("pipeline", ["radix", "ingest"])
 @pytest.mark.parametrize("n,order,vocab,depth", [(2000, 2, 6, 10), (5000, 3, 9, 16), (800, 1, 4, 32)])
-def test_written_files_read_back_into_the_trie(tmp_path, n, order, vocab, depth):
+def test_written_files_read_back_into_the_trie(tmp_path, n, order, vocab, depth, pipeline):
     tok = trie.markov_corpus(n, order, vocab, 1.1, seed=n)
-    trie.write_radix_files(tok, depth, str(tmp_path), vocab)
-    tr = trie.build_trie(tok, depth, counts=True)
+    trie.write_radix_files(tok, depth, str(tmp_path), vocab, pipeline=pipeline)
+    if pipeline == "radix":
+        tr = trie.build_radix_trie(tok, depth, counts=True)
+    else:
+        tr = trie.build_trie(tok, depth, counts=True)
     man = trie.read_radix_manifest(str(tmp_path / "manifest.bin"))
     kids = {}
     for i, p in enumerate(tr.parent):
@@ -76,24 +80,28 @@ def test_written_files_read_back_into_the_trie(tmp_path, n, order, vocab, depth)
         p, t, d = st.rows()
         assert int(d.max()) == max_ep
         qoff = np.concatenate([[0], np.cumsum(st.edge_len)])
-        for r in range(st.radix_id.shape[0]):  # per edge: mass = head visits, counts = endpoint's
+        for r in range(st.radix_id.shape[0]):  # per edge: mass = head's counts, counts = endpoint's
             head, end = base + qoff[r], base + qoff[r + 1] - 1
-            assert st.edge_mass[r] == tr.visits[head]
+            h0, h1 = tr.next_offsets[head], tr.next_offsets[head + 1]
+            assert st.edge_mass[r] == int(tr.next_val[h0:h1].sum())
             a, b = tr.next_offsets[end], tr.next_offsets[end + 1]
             c0, c1 = st.counts_offset[r], st.counts_offset[r + 1]
             assert st.counts_tok[c0:c1].tolist() == tr.next_tok[a:b].tolist()
             assert st.counts_val[c0:c1].tolist() == tr.next_val[a:b].tolist()
-            # the reference's cut: inside an edge every node has one next token and one child
+            # the reference's cut (streaming_radix_builder.cr:155-170): inside an
+            # edge every node has one next-token entry and its child; the
+            # endpoint has not, and it has at least one entry (:177-180)
             for x in range(head, end):
                 assert nent[x] == 1 and len(kids.get(x, [])) == 1
             assert not (nent[end] == 1 and len(kids.get(end, [])) == 1)
+            assert nent[end] >= 1
         rows.append(np.where(p < 0, -1, p + base))
         base += p.shape[0]
         seen += nodes
     assert (np.concatenate(rows) == tr.parent).all()
     meta = (tmp_path / "meta.bin").read_bytes()
-    magic, ver, rcount, dfc, chars = struct.unpack_from("<Iiiiq", meta, 0)
-    assert (magic, ver, rcount, chars) == (MAGIC, 2, seen + 1, tr.n_nodes)
+    magic, ver, rcount, dfc, chars, ntok = struct.unpack_from("<Iiiiqi", meta, 0)
+    assert (magic, ver, rcount, chars, ntok) == (MAGIC, 2, seen + 1, tr.n_nodes, n)
     assert dfc == tr.max_depth + 1
 
 
@@ -106,7 +114,7 @@ def test_model_batch_from_files_equals_batch_from_trie(tmp_path):
 
     tok = trie.markov_corpus(3000, 2, 7, 1.1, seed=3)
     trie.write_radix_files(tok, 10, str(tmp_path), 7)
-    tr = trie.build_trie(tok, 10, counts=True)
+    tr = trie.build_radix_trie(tok, 10, counts=True)
     cfg = model.ModelConfig(vocab=7, d_model=64, n_heads=4, n_layers=2, d_ff=128, max_depth=10)
     b1 = model.TrieBatch(tr, cfg, torch.device("cpu"))
     man = trie.read_radix_manifest(str(tmp_path / "manifest.bin"))
