@@ -45,9 +45,20 @@ HIP_FLAGS = [
 HIP_SOURCES = ["trie_attn.hip", "varlen_attn.hip", "agpt_loss.hip", "agpt_block.hip"]
 
 
+# hipcc applies -Xclang options to the host pass too, whose x86 target does
+# not know the AMDGPU feature and says so once per host compile; clang's
+# -Xarch_device cannot forward an -Xclang pair, so the line is dropped here.
+_HOST_NOISE = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
+
+
 def _run(cmd: list[str]) -> None:
     print("+", " ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(ln for ln in r.stdout.splitlines() if ln.strip() != _HOST_NOISE)
+    if out.strip():
+        print(out, flush=True)
+    if r.returncode:
+        raise subprocess.CalledProcessError(r.returncode, cmd)
 
 
 def build_trie_lib() -> Path:
@@ -60,11 +71,13 @@ def build_trie_lib() -> Path:
 
 def build_attn_lib() -> Path:
     LIB.mkdir(exist_ok=True)
-    objs = []
-    for src in HIP_SOURCES:
-        obj = LIB / (Path(src).stem + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
-        objs.append(str(obj))
+    from concurrent.futures import ThreadPoolExecutor
+
+    objs = [str(LIB / (Path(src).stem + ".o")) for src in HIP_SOURCES]
+    jobs = int(os.environ.get("MAX_JOBS", "4"))
+    with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(HIP_SOURCES)))) as ex:
+        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / so[0]), "-o", so[1]]),
+                    zip(HIP_SOURCES, objs)))
     out = LIB / "libagpt_attn.so"
     tmp = LIB / "libagpt_attn.so.tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])

@@ -1152,6 +1152,18 @@ int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds, int hg = 0) {
   return static_cast<int>(g);
 }
 
+// Clears the block kernels' chunk counters on the stream with a kernel, not
+// a memset node: the launch sequence stays valid under stream capture
+// (memset nodes in captured graphs have given wrong results on replays).
+__global__ void zero_i32_kernel(int32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
+void clear_sched(const agpt_attn_s* h, hipStream_t st) {
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(64), 0, st, h->d_sched,
+                     static_cast<int>(kSchedBytes / sizeof(int32_t)));
+}
+
 template <typename Fn>
 void set_lds(Fn fn, size_t bytes) {
   if (bytes > 65536)
@@ -1197,7 +1209,7 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   pm.mark(0);
   if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32 || HD == 64) {
-      (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
+      clear_sched(h, st);
       with_block_heads(h, h->fwd_uh, [&](auto hgc, auto uhc) {
         constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
         if constexpr (block_shape_ok(HD, HG, UH)) {
@@ -1240,7 +1252,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   bool fused_done = false;
   if constexpr ((HD == 16 || HD == 32) && std::is_same<Tin, float>::value) {
     if (h->variant == 6 && h->fused) {
-      (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
+      clear_sched(h, st);
       auto run = [&](auto hgc, auto cc) {
         constexpr int HG = decltype(hgc)::value;
         constexpr bool kCarry = decltype(cc)::value;
@@ -1280,7 +1292,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if (fused_done) {
   } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32 || HD == 64) {
-      (void)hipMemsetAsync(h->d_sched, 0, kSchedBytes, st);
+      clear_sched(h, st);
       with_block_heads(h, h->unit_all_heads ? h->hg : 1, [&](auto hgc, auto uhc) {
         constexpr int HG = decltype(hgc)::value, UH = decltype(uhc)::value;
         if constexpr (block_shape_ok(HD, HG, UH)) {

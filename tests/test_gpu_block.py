@@ -111,6 +111,43 @@ def test_c3_step_matches_float64(gpu, norm, max_rows):
     m.close()
 
 
+@pytest.mark.parametrize("max_rows", [1 << 20, 700])
+def test_c3_config_step(gpu, max_rows):
+    """C3's own model (4 layers, d_model 128, 8 heads x
+    16, FFN 512, RMSNorm, vocab 65) on a C1-corpus radix trie of ~2K rows
+    (depth 32), linear mass weights, one step against the float64 CPU
+    model: loss within 1e-4 relative, every parameter's gradient within
+    2e-4 of its largest |value|, the update RMSProp on that gradient."""
+    import torch
+
+    from agpt_amd import model, trie
+    from c3_reference import step_f64
+
+    tr = trie.config_trie("C1", scale=0.0005, counts=True)
+    assert 1500 < tr.n_nodes < 4000 and tr.max_depth == 32
+    cfg = model.ModelConfig()
+    assert (cfg.n_layers, cfg.d_model, cfg.n_heads, cfg.d_ff, cfg.vocab, cfg.norm) == (4, 128, 8, 512, 65, "rms")
+    m = model.TrieGPT(cfg, device=gpu, seed=7)
+    m.plan(tr, max_rows=max_rows)
+    flat0 = m.flat.detach().cpu().numpy().copy()
+    loss = float(m.step())
+    torch.cuda.synchronize()
+    grad = m.flat.grad.detach().cpu().numpy()
+    mass = np.concatenate([b.mass.cpu().numpy() for _, b in m.groups])
+    want_loss, want_grad = step_f64(cfg, flat0, tr, mass)
+    assert abs(loss - want_loss) <= 1e-4 * abs(want_loss), (loss, want_loss)
+    off = 0
+    for name, shape in model.param_shapes(cfg):
+        k = int(np.prod(shape))
+        g, w = grad[off:off + k], want_grad[off:off + k]
+        bound = 2e-4 * max(np.abs(w).max(), 1e-6)
+        assert np.abs(g - w).max() <= bound, (name, np.abs(g - w).max(), np.abs(w).max())
+        off += k
+    p1, _ = ORC.rmsprop(flat0, grad, np.zeros_like(flat0), m.lr, m.beta, m.eps)
+    np.testing.assert_allclose(m.flat.detach().cpu().numpy(), p1, rtol=2e-6, atol=1e-6)
+    m.close()
+
+
 def test_c3_checkpoint_round_trip_through_the_model(gpu, tmp_path):
     from agpt_amd import model
 

@@ -168,6 +168,18 @@ def test_parity_c1_sample(gpu):
     _check(tr.parent, 4, 16, seed=1, rope=True)
 
 
+@pytest.mark.parametrize("rope", [False, True])
+def test_parity_c2_sample(gpu, rope):
+    """The headline C2 configuration (the bench's workload) on a reduced
+    corpus: order-5 Markov over 65 symbols, radix trie at depth 32, 8 heads
+    x head_dim 16 (four head groups of two heads in the one-pass backward),
+    fp32."""
+    from agpt_amd import trie
+    tr = trie.config_trie("C2", scale=0.0025)  # 2,750 chars -> ~60K node-tokens, depth 32
+    assert tr.max_depth == 32
+    _check(tr.parent, 8, 16, seed=2, rope=rope)
+
+
 @pytest.mark.parametrize("hd", [8, 16, 64])
 @pytest.mark.parametrize("kind", ["single", "roots", "chain256", "tile_edge", "tile_edge1", "deep48"])
 def test_edge_shapes(gpu, kind, hd):

@@ -248,6 +248,60 @@ def test_varlen_layout_equals_trie():
     assert_close(dv_s, dV, what="scatter dV")
 
 
+def test_varlen_L_layout_equals_bruteforce():
+    """The radix chunk-packer layout (agpt_train.cu:4456-4479): the queries
+    of radix node i are its edge rows, its packed prefix is its ancestor
+    rows then its edge rows, query j of the edge sees the first
+    kv_len - L + j + 1 of them (agpt_train.cu:3106-3117). Scatter-adding the
+    packed dK/dV rows of oracle_varlen_L_bwd back to their owner rows, and
+    reading dQ by query, reproduces the float64 masked-dense autograd (and
+    the trie oracle); seeded packed accumulators pass through unchanged
+    (the backward accumulates)."""
+    tr = small_trie(n_tokens=140, depth=8, seed=21)
+    T, H, hd = tr.n_nodes, 2, 8
+    D = H * hd
+    Q, K, V, G = tensors(T, D, seed=22)
+    sc = scale_of(hd)
+    heads = np.flatnonzero(tr.radix_head)
+    R = heads.shape[0]
+    assert R < T  # some edges hold several rows, so L > 1 queries share a prefix
+    qoff = np.append(heads, T).astype(np.int32)
+    q2n = np.repeat(np.arange(R, dtype=np.int32), np.diff(qoff))
+    kv_rows, kv_off, kv_len = [], np.zeros(R, np.int32), np.zeros(R, np.int32)
+    for r in range(R):
+        path, a = [], int(qoff[r + 1]) - 1
+        while a >= 0:
+            path.append(a)
+            a = int(tr.parent[a])
+        kv_off[r], kv_len[r] = len(kv_rows), len(path)
+        kv_rows.extend(path[::-1])
+    kv_rows = np.array(kv_rows)
+    Kp, Vp = K[kv_rows], V[kv_rows]
+    max_kv = int(kv_len.max())
+    o, w = ORC.varlen_L_fwd(Q, Kp, Vp, q2n, qoff, kv_off, kv_len, T, H, hd, max_kv, sc)
+    seed = np.random.default_rng(5).standard_normal(kv_rows.size * D).astype(np.float32)
+    dq, dk, dv = ORC.varlen_L_bwd(Q, Kp, Vp, w, G, q2n, qoff, kv_off, kv_len, T, H, hd, max_kv, sc,
+                                  kv_rows.size, dk=seed, dv=seed)
+    dk_s = np.zeros((T, D))
+    dv_s = np.zeros((T, D))
+    np.add.at(dk_s, kv_rows, (dk - seed).reshape(-1, D))
+    np.add.at(dv_s, kv_rows, (dv - seed).reshape(-1, D))
+    bo, blse, bdq, bdk, bdv = brute_force(tr.parent, Q, K, V, G, H, hd, sc)
+    assert_close(o.reshape(T, D), bo, what="L O vs brute force")
+    assert_close(dq.reshape(T, D), bdq, what="L dQ vs brute force")
+    assert_close(dk_s, bdk, what="L scattered dK vs brute force")
+    assert_close(dv_s, bdv, what="L scattered dV vs brute force")
+    O, W, _ = ORC.fwd(tr.parent, Q, K, V, H, hd, sc)
+    dQ, dK, dV = ORC.bwd(tr.parent, Q, K, V, W, G, H, hd, sc)
+    assert_close(dk_s, dK, what="L scattered dK vs trie oracle")
+    assert_close(dv_s, dV, what="L scattered dV vs trie oracle")
+    # weights: query t's visible prefix only, and they sum to 1 per (t, h)
+    wv = w.reshape(T, H, max_kv)
+    vis = (kv_len[q2n] - np.diff(qoff)[q2n] + (np.arange(T) - qoff[q2n]) + 1)
+    assert np.allclose(wv.sum(-1), 1.0, atol=1e-6)
+    assert all(np.all(wv[t, :, vis[t]:] == 0) for t in range(T))
+
+
 # ------------------------------------------------- the spec's own agreement
 
 def _spec_chain_inputs():
