@@ -347,6 +347,7 @@ class TrieGPT:
         self.cos, self.sin = rope_tables(cfg.max_depth, hd, device=self.dev)
         self.groups = []  # (TrieAttention, TrieBatch) per batch of subtrees
         self.attn_hook = None  # called before and after every attention fwd / bwd (timing)
+        self.relu_hook = None  # called with (layer, FFN activation) after each ReLU (inspection)
 
     def plan(self, tr, mass_mode: int = L.MASS_LINEAR, max_rows: int = 1 << 20) -> None:
         """Splits the trie into batches of whole root-child subtrees (at most
@@ -426,6 +427,8 @@ class TrieGPT:
             x = x + _Lin.apply(o, P[f"wo{l}"], P[f"bo{l}"])
             n2, x = self._norm_res(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
             h = _LinRelu.apply(n2, P[f"w1{l}"], P[f"b1{l}"])
+            if self.relu_hook is not None:
+                self.relu_hook(l, h)
             x = x + _Lin.apply(h, P[f"w2{l}"], P[f"b2{l}"])
         logits = _Lin.apply(self._norm(x, P["nf_w"], P["nf_b"]), P["w_out"], P["b_out"])
         return _Loss.apply(logits, batch)

@@ -35,9 +35,16 @@ def _rope(x, pos, cos_t, sin_t, H, hd):
     return torch.stack([y0, y1], dim=-1).reshape(x.shape[0], H * hd)
 
 
-def step_f64(cfg, flat: np.ndarray, tr, mass: np.ndarray | None):
-    """Returns (loss, grad of the flat buffer) in float64."""
-    dt = torch.float64
+def step_f64(cfg, flat: np.ndarray, tr, mass: np.ndarray | None, dt=torch.float64, relu_masks=None):
+    """Returns (loss, grad of the flat buffer) in float64 (dt=torch.float32
+    gives the same model in float32 on the CPU: how far plain float32
+    arithmetic lands from float64 on a given model and trie).
+
+    relu_masks (per layer, bool [T, d_ff]) replaces the ReLU's own decision
+    (input > 0) by the given one: the gradient of the model that took the
+    same side of every kink. step_f64.relu_flips then holds, per layer, the
+    relative size |input| / mean |input| of the inputs where the given mask
+    differs from the float64 decision."""
     fl = torch.tensor(flat, dtype=dt, requires_grad=True)
     P, off = {}, 0
     for name, shape in param_shapes(cfg):
@@ -60,6 +67,7 @@ def step_f64(cfg, flat: np.ndarray, tr, mass: np.ndarray | None):
 
     x = P["tok_emb"][torch.from_numpy(tr.token.astype(np.int64))]
     T = x.shape[0]
+    margins, flips = [], []
     for l in range(cfg.n_layers):
         n1 = norm(x, P[f"n1_w{l}"], P[f"n1_b{l}"])
         q = _rope(n1 @ P[f"wq{l}"].T + P[f"bq{l}"], pos, cos_t, sin_t, H, hd).reshape(T, H, hd)
@@ -70,7 +78,17 @@ def step_f64(cfg, flat: np.ndarray, tr, mass: np.ndarray | None):
         o = torch.einsum("hij,jhd->ihd", torch.softmax(s, -1), v).reshape(T, D)
         x = x + o @ P[f"wo{l}"].T + P[f"bo{l}"]
         n2 = norm(x, P[f"n2_w{l}"], P[f"n2_b{l}"])
-        x = x + torch.relu(n2 @ P[f"w1{l}"].T + P[f"b1{l}"]) @ P[f"w2{l}"].T + P[f"b2{l}"]
+        pre = n2 @ P[f"w1{l}"].T + P[f"b1{l}"]
+        a = pre.detach().abs()
+        margins.append(float(a.min() / a.mean()))
+        if relu_masks is not None:
+            mk = torch.as_tensor(relu_masks[l])
+            flip = mk != (pre.detach() > 0)
+            flips.append((a[flip] / a.mean()).numpy())
+            act = torch.where(mk, pre, torch.zeros((), dtype=dt))
+        else:
+            act = torch.relu(pre)
+        x = x + act @ P[f"w2{l}"].T + P[f"b2{l}"]
     logits = norm(x, P["nf_w"], P["nf_b"]) @ P["w_out"].T + P["b_out"]
     logp = torch.log_softmax(logits, -1)
     p = logp.exp()
@@ -91,4 +109,9 @@ def step_f64(cfg, flat: np.ndarray, tr, mass: np.ndarray | None):
     w = torch.ones(T, dtype=dt) if mass is None else torch.tensor(mass, dtype=dt)
     loss = -(w[:, None] * tgt * torch.log(p + 1e-10)).sum()
     loss.backward()
+    # ReLU inputs nearest zero, relative to their mean size: an input within
+    # rounding of the kink may fall on the other side in float32, which
+    # changes the gradient by a whole unit's term (not by rounding).
+    step_f64.relu_margin = min(margins) if margins else float("inf")
+    step_f64.relu_flips = flips
     return float(loss.detach()), fl.grad.numpy()

@@ -98,3 +98,79 @@ def loss_batch(n_nodes, V, seed, max_edge=4, max_entries=6, dup=False, empty_fra
         token_ids=rng.integers(0, V, T_q).astype(np.int32), counts_offset=coff.astype(np.int32),
         counts_tok=ctok, counts_val=cval,
         edge_mass=rng.integers(1, 1000, R).astype(np.int32), edge_len_by_id=np.zeros(R, np.int32))
+
+
+def f64_key_grads(parent, Q, K, V, G, H, hd, scale, keys, rope=None, acc=None):
+    """float64 dK, dV of the given key rows: each key's sums over every query
+    of its subtree (dK[a] = R(pos_a)^T (sum ds_{n,a} q_n + acc_k[a]),
+    dV[a] = sum w_{n,a} dO_n + acc_v[a]), from each query's softmax over its
+    own path. parent in DFS preorder; rope = (cos, sin) tables or None."""
+    T = parent.shape[0]
+    depth = np.zeros(T, np.int64)
+    end = np.arange(1, T + 1)
+    for i in range(T):
+        depth[i] = 1 if parent[i] < 0 else depth[parent[i]] + 1
+    for i in range(T - 1, -1, -1):
+        if parent[i] >= 0:
+            end[parent[i]] = max(end[parent[i]], end[i])
+    D = H * hd
+    out_k = np.zeros((len(keys), D))
+    out_v = np.zeros((len(keys), D))
+    for x, a in enumerate(keys):
+        qs = np.arange(a, end[a])
+        da = int(depth[a])
+        # path of every query, root first; column da-1 is the key a
+        P = int(depth[qs].max())
+        path = np.full((qs.size, P), -1, np.int64)
+        cur = qs.copy()
+        for step in range(P):
+            col = depth[qs] - 1 - step
+            ok = (cur >= 0) & (col >= 0)
+            path[np.flatnonzero(ok), col[ok]] = cur[ok]
+            cur = np.where(cur >= 0, parent[np.maximum(cur, 0)], -1)
+        valid = path >= 0
+        safe = np.maximum(path, 0)
+        for h in range(H):
+            sl = slice(h * hd, (h + 1) * hd)
+            q = Q[qs, sl].astype(np.float64)
+            kp = K[safe, sl].astype(np.float64)
+            vp = V[safe, sl].astype(np.float64)
+            g = G[qs, sl].astype(np.float64)
+            s = np.einsum("nd,npd->np", q, kp) * scale
+            s = np.where(valid, s, -np.inf)
+            s -= s.max(1, keepdims=True)
+            w = np.exp(s)
+            w /= w.sum(1, keepdims=True)
+            dw = np.einsum("nd,npd->np", g, vp)
+            ds = w * (dw - (w * dw).sum(1, keepdims=True)) * scale
+            dk = (ds[:, da - 1, None] * q).sum(0)
+            dv = (w[:, da - 1, None] * g).sum(0)
+            if acc is not None:
+                dk += acc[0][a, sl]
+                dv += acc[1][a, sl]
+            if rope is not None:
+                pos = min(da - 1, rope[0].shape[0] - 1)
+                c = rope[0][pos].astype(np.float64)
+                sn = rope[1][pos].astype(np.float64)
+                d0, d1 = dk[0::2].copy(), dk[1::2].copy()
+                dk[0::2] = d0 * c[0::2] + d1 * sn[0::2]
+                dk[1::2] = -d0 * sn[0::2] + d1 * c[0::2]
+            out_k[x, sl] = dk
+            out_v[x, sl] = dv
+    return out_k, out_v
+
+
+def assert_close_or_f64(got, want, f64_rows, rtol=RTOL_F32, atol=ATOL_F32, what=""):
+    """assert_close elementwise against `want` (the float32 oracle); rows that
+    fail it must pass the same bar against their float64 value,
+    f64_rows(rows) -> [len(rows), D]. For sums over a key's whole subtree
+    (dK, dV), whose terms can be far larger than the result: two float32
+    summation orders then differ by more than 1e-4 of the result, and the
+    bar is held against the true value."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    bad = (np.abs(got - want) > atol + rtol * np.abs(want)).any(1)
+    rows = np.flatnonzero(bad)
+    assert rows.size <= 64, f"{what}: {rows.size} rows outside the bar against the oracle"
+    if rows.size:
+        assert_close(got[rows], f64_rows(rows), rtol, atol, f"{what} (rows {rows[:8].tolist()} vs float64)")

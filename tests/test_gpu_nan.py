@@ -5,11 +5,13 @@ The reference's divergence check is a NaN in the loss log
 vanish inside the attention (in a softmax max, a masked select or a
 rescale). One NaN is planted per case; the CPU oracle (plain IEEE C)
 computes which output elements it reaches. Bar: every element the oracle
-makes NaN is NaN on the GPU; every element finite on both sides matches at
-the usual tolerance; O, lse and dQ hold no NaN the oracle does not. dK / dV
-may hold more: a 16x16 block pair with a NaN query row multiplies its masked
-(zero-weight) pairs by that row, and 0 x NaN is NaN, so a NaN in Q or dO
-also reaches dK / dV of keys that share a block with that query.
+makes NaN is NaN on the GPU, and every element finite on both sides
+matches at the usual tolerance. The GPU may hold more NaN than the oracle,
+but only near the affected rows: a 16x16 block pair multiplies its masked
+(zero-weight) pairs by the operand rows as well, and 0 x NaN is NaN, so a
+NaN row also reaches the other rows of the block pairs it takes part in.
+Those rows lie in a 64-row tile that holds an affected row, or are
+ancestors (prefix keys) of such a tile's rows.
 """
 from __future__ import annotations
 
@@ -55,15 +57,26 @@ def test_nan_surfaces(gpu, dtype, H, hd, where):
     dQ, dK, dV = ORC.bwd(tr.parent, Q, K, V, W, G, H, hd, sc)
     got = _run(tr.parent, Q, K, V, G, H, hd, dtype)
     rtol, atol = (RTOL_F32, ATOL_F32) if dtype == "f32" else (RTOL_BF16, ATOL_BF16)
+    want = (Oo, lse_o, dQ, dK, dV)
+    affected = np.zeros(T, bool)
+    for w in want:
+        affected |= np.isnan(w).reshape(T, -1).any(1)
+    # rows of the 64-row tiles holding an affected row, and their ancestors
+    near = np.isin(np.arange(T) // 64, np.unique(np.flatnonzero(affected) // 64))
+    cur = np.flatnonzero(near)
+    while cur.size:
+        cur = tr.parent[cur]
+        cur = cur[cur >= 0]
+        cur = cur[~near[cur]]
+        near[cur] = True
     n_reached = 0
-    for name, g, w in zip(("O", "lse", "dQ", "dK", "dV"), got, (Oo, lse_o, dQ, dK, dV)):
+    for name, g, w in zip(("O", "lse", "dQ", "dK", "dV"), got, want):
         wn, gn = np.isnan(w), np.isnan(g)
         n_reached += int(wn.sum())
         missed = wn & ~gn
         assert not missed.any(), f"{name}: {int(missed.sum())} NaN outputs of the oracle are not NaN"
-        extra = gn & ~wn
-        if name in ("O", "lse", "dQ"):
-            assert not extra.any(), f"{name}: {int(extra.sum())} NaN outputs the oracle does not have"
+        extra_rows = (gn & ~wn).reshape(T, -1).any(1)
+        assert not (extra_rows & ~near).any(), f"{name}: NaN in rows away from the affected ones"
         both = ~wn & ~gn
         if dtype == "f32":
             err = np.abs(g - w)[both]

@@ -248,6 +248,28 @@ def test_varlen_layout_equals_trie():
     assert_close(dv_s, dV, what="scatter dV")
 
 
+@pytest.mark.parametrize("rope,acc", [(False, False), (True, True)])
+def test_f64_key_grads_equals_bruteforce(rope, acc):
+    """The float64 subtree sums the GPU parity tests fall back to for
+    cancelling dK/dV rows (helpers.f64_key_grads) equal the masked-dense
+    float64 autograd, with RoPE and accumulator seeds."""
+    from helpers import f64_key_grads
+    tr = small_trie(n_tokens=150, depth=9, seed=31)
+    T, H, hd = tr.n_nodes, 2, 8
+    Q, K, V, G = tensors(T, H * hd, seed=32)
+    sc = scale_of(hd)
+    accs = None
+    if acc:
+        rng = np.random.default_rng(3)
+        accs = [rng.standard_normal((T, H * hd)).astype(np.float32) for _ in range(2)]
+    _, _, _, bdk, bdv = brute_force(tr.parent, Q, K, V, G, H, hd, sc, rope=rope, acc=accs)
+    keys = np.arange(T)
+    rt = ORC.rope_table(64, hd) if rope else None
+    dk, dv = f64_key_grads(tr.parent, Q, K, V, G, H, hd, sc, keys, rope=rt, acc=accs)
+    assert np.abs(dk - bdk).max() <= 1e-5 * max(np.abs(bdk).max(), 1.0)
+    assert np.abs(dv - bdv).max() <= 1e-9 * max(np.abs(bdv).max(), 1.0)
+
+
 def test_varlen_L_layout_equals_bruteforce():
     """The radix chunk-packer layout (agpt_train.cu:4456-4479): the queries
     of radix node i are its edge rows, its packed prefix is its ancestor
