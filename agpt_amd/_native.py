@@ -54,6 +54,7 @@ ATTN_SYMBOLS = {
     "agpt_attn_create": (C.c_int, [C.POINTER(AttnConfig), C.POINTER(_vp)]),
     "agpt_attn_destroy": (C.c_int, [_vp]),
     "agpt_attn_plan": (C.c_int, [_vp, _i32p, C.c_int64]),
+    "agpt_attn_plan_static": (C.c_int, [_vp, _i32p, C.c_int64]),
     "agpt_attn_plan_radix": (C.c_int, [_vp, _i32p, _i32p, C.c_int64]),
     "agpt_attn_plan_info": (C.c_int, [_vp, _i64p, _i64p, _i64p, _i32p]),
     "agpt_attn_describe": (C.c_char_p, [_vp]),

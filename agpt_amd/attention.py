@@ -90,6 +90,15 @@ class TrieAttention:
                                          par.shape[0]))
         self.n_nodes = int(par.shape[0])
 
+    def plan_static(self, parent: np.ndarray) -> None:
+        """plan() with every device table and workspace in the library's
+        static scratch (agpt_attn_plan_static: no device allocation; one
+        such plan is live per device at a time)."""
+        par = np.ascontiguousarray(parent, dtype=np.int32)
+        N.check(self._lib.agpt_attn_plan_static(self._h, par.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                par.shape[0]))
+        self.n_nodes = int(par.shape[0])
+
     def plan_radix(self, radix_parent: np.ndarray, edge_len: np.ndarray) -> None:
         rp = np.ascontiguousarray(radix_parent, dtype=np.int32)
         el = np.ascontiguousarray(edge_len, dtype=np.int32)

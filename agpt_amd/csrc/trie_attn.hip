@@ -32,6 +32,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -581,32 +582,92 @@ struct agpt_attn_s {
   size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0;
   int max_lds = 65536;
   std::string desc;
+  // plan placed in the library's static scratch (agpt_attn_plan_static):
+  // nothing to free; valid while static_gen is the device's latest
+  bool static_plan = false;
+  uint64_t static_gen = 0;
 };
 
 namespace {
 
 void free_plan(agpt_attn_s* h) {
+  // A static plan's buffers live in the library's scratch array: they are
+  // dropped, not freed.
+  const bool own = !h->static_plan;
   int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
                     &h->d_prefix,   &h->d_q_item_off,  &h->d_k_item_off};
   for (auto p : ip)
     if (*p) {
-      (void)hipFree(*p);
+      if (own) (void)hipFree(*p);
       *p = nullptr;
     }
   float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv, &h->d_Dl, &h->d_E, &h->d_F};
   for (auto p : fp)
     if (*p) {
-      (void)hipFree(*p);
+      if (own) (void)hipFree(*p);
       *p = nullptr;
     }
   int32_t** op[] = {&h->d_q_items, &h->d_k_items, &h->d_sched};
   for (auto p : op)
     if (*p) {
-      (void)hipFree(*p);
+      if (own) (void)hipFree(*p);
       *p = nullptr;
     }
   h->planned = false;
+  h->static_plan = false;
 }
+
+// ---- static scratch (agpt_attn_plan_static) ---------------------------------
+// A plan's device tables and workspace, for callers that cannot allocate,
+// live in this file-scope array: one copy per device, held until the process
+// ends. Host code never uses the array's name as an address: each device's
+// copy is looked up once with hipGetSymbolAddress (that device current) and
+// its address kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = AGPT_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};
+uint64_t g_scratch_gen[kMaxDevices] = {};  // the device's latest static plan
+
+// Device address of the current device's scratch (looked up on first use).
+int scratch_base(int dev, unsigned char** out) {
+  if (dev < 0 || dev >= kMaxDevices) return set_error(AGPT_ERR_DEVICE, "device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return AGPT_OK;
+}
+
+bool static_plan_current(const agpt_attn_s* h) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return h->static_gen == g_scratch_gen[h->device];
+}
+
+// Device buffers of a plan: hipMalloc, or 256-byte aligned slices of the
+// static scratch. Past the scratch's end it keeps counting (no address is
+// handed out) so the caller can report the bytes the batch needs.
+struct Arena {
+  unsigned char* base = nullptr;  // null: hipMalloc
+  size_t used = 0;
+  bool overflow = false;
+  int get(void** p, size_t bytes) {
+    bytes = std::max<size_t>(bytes, 16);
+    if (!base) {
+      HIP_TRY(hipMalloc(p, bytes));
+      return AGPT_OK;
+    }
+    const size_t off = (used + 255) & ~static_cast<size_t>(255);
+    used = off + bytes;
+    if (used > kScratchBytes) overflow = true;
+    *p = overflow ? nullptr : base + off;
+    return AGPT_OK;
+  }
+};
 
 bool head_dim_supported(int hd) { return hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64; }
 
@@ -854,14 +915,15 @@ void choose_variant(agpt_attn_s* h, int& tile) {
 }
 
 template <typename T>
-int upload(T** dst, const std::vector<T>& src) {
+int upload(Arena& ar, T** dst, const std::vector<T>& src) {
   const size_t bytes = std::max<size_t>(src.size(), 1) * sizeof(T);
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(dst), bytes));
-  if (!src.empty()) HIP_TRY(hipMemcpy(*dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice));
+  int rc = ar.get(reinterpret_cast<void**>(dst), bytes);
+  if (rc != AGPT_OK) return rc;
+  if (*dst && !src.empty()) HIP_TRY(hipMemcpy(*dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice));
   return AGPT_OK;
 }
 
-int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
+int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n, Arena& ar) {
   free_plan(h);
   std::vector<int32_t> depth(static_cast<size_t>(n)), end(static_cast<size_t>(n));
   int rc = agpt_attn_check_tree(parent, n, depth.data(), end.data());
@@ -980,20 +1042,21 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
   h->n_chunks = (n_tiles + kChunkTiles - 1) / kChunkTiles;
   h->sum_depth = sumd;
   h->n_prefix_rows = pref_off[n_tiles];
+  h->static_plan = ar.base != nullptr;  // from here on free_plan must not free
   std::vector<int32_t> par(parent, parent + n);
-  if ((rc = upload(&h->d_parent, par)) != AGPT_OK) return rc;
-  if ((rc = upload(&h->d_depth, depth)) != AGPT_OK) return rc;
-  if ((rc = upload(&h->d_end, end)) != AGPT_OK) return rc;
-  if ((rc = upload(&h->d_pref_off, pref_off)) != AGPT_OK) return rc;
-  if ((rc = upload(&h->d_prefix, prefix)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_parent, par)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_depth, depth)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_end, end)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_pref_off, pref_off)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_prefix, prefix)) != AGPT_OK) return rc;
   if (h->variant == 5) {
-    if ((rc = upload(&h->d_q_items, q_items)) != AGPT_OK) return rc;
-    if ((rc = upload(&h->d_k_items, k_items)) != AGPT_OK) return rc;
-    if ((rc = upload(&h->d_q_item_off, q_off)) != AGPT_OK) return rc;
-    if ((rc = upload(&h->d_k_item_off, k_off)) != AGPT_OK) return rc;
+    if ((rc = upload(ar, &h->d_q_items, q_items)) != AGPT_OK) return rc;
+    if ((rc = upload(ar, &h->d_k_items, k_items)) != AGPT_OK) return rc;
+    if ((rc = upload(ar, &h->d_q_item_off, q_off)) != AGPT_OK) return rc;
+    if ((rc = upload(ar, &h->d_k_item_off, k_off)) != AGPT_OK) return rc;
   }
   if (h->variant == 6) {
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_sched), kSchedBytes));
+    if ((rc = ar.get(reinterpret_cast<void**>(&h->d_sched), kSchedBytes)) != AGPT_OK) return rc;
     // Up to 24 tiles per claim (the carry's reach), but at least ~8 chunks
     // per CU: a plan of few tiles (C5: 2048) would otherwise leave most
     // workgroups without a chunk.
@@ -1003,20 +1066,23 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n) {
     h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", dflt));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
   }
+  auto fl = [&](float** p, size_t bytes) { return ar.get(reinterpret_cast<void**>(p), bytes); };
   if (h->carry) {
     const size_t ebytes = static_cast<size_t>(h->n_chunks_sched) * agpt_blk::prefix_cap(maxd) * 2 * D * sizeof(float);
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_E), std::max<size_t>(ebytes, 16)));
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_F), std::max<size_t>(ebytes, 16)));
+    if ((rc = fl(&h->d_E, ebytes)) != AGPT_OK || (rc = fl(&h->d_F, ebytes)) != AGPT_OK) return rc;
   } else {
     const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pk), pbytes));
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Pv), pbytes));
+    if ((rc = fl(&h->d_Pk, pbytes)) != AGPT_OK || (rc = fl(&h->d_Pv, pbytes)) != AGPT_OK) return rc;
     const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Ck), cbytes));
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Cv), cbytes));
+    if ((rc = fl(&h->d_Ck, cbytes)) != AGPT_OK || (rc = fl(&h->d_Cv, cbytes)) != AGPT_OK) return rc;
   }
   if (h->variant == 5 || h->variant == 6)
-    HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_Dl), static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float)));
+    if ((rc = fl(&h->d_Dl, static_cast<size_t>(n) * h->cfg.n_heads * sizeof(float))) != AGPT_OK) return rc;
+  if (ar.overflow)
+    return set_error(AGPT_ERR_INVALID_ARG,
+                     "agpt_attn_plan_static: the batch needs %zu bytes of device tables and workspace, more "
+                     "than the %zu bytes of static scratch (AGPT_STATIC_SCRATCH_BYTES); use agpt_attn_plan",
+                     ar.used, kScratchBytes);
   h->planned = true;
   g_last_error.clear();
   return AGPT_OK;
@@ -1028,7 +1094,30 @@ extern "C" int agpt_attn_plan(agpt_attn_handle h, const int32_t* parent, int64_t
   if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
   if (n < 1 || !parent) return set_error(AGPT_ERR_INVALID_ARG, "empty tree or null parent table");
   HIP_TRY(hipSetDevice(h->device));
-  const int rc = plan_impl(h, parent, n);
+  Arena ar;
+  const int rc = plan_impl(h, parent, n, ar);
+  if (rc != AGPT_OK) free_plan(h);
+  return rc;
+}
+
+extern "C" int agpt_attn_plan_static(agpt_attn_handle h, const int32_t* parent, int64_t n) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (n < 1 || !parent) return set_error(AGPT_ERR_INVALID_ARG, "empty tree or null parent table");
+  if (h->planned && !h->static_plan)
+    return set_error(AGPT_ERR_INVALID_ARG,
+                     "agpt_attn_plan_static: the handle holds an allocated plan (freeing it would call "
+                     "hipFree); use a handle without one");
+  HIP_TRY(hipSetDevice(h->device));
+  Arena ar;
+  int rc = scratch_base(h->device, &ar.base);
+  if (rc != AGPT_OK) return rc;
+  {
+    // Claim the scratch first: an earlier static plan on this device stops
+    // being valid whatever happens next.
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    h->static_gen = ++g_scratch_gen[h->device];
+  }
+  rc = plan_impl(h, parent, n, ar);
   if (rc != AGPT_OK) free_plan(h);
   return rc;
 }
@@ -1437,6 +1526,8 @@ extern "C" int agpt_attn_fwd(agpt_attn_handle h, const void* q, const void* k, c
                              void* o, float* lse, const agpt_attn_opts* opts) {
   if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
   if (!h->planned) return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_fwd before agpt_attn_plan");
+  if (h->static_plan && !static_plan_current(h))
+    return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_fwd: a later agpt_attn_plan_static on this device took the scratch");
   if (!q || !k || !v || !o || !lse) return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse))
     return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
@@ -1463,6 +1554,8 @@ extern "C" int agpt_attn_bwd(agpt_attn_handle h, const void* q, const void* k, c
                              const agpt_attn_opts* opts) {
   if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
   if (!h->planned) return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_bwd before agpt_attn_plan");
+  if (h->static_plan && !static_plan_current(h))
+    return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_bwd: a later agpt_attn_plan_static on this device took the scratch");
   if (!q || !k || !v || !o || !lse || !d_o || !dq || !dk || !dv)
     return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
   const void* ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv};

@@ -105,7 +105,28 @@ int agpt_attn_destroy(agpt_attn_handle h);
  * batched_depth_forward.cr:342-361. */
 int agpt_attn_plan(agpt_attn_handle h, const int32_t* parent, int64_t n_nodes);
 
-/* Same, but the tree arrives as radix nodes (agpt_train.cu:892-940): radix
+/* Size of the static scratch array agpt_attn_plan_static places a plan in,
+ * per device. */
+#define AGPT_STATIC_SCRATCH_BYTES (64u << 20)
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same contract and results as agpt_attn_plan, but every
+ * device table and workspace of the plan is placed in a static array of the
+ * library (AGPT_STATIC_SCRATCH_BYTES = 64 MiB per device, held until the
+ * process ends) instead of being allocated: the call makes no hipMalloc or
+ * hipFree (its only device calls are hipMemcpy uploads of the tables and,
+ * once per device, hipGetSymbolAddress). A batch needing more returns
+ * AGPT_ERR_INVALID_ARG with the bytes it needs (an fp32 batch with 8 heads
+ * x 16 at depth 32 fits up to ~60K node-tokens). fwd/bwd then run unchanged.
+ * Every static plan on a device shares that device's array: each call takes
+ * it over, and fwd/bwd of a handle whose plan an earlier static plan made
+ * return AGPT_ERR_NO_PLAN. Work of the previous static plan still running on
+ * a stream races with this call's uploads: the caller orders them. Rejects a
+ * handle that holds an allocated plan (releasing it would call hipFree). */
+int agpt_attn_plan_static(agpt_attn_handle h, const int32_t* parent, int64_t n_nodes);
+
+/* agpt_attn_plan, but the tree arrives as radix nodes (agpt_train.cu:892-940): radix
  * node r (DFS preorder, radix_parent[r] < r or -1) owns edge_len[r] >= 1
  * consecutive node-token rows; row j of the edge has the edge's previous row
  * as parent. Row order: radix nodes in order, edge rows in order. */
