@@ -21,6 +21,8 @@ AGPT_ERR_UNSUPPORTED = 4
 AGPT_ERR_DEVICE = 5
 AGPT_ERR_TOO_DEEP = 6
 
+AGPT_CTX_GLOBAL = 0
+AGPT_CTX_PACKED = 1
 AGPT_DTYPE_F32 = 0
 AGPT_DTYPE_BF16 = 1
 
@@ -55,6 +57,7 @@ ATTN_SYMBOLS = {
     "agpt_attn_destroy": (C.c_int, [_vp]),
     "agpt_attn_plan": (C.c_int, [_vp, _i32p, C.c_int64]),
     "agpt_attn_plan_static": (C.c_int, [_vp, _i32p, C.c_int64]),
+    "agpt_attn_plan_range": (C.c_int, [_vp, _i32p, C.c_int64, C.c_int64, C.c_int64, C.c_int]),
     "agpt_attn_plan_radix": (C.c_int, [_vp, _i32p, _i32p, C.c_int64]),
     "agpt_attn_plan_info": (C.c_int, [_vp, _i64p, _i64p, _i64p, _i32p]),
     "agpt_attn_describe": (C.c_char_p, [_vp]),

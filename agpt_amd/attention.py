@@ -71,6 +71,7 @@ class TrieAttention:
         N.check(self._lib.agpt_attn_create(C.byref(cfg), C.byref(h)))
         self._h = h
         self.n_nodes = 0
+        self.n_ctx = 0
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -89,6 +90,27 @@ class TrieAttention:
         N.check(self._lib.agpt_attn_plan(self._h, par.ctypes.data_as(C.POINTER(C.c_int32)),
                                          par.shape[0]))
         self.n_nodes = int(par.shape[0])
+        self.n_ctx = 0
+
+    def plan_range(self, parent: np.ndarray, row_begin: int, row_end: int, packed: bool = False) -> None:
+        """Plans rows [row_begin, row_end) of the trie `parent` (its whole DFS
+        table) as one batch (agpt_attn_plan_range). packed=False: forward /
+        backward take the whole trie's tensors, and the backward adds the
+        batch's share of dK/dV of its context rows (the ancestors of
+        row_begin before the range) into their rows: run the ranges of a
+        trie in ascending order. packed=True: the tensors hold the n_ctx
+        context rows (root first) and then the range's rows; the backward
+        writes the context rows' share into rows 0..n_ctx-1."""
+        par = np.ascontiguousarray(parent, dtype=np.int32)
+        mode = N.AGPT_CTX_PACKED if packed else N.AGPT_CTX_GLOBAL
+        N.check(self._lib.agpt_attn_plan_range(self._h, par.ctypes.data_as(C.POINTER(C.c_int32)),
+                                               par.shape[0], int(row_begin), int(row_end), mode))
+        self.n_ctx = 0
+        a = int(par[row_begin])
+        while a >= 0:
+            self.n_ctx += 1
+            a = int(par[a])
+        self.n_nodes = (row_end - row_begin + self.n_ctx) if packed else int(par.shape[0])
 
     def plan_static(self, parent: np.ndarray) -> None:
         """plan() with every device table and workspace in the library's
@@ -173,6 +195,76 @@ class TrieAttention:
                                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                         _addr(acc_dk), _addr(acc_dv), C.byref(opts)))
         return dq, dk, dv
+
+
+def partition_starts(radix_head: np.ndarray, depth: np.ndarray) -> np.ndarray:
+    """First rows of the bigram partitions (streaming_radix_builder.cr:212-240)
+    of a DFS-ordered trie: each root child whose radix edge is longer than
+    one token is one partition (key: its first two tokens); a root child
+    whose edge is one token is a partition of its own (second token 255),
+    and each subtree below it is one more (key: first token, that
+    subtree's first token)."""
+    rh = np.asarray(radix_head)
+    d = np.asarray(depth)
+    return np.flatnonzero((d == 1) | ((d == 2) & (rh != 0)))
+
+
+def range_batches(n_rows: int, max_rows: int, starts: np.ndarray | None = None) -> list[tuple[int, int]]:
+    """Contiguous row ranges covering [0, n_rows), each at most max_rows long
+    unless a single unit is longer; ranges are cut only at `starts` (the
+    units' first rows, e.g. partition_starts), or anywhere when None."""
+    if starts is None:
+        return [(a, min(a + max_rows, n_rows)) for a in range(0, n_rows, max_rows)]
+    bounds = np.append(np.asarray(starts, dtype=np.int64), n_rows)
+    if bounds[0] != 0:
+        raise ValueError("the first unit must start at row 0")
+    out, a = [], 0
+    for r in range(1, bounds.shape[0]):
+        if bounds[r] - a > max_rows and bounds[r - 1] > a:
+            out.append((a, int(bounds[r - 1])))
+            a = int(bounds[r - 1])
+    if n_rows > a:
+        out.append((a, n_rows))
+    return out
+
+
+class RangedTrieAttention:
+    """A trie processed as contiguous row ranges, one plan each (exact:
+    every range reads its context rows as keys and returns their share of
+    dK/dV). Forward and backward take the whole trie's [T, D] tensors; the
+    ranges run in ascending order on one stream."""
+
+    def __init__(self, n_heads: int, head_dim: int, parent: np.ndarray, ranges, max_depth: int = 32,
+                 dtype: torch.dtype = torch.float32):
+        self.ranges = list(ranges)
+        self.parts = []
+        par = np.ascontiguousarray(parent, dtype=np.int32)
+        for a, b in self.ranges:
+            att = TrieAttention(n_heads, head_dim, max_depth=max_depth, dtype=dtype)
+            att.plan_range(par, a, b)
+            self.parts.append(att)
+        self.n_nodes = int(par.shape[0])
+        self.n_heads, self.d_model, self.dtype = n_heads, n_heads * head_dim, dtype
+
+    def forward(self, q, k, v, *, scale=None, stream=None):
+        o = torch.empty_like(q)
+        lse = torch.empty(self.n_nodes, self.n_heads, device=q.device, dtype=torch.float32)
+        for att in self.parts:
+            att.forward(q, k, v, scale=scale, stream=stream, out=o, lse=lse)
+        return o, lse
+
+    def backward(self, q, k, v, o, lse, d_o, *, acc_dk=None, acc_dv=None, rope=None, scale=None, stream=None):
+        out = tuple(torch.empty(self.n_nodes, self.d_model, device=q.device, dtype=torch.float32)
+                    for _ in range(3))
+        for att in self.parts:
+            att.backward(q, k, v, o, lse, d_o, acc_dk=acc_dk, acc_dv=acc_dv, rope=rope, scale=scale,
+                         stream=stream, out=out)
+        return out
+
+    def close(self) -> None:
+        for att in self.parts:
+            att.close()
+        self.parts = []
 
 
 # -- packed varlen drop-ins (µGPT extern argument meaning) --------------------

@@ -67,7 +67,8 @@ struct PlanDev {
   const int32_t* depth;
   const int32_t* end;
   const int32_t* pref_off;  // [n_tiles + 1]
-  const int32_t* prefix;    // [pref_off[n_tiles]]
+  const int32_t* prefix;    // [pref_off[n_tiles]] rows; negative: context rows before the batch
+  const int32_t* pref_end;  // [pref_off[n_tiles]] subtree end (batch rows) of each prefix entry
   int64_t T;
   int32_t n_tiles;
   int32_t max_depth;
@@ -108,7 +109,7 @@ __device__ __forceinline__ void load_tile(const PlanDev& pl, int t, int64_t s, i
   for (int i = threadIdx.x; i < A; i += blockDim.x) {
     const int32_t a = pl.prefix[off + i];
     sh.prefix[i] = a;
-    if (need_ends) sh.prefix_end[i] = pl.end[a];
+    if (need_ends) sh.prefix_end[i] = pl.pref_end[off + i];
   }
 }
 
@@ -526,6 +527,76 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Context rows of a range plan (agpt_attn_plan_range): the ancestors of the
+// batch's row 0 that lie before the batch are prefix entries d = 0 ..
+// n_ctx-1 of tile 0, read as keys by every tile in their subtree. Their
+// share of dK/dV over the batch's queries sits in the backward's partials:
+// entry d of every tile inside the key's subtree (Pk/Pv, tile by tile) or,
+// with the path carry, of every chunk inside it (E: [chunk][P][2][D]). One
+// workgroup per (key, 4 columns of dK or of dV): each thread sums a strided
+// subset of the parts in order, then a fixed-order tree in LDS (no
+// atomics: reruns give the same bytes); inverse RoPE at the key's depth;
+// the result is added into the key's row (its owner batch wrote it) or
+// written there (a packed batch).
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void trie_ctx_kernel(PlanDev pl, const float* __restrict__ Pk,
+                                                       const float* __restrict__ Pv, int from_chunks, int P,
+                                                       int rows_per_part, int n_parts, float* __restrict__ dK,
+                                                       float* __restrict__ dV, RopeArgs rope, int H, int add) {
+  const int d = blockIdx.y;
+  const int D = H * HD;
+  const int tv = static_cast<int>(blockIdx.x) / (D / 4);  // 0: dK, 1: dV
+  const int col = (static_cast<int>(blockIdx.x) - tv * (D / 4)) * 4;
+  const int64_t a = pl.prefix[d];
+  const int64_t ea = pl.pref_end[d];
+  const int np = static_cast<int>(min(static_cast<int64_t>(n_parts), (ea + rows_per_part - 1) / rows_per_part));
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int p = threadIdx.x; p < np; p += blockDim.x) {
+    const float* src = from_chunks
+                           ? Pk + ((static_cast<int64_t>(p) * P + d) * 2 + tv) * D + col
+                           : (tv ? Pv : Pk) + (static_cast<int64_t>(pl.pref_off[p]) + d) * D + col;
+    float y[4];
+    load_vec<4>(src, y);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) v[x] += y[x];
+  }
+  __shared__ float red[256][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) red[threadIdx.x][x] = v[x];
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (static_cast<int>(threadIdx.x) < s)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) red[threadIdx.x][x] += red[threadIdx.x + s][x];
+    __syncthreads();
+  }
+  if (threadIdx.x != 0) return;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) v[x] = red[0][x];
+  if (tv == 0 && rope.cos_t) {
+    const int pos = rope_pos(d + 1, rope.seq_len);
+#pragma unroll
+    for (int p = 0; p < 4; p += 2) {
+      const int j = (col + p) % HD;  // even: pair (j, j+1) of the head
+      const float c = rope.cos_t[pos * HD + j];
+      const float sn = rope.sin_t[pos * HD + j];
+      const float x0 = v[p], x1 = v[p + 1];
+      v[p] = x0 * c + x1 * sn;
+      v[p + 1] = -x0 * sn + x1 * c;
+    }
+  }
+  float* out = (tv ? dV : dK) + a * D + col;
+  if (add) {
+    float y[4];
+    load_vec<4>(out, y);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) v[x] += y[x];
+  }
+  store_vec<4>(out, v);
+}
+
 }  // namespace
 
 #include "trie_fast.h"
@@ -552,6 +623,14 @@ struct agpt_attn_s {
   int32_t* d_end = nullptr;
   int32_t* d_pref_off = nullptr;
   int32_t* d_prefix = nullptr;
+  int32_t* d_pref_end = nullptr;
+  // batch placement (agpt_attn_plan_range): the caller's tensors hold the
+  // batch's row 0 at row row_off; n_ctx context rows (ancestors of row 0
+  // before the batch) are keys only; ctx_add: their share of dK/dV is added
+  // into their rows (else written)
+  int64_t row_off = 0;
+  int32_t n_ctx = 0;
+  bool ctx_add = true;
   // workspace: prefix partials, chunk sums, δ
   float* d_Pk = nullptr;
   float* d_Pv = nullptr;
@@ -595,7 +674,7 @@ void free_plan(agpt_attn_s* h) {
   // dropped, not freed.
   const bool own = !h->static_plan;
   int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
-                    &h->d_prefix,   &h->d_q_item_off,  &h->d_k_item_off};
+                    &h->d_prefix,   &h->d_pref_end,    &h->d_q_item_off,  &h->d_k_item_off};
   for (auto p : ip)
     if (*p) {
       if (own) (void)hipFree(*p);
@@ -678,6 +757,7 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.end = h->d_end;
   p.pref_off = h->d_pref_off;
   p.prefix = h->d_prefix;
+  p.pref_end = h->d_pref_end;
   p.T = h->T;
   p.n_tiles = h->n_tiles;
   p.max_depth = h->max_depth;
@@ -923,11 +1003,26 @@ int upload(Arena& ar, T** dst, const std::vector<T>& src) {
   return AGPT_OK;
 }
 
-int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n, Arena& ar) {
+// Plans the batch rows A0 .. n_ext-1 of an extended parent table whose first
+// A0 rows are the batch's context: the ancestors of its first row that lie
+// before the batch (a chain, root first). ctx_local[j] is the row of context
+// row j in the caller's tensors, relative to the batch's row 0 (negative).
+// The device tables cover the batch rows only; prefix entries name rows in
+// that relative numbering, so a context row is an ordinary prefix key.
+int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
+              const std::vector<int32_t>& ctx_local, Arena& ar) {
   free_plan(h);
-  std::vector<int32_t> depth(static_cast<size_t>(n)), end(static_cast<size_t>(n));
-  int rc = agpt_attn_check_tree(parent, n, depth.data(), end.data());
+  std::vector<int32_t> dext(static_cast<size_t>(n_ext)), eext(static_cast<size_t>(n_ext));
+  int rc = agpt_attn_check_tree(ext, n_ext, dext.data(), eext.data());
   if (rc != AGPT_OK) return rc;
+  const int64_t n = n_ext - A0;
+  auto loc = [&](int32_t x) -> int32_t { return x < 0 ? -1 : x < A0 ? ctx_local[x] : x - A0; };
+  std::vector<int32_t> parent(static_cast<size_t>(n)), depth(static_cast<size_t>(n)), end(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) {
+    parent[i] = loc(ext[A0 + i]);
+    depth[i] = dext[A0 + i];
+    end[i] = static_cast<int32_t>(eext[A0 + i] - A0);
+  }
   int32_t maxd = 1;
   int64_t sumd = 0;
   for (int64_t i = 0; i < n; ++i) {
@@ -944,12 +1039,14 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n, Arena& ar) {
   for (int32_t t = 0; t < n_tiles; ++t) pref_off[t + 1] = pref_off[t] + depth[static_cast<int64_t>(t) * tile] - 1;
   pref_off[n_tiles + 1] = pref_off[n_tiles];  // sentinel read by the reducer
   std::vector<int32_t> prefix(static_cast<size_t>(pref_off[n_tiles]));
+  std::vector<int32_t> pref_end(prefix.size());
   for (int32_t t = 0; t < n_tiles; ++t) {
     const int64_t s = static_cast<int64_t>(t) * tile;
-    int32_t a = parent[s];
+    int32_t a = ext[A0 + s];  // walked in the extended table
     for (int d = depth[s] - 2; d >= 0; --d) {
-      prefix[pref_off[t] + d] = a;
-      a = parent[a];
+      prefix[pref_off[t] + d] = loc(a);
+      pref_end[pref_off[t] + d] = static_cast<int32_t>(eext[a] - A0);
+      a = ext[a];
     }
   }
   // Work items of the fast kernels: chain groups (each row the previous
@@ -1020,7 +1117,7 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n, Arena& ar) {
         return c == 0 ? A > 0 : parent[s + c] == s + c - 1;
       };
       auto range_len = [&](int k) {
-        if (k < A) return static_cast<int>(std::min<int64_t>(end[prefix[pref_off[t] + k]] - s, nt));
+        if (k < A) return static_cast<int>(std::min<int64_t>(pref_end[pref_off[t] + k] - s, nt));
         const int c = k - A;
         return static_cast<int>(std::min<int64_t>(end[s + c] - s, nt)) - c;
       };
@@ -1043,12 +1140,12 @@ int plan_impl(agpt_attn_s* h, const int32_t* parent, int64_t n, Arena& ar) {
   h->sum_depth = sumd;
   h->n_prefix_rows = pref_off[n_tiles];
   h->static_plan = ar.base != nullptr;  // from here on free_plan must not free
-  std::vector<int32_t> par(parent, parent + n);
-  if ((rc = upload(ar, &h->d_parent, par)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_parent, parent)) != AGPT_OK) return rc;
   if ((rc = upload(ar, &h->d_depth, depth)) != AGPT_OK) return rc;
   if ((rc = upload(ar, &h->d_end, end)) != AGPT_OK) return rc;
   if ((rc = upload(ar, &h->d_pref_off, pref_off)) != AGPT_OK) return rc;
   if ((rc = upload(ar, &h->d_prefix, prefix)) != AGPT_OK) return rc;
+  if ((rc = upload(ar, &h->d_pref_end, pref_end)) != AGPT_OK) return rc;
   if (h->variant == 5) {
     if ((rc = upload(ar, &h->d_q_items, q_items)) != AGPT_OK) return rc;
     if ((rc = upload(ar, &h->d_k_items, k_items)) != AGPT_OK) return rc;
@@ -1095,9 +1192,69 @@ extern "C" int agpt_attn_plan(agpt_attn_handle h, const int32_t* parent, int64_t
   if (n < 1 || !parent) return set_error(AGPT_ERR_INVALID_ARG, "empty tree or null parent table");
   HIP_TRY(hipSetDevice(h->device));
   Arena ar;
-  const int rc = plan_impl(h, parent, n, ar);
+  const int rc = plan_impl(h, parent, n, 0, {}, ar);
   if (rc != AGPT_OK) free_plan(h);
+  h->row_off = 0;
+  h->n_ctx = 0;
   return rc;
+}
+
+extern "C" int agpt_attn_plan_range(agpt_attn_handle h, const int32_t* parent, int64_t n_total,
+                                    int64_t row_begin, int64_t row_end, int ctx_mode) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  if (!parent || row_begin < 0 || row_end <= row_begin || row_end > n_total)
+    return set_error(AGPT_ERR_INVALID_ARG, "need 0 <= row_begin < row_end <= n_total and a parent table");
+  if (ctx_mode != AGPT_CTX_GLOBAL && ctx_mode != AGPT_CTX_PACKED)
+    return set_error(AGPT_ERR_INVALID_ARG, "ctx_mode %d", ctx_mode);
+  if (n_total >= (int64_t{1} << 31) - kMaxTileRows)
+    return set_error(AGPT_ERR_INVALID_ARG, "n_total %lld exceeds int32 row indexing", (long long)n_total);
+  // The context: ancestors of row_begin, root first (ascending rows).
+  std::vector<int64_t> chain;
+  for (int64_t a = parent[row_begin]; a >= 0; a = parent[a]) {
+    if (a >= row_begin || parent[a] >= a || parent[a] < -1)
+      return set_error(AGPT_ERR_NOT_DFS, "ancestor %lld of row_begin is not an earlier row", (long long)a);
+    if (static_cast<int>(chain.size()) >= kMaxDepth)
+      return set_error(AGPT_ERR_TOO_DEEP, "row_begin is deeper than %d", kMaxDepth);
+    chain.push_back(a);
+  }
+  std::reverse(chain.begin(), chain.end());
+  const int32_t A0 = static_cast<int32_t>(chain.size());
+  const int64_t n = row_end - row_begin;
+  std::vector<int32_t> ext(static_cast<size_t>(A0 + n));
+  for (int32_t j = 0; j < A0; ++j) ext[j] = j - 1;
+  for (int64_t g = row_begin; g < row_end; ++g) {
+    const int32_t p = parent[g];
+    int32_t e;
+    if (p >= g || p < -1) {
+      return set_error(AGPT_ERR_NOT_DFS, "parent[%lld] = %d is not an earlier row or -1", (long long)g, p);
+    } else if (p >= row_begin) {
+      e = static_cast<int32_t>(A0 + (p - row_begin));
+    } else if (p < 0) {
+      e = -1;
+    } else {
+      const auto it = std::lower_bound(chain.begin(), chain.end(), static_cast<int64_t>(p));
+      if (it == chain.end() || *it != p)
+        return set_error(AGPT_ERR_NOT_DFS,
+                         "row %lld: its parent %d lies before the range and is not an ancestor of row_begin",
+                         (long long)g, p);
+      e = static_cast<int32_t>(it - chain.begin());
+    }
+    ext[A0 + (g - row_begin)] = e;
+  }
+  std::vector<int32_t> ctx_local(static_cast<size_t>(A0));
+  for (int32_t j = 0; j < A0; ++j)
+    ctx_local[j] = static_cast<int32_t>(ctx_mode == AGPT_CTX_PACKED ? j - A0 : chain[j] - row_begin);
+  HIP_TRY(hipSetDevice(h->device));
+  Arena ar;
+  const int rc = plan_impl(h, ext.data(), A0 + n, A0, ctx_local, ar);
+  if (rc != AGPT_OK) {
+    free_plan(h);
+    return rc;
+  }
+  h->row_off = ctx_mode == AGPT_CTX_PACKED ? A0 : row_begin;
+  h->n_ctx = A0;
+  h->ctx_add = ctx_mode == AGPT_CTX_GLOBAL;
+  return AGPT_OK;
 }
 
 extern "C" int agpt_attn_plan_static(agpt_attn_handle h, const int32_t* parent, int64_t n) {
@@ -1117,8 +1274,10 @@ extern "C" int agpt_attn_plan_static(agpt_attn_handle h, const int32_t* parent, 
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     h->static_gen = ++g_scratch_gen[h->device];
   }
-  rc = plan_impl(h, parent, n, ar);
+  rc = plan_impl(h, parent, n, 0, {}, ar);
   if (rc != AGPT_OK) free_plan(h);
+  h->row_off = 0;
+  h->n_ctx = 0;
   return rc;
 }
 
@@ -1149,7 +1308,7 @@ extern "C" int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_par
 extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (!h) return "null handle";
   if (!h->planned) return "no plan";
-  char buf[320];
+  char buf[400];
   if (h->variant == 6)
     snprintf(buf, sizeof(buf),
              "streaming block-sparse 16x16 mfma, %s backward: tile_rows=%d tiles=%d heads_per_wg=%d "
@@ -1167,6 +1326,11 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   else
     snprintf(buf, sizeof(buf), "global-memory walk: tile_rows=%d tiles=%d", h->tile, h->n_tiles);
   h->desc = buf;
+  if (h->n_ctx > 0) {
+    snprintf(buf, sizeof(buf), "; range batch: %d context rows (%s)", h->n_ctx,
+             h->ctx_add ? "dK/dV added into their rows" : "dK/dV written to the packed rows");
+    h->desc += buf;
+  }
   return h->desc.c_str();
 }
 
@@ -1331,6 +1495,20 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   pm.mark(1);
 }
 
+// Finishes the context rows' share of dK/dV (range plans; see trie_ctx_kernel).
+template <int HD>
+void launch_ctx(const agpt_attn_s* h, float* dk, float* dv, RopeArgs rope, hipStream_t st) {
+  if (h->n_ctx <= 0) return;
+  const int D = h->cfg.n_heads * HD;
+  const bool chunks = h->variant == 6 && h->fused && h->carry;
+  const int P = agpt_blk::prefix_cap(h->max_depth);
+  const int rows = chunks ? h->chunk_tiles * agpt_blk::kTile : h->tile;
+  const int parts = chunks ? h->n_chunks_sched : h->n_tiles;
+  hipLaunchKernelGGL((trie_ctx_kernel<HD>), dim3(2 * D / 4, h->n_ctx), dim3(256), 0, st, plan_dev(h),
+                     chunks ? h->d_E : h->d_Pk, chunks ? h->d_E : h->d_Pv, chunks ? 1 : 0, P, rows, parts, dk, dv,
+                     rope, h->cfg.n_heads, h->ctx_add ? 1 : 0);
+}
+
 template <int HD, typename Tin>
 void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, const void* o,
                 const float* lse, const void* dO, float* dq, float* dk, float* dv,
@@ -1373,6 +1551,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
           hipLaunchKernelGGL((agpt_blk::bwd_carry_kernel<HD, PlanDev, RopeArgs>), dim3(h->n_chunks_sched - 1),
                              dim3(256), 0, st, plan_dev(h), h->d_E, h->d_F, dk, dv, acc_dk, acc_dv, rope,
                              h->cfg.n_heads);
+        launch_ctx<HD>(h, dk, dv, rope, st);
         pm.mark(4);
         return;
       }
@@ -1444,6 +1623,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   } else {
     pm.mark(3);
   }
+  launch_ctx<HD>(h, dk, dv, rope, st);
   pm.mark(4);
 }
 
@@ -1522,6 +1702,16 @@ void fit_scratch(agpt_attn_s* h) {
 
 }  // namespace
 
+namespace {
+// A tensor pointer moved to the batch's row 0 (range plans place it at row
+// row_off of the caller's tensors); rows are `bytes` long.
+template <typename T>
+T* at_batch(T* p, const agpt_attn_s* h, int64_t bytes) {
+  using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+  return p ? reinterpret_cast<T*>(reinterpret_cast<C*>(p) + h->row_off * bytes) : p;
+}
+}  // namespace
+
 extern "C" int agpt_attn_fwd(agpt_attn_handle h, const void* q, const void* k, const void* v,
                              void* o, float* lse, const agpt_attn_opts* opts) {
   if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
@@ -1529,8 +1719,19 @@ extern "C" int agpt_attn_fwd(agpt_attn_handle h, const void* q, const void* k, c
   if (h->static_plan && !static_plan_current(h))
     return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_fwd: a later agpt_attn_plan_static on this device took the scratch");
   if (!q || !k || !v || !o || !lse) return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(lse))
+  {
+    const int64_t row = static_cast<int64_t>(h->cfg.n_heads) * h->cfg.head_dim *
+                        (h->cfg.dtype == AGPT_DTYPE_F32 ? 4 : 2);
+    q = at_batch(q, h, row);
+    k = at_batch(k, h, row);
+    v = at_batch(v, h, row);
+    o = at_batch(o, h, row);
+    lse = at_batch(lse, h, 4 * static_cast<int64_t>(h->cfg.n_heads));
+  }
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(lse) & 3u) != 0)  // read and written one float at a time
+    return set_error(AGPT_ERR_INVALID_ARG, "lse must be 4-byte aligned");
   int rc = check_opts(opts);
   if (rc != AGPT_OK) return rc;
   HIP_TRY(hipSetDevice(h->device));
@@ -1558,9 +1759,26 @@ extern "C" int agpt_attn_bwd(agpt_attn_handle h, const void* q, const void* k, c
     return set_error(AGPT_ERR_NO_PLAN, "agpt_attn_bwd: a later agpt_attn_plan_static on this device took the scratch");
   if (!q || !k || !v || !o || !lse || !d_o || !dq || !dk || !dv)
     return set_error(AGPT_ERR_INVALID_ARG, "null tensor");
-  const void* ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv};
+  {
+    const int64_t D = static_cast<int64_t>(h->cfg.n_heads) * h->cfg.head_dim;
+    const int64_t row = D * (h->cfg.dtype == AGPT_DTYPE_F32 ? 4 : 2);
+    q = at_batch(q, h, row);
+    k = at_batch(k, h, row);
+    v = at_batch(v, h, row);
+    o = at_batch(o, h, row);
+    d_o = at_batch(d_o, h, row);
+    lse = at_batch(lse, h, 4 * static_cast<int64_t>(h->cfg.n_heads));
+    dq = at_batch(dq, h, 4 * D);
+    dk = at_batch(dk, h, 4 * D);
+    dv = at_batch(dv, h, 4 * D);
+    acc_dk = at_batch(acc_dk, h, 4 * D);
+    acc_dv = at_batch(acc_dv, h, 4 * D);
+  }
+  const void* ptrs[] = {q, k, v, o, d_o, dq, dk, dv, acc_dk, acc_dv};
   for (const void* p : ptrs)
     if (p && !aligned16(p)) return set_error(AGPT_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(lse) & 3u) != 0)  // read one float at a time
+    return set_error(AGPT_ERR_INVALID_ARG, "lse must be 4-byte aligned");
   int rc = check_opts(opts);
   if (rc != AGPT_OK) return rc;
   HIP_TRY(hipSetDevice(h->device));

@@ -422,12 +422,12 @@ struct BStream {
       const int j = tid + k * kThreads;
       const int d = j / PJ;
       const int rem = j % PJ;
-      const int id = d < n_A ? cp_id[k] : -1;
+      const int id = cp_id[k];
       int src = P, e = 0;  // cold or no entry: a dummy read
-      if (!cold && id >= s) {
+      if (!cold && d < n_A && id >= s) {
         src = P + (id - s);
         e = tb.tend[id - s];
-      } else if (!cold && id >= 0) {  // an ancestor of s: d < A
+      } else if (!cold && d < n_A) {  // an ancestor of s (a context row: negative): d < A
         src = P - A + d;
         e = tb.pend[d];
       }
@@ -491,7 +491,7 @@ struct BStream {
         const int id = pl.prefix[n_poff + d];
         *reinterpret_cast<u4*>((rem < CPR ? Ks : Vs) + (P - n_A + d) * WS + (rem % CPR) * EPC) =
             *reinterpret_cast<const u4*>(gsrc(rem < CPR ? K : V, id, rem % CPR));
-        if (rem == 0) set_prefix_entry(d, pl.end[id]);
+        if (rem == 0) set_prefix_entry(d, pl.pref_end[n_poff + d]);
       }
     }
     // Dead slots of the first prefix block, and the tile rows.

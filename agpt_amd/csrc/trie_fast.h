@@ -453,7 +453,7 @@ struct Stream {
         const int id = pl.prefix[n_poff + d];
         *reinterpret_cast<u4*>((rem < CPR ? Ks : Vs) + d * WS + (rem % CPR) * EPC) =
             *reinterpret_cast<const u4*>(gsrc(rem < CPR ? K : V, id, rem % CPR));
-        if (kK && rem == 0) tb.pend[d] = pl.end[id];
+        if (kK && rem == 0) tb.pend[d] = pl.pref_end[n_poff + d];
       }
     }
     const int lane = tid & 63;

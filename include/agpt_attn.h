@@ -105,6 +105,39 @@ int agpt_attn_destroy(agpt_attn_handle h);
  * batched_depth_forward.cr:342-361. */
 int agpt_attn_plan(agpt_attn_handle h, const int32_t* parent, int64_t n_nodes);
 
+/* Batches of one trie: a contiguous range of its DFS rows, e.g. a run of
+ * bigram partitions (the reference's --partition-depth batching,
+ * agpt_train.cu:3808-3890; subtree keys streaming_radix_builder.cr:212-240).
+ * The reference truncates the ancestor chain of a partition whose root
+ * child lives in another file (its known approximation,
+ * streaming_radix_builder.cr:46-55); here every row of the range attends
+ * its whole path: the ancestors of row_begin that lie before the range (the
+ * range's context, at most max_depth-1 rows) are read as keys, and the
+ * range's share of their dK/dV is returned to them:
+ *   AGPT_CTX_GLOBAL: fwd/bwd take the whole trie's tensors ([n_total, D]);
+ *     the range's rows are read and written in place, and bwd ADDS the
+ *     range's share of dK/dV of each context row into that row of dK/dV
+ *     (seeds and inverse RoPE as usual: the sum of the parts is the whole).
+ *     The batch holding a row as a query writes it, so the ranges of a trie
+ *     run in ascending row order, on one stream (or ordered by the caller).
+ *   AGPT_CTX_PACKED: fwd/bwd take tensors holding the range alone, after its
+ *     n_ctx context rows: rows 0..n_ctx-1 are the ancestors of row_begin,
+ *     root first (the reference's suggested context-only duplicate,
+ *     streaming_radix_builder.cr:53-55), then the range's rows. bwd WRITES
+ *     the range's share of dK/dV of the context rows into rows 0..n_ctx-1
+ *     (no seeds there; inverse RoPE applied) for the caller to add to their
+ *     owners; O, lse and dQ of those rows are not written.
+ * Context rows are keys only: they are not queries of the range. */
+#define AGPT_CTX_GLOBAL 0
+#define AGPT_CTX_PACKED 1
+
+/* Plans rows [row_begin, row_end) of a trie whose whole DFS parent table
+ * (n_total rows, host memory) is `parent`, as described above. n_ctx =
+ * depth(row_begin) - 1 (agpt_attn_plan_info's max_depth and n_nodes refer to
+ * the range). agpt_attn_plan(h, parent, n) is this with the whole trie. */
+int agpt_attn_plan_range(agpt_attn_handle h, const int32_t* parent, int64_t n_total,
+                         int64_t row_begin, int64_t row_end, int ctx_mode);
+
 /* Size of the static scratch array agpt_attn_plan_static places a plan in,
  * per device. */
 #define AGPT_STATIC_SCRATCH_BYTES (64u << 20)

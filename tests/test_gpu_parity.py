@@ -75,7 +75,66 @@ def _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=None, acc=None, max_depth
     return res
 
 
-def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0, normwise=False):
+def _run_gpu_ranges(tr_parent, Q, K, V, G, H, hd, dtype, ranges, packed, rope=None, acc=None, max_depth=None):
+    """The trie as contiguous row ranges, one plan each, in ascending order.
+    Whole-trie tensors (packed=False), or per range a packed copy [context
+    rows, range rows] whose context dK/dV share is added to the owner rows
+    here, in range order."""
+    import torch
+
+    from agpt_amd.attention import RangedTrieAttention, TrieAttention
+
+    dev = torch.device("cuda:0")
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    md = max_depth or max(1, int(ORC.depths(tr_parent).max()))
+    T, D = tr_parent.shape[0], H * hd
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    rt = None if rope is None else tuple(cu(x) for x in rope)
+    if not packed:
+        ratt = RangedTrieAttention(H, hd, tr_parent, ranges, max_depth=md, dtype=tdt)
+        print("kernel:", ratt.parts[-1].describe())
+        q, k, v, g = (cu(x).to(tdt).contiguous() for x in (Q, K, V, G))
+        o, lse = ratt.forward(q, k, v)
+        ak = None if acc is None else cu(acc[0])
+        av = None if acc is None else cu(acc[1])
+        dq, dk, dv = ratt.backward(q, k, v, o, lse, g, acc_dk=ak, acc_dv=av, rope=rt)
+        torch.cuda.synchronize()
+        res = [x.float().cpu().numpy() for x in (o, lse, dq, dk, dv)]
+        ratt.close()
+        return res
+    out = [np.zeros((T, D), np.float32), np.zeros((T, H), np.float32)] + [np.zeros((T, D), np.float64)
+                                                                         for _ in range(3)]
+    for a, b in ranges:
+        ctx = []
+        x = int(tr_parent[a])
+        while x >= 0:
+            ctx.append(x)
+            x = int(tr_parent[x])
+        rows = np.concatenate([np.array(ctx[::-1], np.int64), np.arange(a, b)])
+        nc = len(ctx)
+        att = TrieAttention(H, hd, max_depth=md, dtype=tdt)
+        att.plan_range(tr_parent, a, b, packed=True)
+        assert att.n_ctx == nc
+        q, k, v, g = (cu(x[rows]).to(tdt).contiguous() for x in (Q, K, V, G))
+        g[:nc] = 0  # context rows are not queries: their dO is unused
+        o, lse = att.forward(q, k, v)
+        ak = av = None
+        if acc is not None:  # the owner batch adds a row's seeds, context rows get none
+            ak, av = (cu(np.concatenate([np.zeros((nc, D), np.float32), s[a:b]])) for s in acc)
+        dq, dk, dv = att.backward(q, k, v, o, lse, g, acc_dk=ak, acc_dv=av, rope=rt)
+        torch.cuda.synchronize()
+        o, lse, dq, dk, dv = (x.float().cpu().numpy() for x in (o, lse, dq, dk, dv))
+        out[0][a:b], out[1][a:b], out[2][a:b] = o[nc:], lse[nc:], dq[nc:]
+        out[3][a:b] += dk[nc:]
+        out[4][a:b] += dv[nc:]
+        out[3][rows[:nc]] += dk[:nc]  # the range's share of its context rows, to their owners
+        out[4][rows[:nc]] += dv[:nc]
+        att.close()
+    return out
+
+
+def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0, normwise=False,
+           ranges=None, packed=False):
     T = tr_parent.shape[0]
     D = H * hd
     Q, K, V, G = tensors(T, D, seed, sharp=sharp)
@@ -87,7 +146,11 @@ def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0
     if acc:
         rng = np.random.default_rng(seed + 99)
         accs = [rng.standard_normal((T, D)).astype(np.float32) * np.float32(0.1) for _ in range(2)]
-    o, lse, dq, dk, dv = _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=rope_t, acc=accs)
+    if ranges is None:
+        o, lse, dq, dk, dv = _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=rope_t, acc=accs)
+    else:
+        o, lse, dq, dk, dv = _run_gpu_ranges(tr_parent, Q, K, V, G, H, hd, dtype, ranges, packed, rope=rope_t,
+                                             acc=accs)
     Oo, W, lse_o = ORC.fwd(tr_parent, Q, K, V, H, hd, scale)
     if dtype == "bf16":
         rtol, atol = RTOL_BF16, ATOL_BF16
@@ -185,6 +248,36 @@ def test_parity_c2_sample(gpu, rope):
     tr = trie.config_trie("C2", scale=0.0025)  # 2,750 chars -> ~60K node-tokens, depth 32
     assert tr.max_depth == 32
     _check(tr.parent, 8, 16, seed=2, rope=rope)
+
+
+@pytest.mark.parametrize("cut,packed", [("bigram", False), ("rows", False), ("rows", True)])
+def test_range_batches_equal_whole_trie(gpu, cut, packed):
+    """A C2-shaped trie processed as contiguous row ranges, each planned
+    alone, equals the oracle on the whole trie. Cuts at bigram partitions
+    (context: the one-token root child above a partition) or every 777 rows
+    (contexts of any depth, cuts inside subtrees). Every range reads its
+    out-of-range ancestors as keys and returns their share of dK/dV: added
+    in place in ascending range order, or written to the packed context rows
+    and added to the owners here."""
+    from agpt_amd import trie
+    from agpt_amd.attention import partition_starts, range_batches
+    tr = trie.config_trie("C2", scale=0.001)  # ~33K node-tokens, depth 32
+    if cut == "bigram":
+        ranges = range_batches(tr.n_nodes, 3000, partition_starts(tr.radix_head, tr.depth))
+    else:
+        ranges = range_batches(tr.n_nodes, 777)
+    assert len(ranges) > 8
+    _check(tr.parent, 8, 16, seed=6, rope=True, acc=True, ranges=ranges, packed=packed)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_range_batches_bf16_hd64(gpu, packed):
+    """Range batches at head_dim 64 with bf16 inputs (the C4 shape), on a
+    depth-40 trie cut every 500 rows."""
+    from agpt_amd.attention import range_batches
+    tr = small_trie(n_tokens=900, depth=40, seed=12)
+    _check(tr.parent, 2, 64, seed=7, dtype="bf16", rope=True, acc=True,
+           ranges=range_batches(tr.n_nodes, 500), packed=packed)
 
 
 @pytest.mark.parametrize("hd", [8, 16, 64])
