@@ -107,28 +107,43 @@ def make_inputs(tr, D, H, hd, dtype, seed, dev):
     return outs[0], outs[1], outs[2], d_o
 
 
-def cpu_baseline(tr, q, k, v, d_o, H, hd, rows: int) -> dict:
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the platform's."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(tr, q, k, v, d_o, H, hd, rows: int, reps: int = 5) -> dict:
     """The oracle (single-threaded C restatement of the Crystal CPU loops)
-    over the first `rows` DFS rows of the same trie and tensors."""
+    over the first `rows` DFS rows of the same trie and tensors: the median
+    of `reps` repetitions."""
     from oracle import oracle as ORC
-    import torch
     M = min(rows, tr.n_nodes)
     par = tr.parent[:M]
     dep = tr.depth[:M]
     Q, K, V, G = (x[:M].float().cpu().numpy() for x in (q, k, v, d_o))
     scale = float(np.float32(1.0 / np.sqrt(hd)))
-    t0 = time.perf_counter()
-    O, W, _ = ORC.fwd(par, Q, K, V, H, hd, scale, depth=dep)
-    ORC.bwd(par, Q, K, V, W, G, H, hd, scale, depth=dep)
-    dt = time.perf_counter() - t0
-    del torch
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O, W, _ = ORC.fwd(par, Q, K, V, H, hd, scale, depth=dep)
+        ORC.bwd(par, Q, K, V, W, G, H, hd, scale, depth=dep)
+        times.append(time.perf_counter() - t0)
+        del O, W
+    dt = float(np.median(times))
     return {"value": M / dt, "unit": "node-tokens/s", "cores": 1, "kind": "port",
             "sample": (f"first {M} DFS rows of the same trie (a closed sub-forest, "
                        f"{int(dep.astype(np.int64).sum())} keys attended), same Q/K/V/dO, "
                        f"oracle fwd+bwd (C restatement of cpu_grouped_attention + "
                        f"optimized_attention_backward_head + accumulators), 1 thread, "
-                       f"{dt:.1f} s on {platform.processor() or platform.machine()}, "
-                       f"nproc {os.cpu_count()}")}
+                       f"median of {reps} reps ({min(times):.2f}-{max(times):.2f} s each) on "
+                       f"{cpu_model()}, nproc {os.cpu_count()}")}
 
 
 LOSS_METRIC = "AGPT per-query loss (softmax + targets + d_logits) queries/sec (1 GPU)"
@@ -309,6 +324,23 @@ def load_traffic(name: str):
         return None
 
 
+def load_counters(workload: str, kernel: str) -> dict | None:
+    """The committed rocprofv3 counters of one kernel on one workload
+    (profiles/counters_<workload>.json: MfmaUtil, VALUBusy, occupancy,
+    FETCH_SIZE / WRITE_SIZE scaled to HBM bytes, and the commit measured)."""
+    p = ROOT / "profiles" / f"counters_{workload}.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    k = d.get("kernels", {}).get(kernel)
+    if k is None:
+        return None
+    return {"commit": d.get("commit"), **k}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -322,7 +354,7 @@ def main() -> int:
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
                          "one GPU holds)")
-    ap.add_argument("--cpu-rows", type=int, default=1_000_000)
+    ap.add_argument("--cpu-rows", type=int, default=250_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC byte-counter "
@@ -436,6 +468,7 @@ def main() -> int:
         log(f"cpu baseline: {cpu['value']:.0f} node-tokens/s")
 
     flops = 12.0 * tr.sum_depth * D
+    ctr = load_counters(args.workload, dominant) if args.scale == cfg.get("one_gpu_scale", 1.0) else None
     out = {
         "metric": METRIC,
         "value": value,
@@ -458,9 +491,15 @@ def main() -> int:
         "roofline": {
             "bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": load_traffic(f"{dominant}_{args.workload}"),
+            "traffic": (ctr or {}).get("traffic_bytes"),
             "algorithmic_bytes_per_launch": kern_bytes[dominant],
             "avg_launch_ms": avg[dominant],
+            "mfma_util": (ctr or {}).get("mfma_util"),
+            "counters": None if ctr is None else {
+                "source": f"profiles/counters_{args.workload}.md", "commit": ctr["commit"],
+                "mfma_util": ctr["mfma_util"], "valu_busy": ctr["valu_busy"],
+                "occupancy": ctr["occupancy"], "lds_bank_conflict": ctr["lds_bank_conflict"],
+                "mfma_tflop_executed": (ctr["mfma_flop_f32"] + ctr["mfma_flop_bf16"]) / 1e12},
         },
         "step_roofline": {"bytes_per_node_token": bpt["step"], "achieved_GBps": step_gbs,
                           "frac": step_gbs / HBM_PEAK_GBS,
