@@ -354,6 +354,9 @@ def main() -> int:
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
                          "one GPU holds)")
+    ap.add_argument("--batch-rows", type=int, default=None,
+                    help="attn path: batches of whole bigram partitions of at most this many rows, "
+                         "one plan each, run in row order (default 0: every partition in one plan)")
     ap.add_argument("--cpu-rows", type=int, default=250_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -380,7 +383,7 @@ def main() -> int:
 
     import torch
     from agpt_amd import trie as trie_mod
-    from agpt_amd.attention import TrieAttention
+    from agpt_amd.attention import TrieAttention, partition_starts, range_batches
 
     if args.path == "c3":
         if args.scale is None:
@@ -402,10 +405,26 @@ def main() -> int:
     if args.path == "loss":
         return bench_loss(args, tr, args.vocab)
     dev = torch.device("cuda:0")
-    att = TrieAttention(H, hd, max_depth=max(tr.max_depth, 1), dtype=dtype)
-    att.plan(tr.parent)
-    info = att.plan_info()
-    log(f"plan: {info}; kernel: {att.describe()}")
+    # One plan per batch: the whole trie, or contiguous runs of whole bigram
+    # partitions of at most --batch-rows rows (each reads its context rows,
+    # the ancestors before it, as keys and adds their dK/dV share in place).
+    batch_rows = args.batch_rows if args.batch_rows is not None else 0
+    starts = partition_starts(tr.radix_head, tr.depth)
+    ranges = range_batches(T, batch_rows, starts) if batch_rows > 0 else [(0, T)]
+    parts = []
+    for a, b in ranges:
+        att = TrieAttention(H, hd, max_depth=max(tr.max_depth, 1), dtype=dtype)
+        if len(ranges) == 1:
+            att.plan(tr.parent)
+        else:
+            att.plan_range(tr.parent, a, b)
+        parts.append(att)
+    infos = [p.plan_info() for p in parts]
+    info = {"n_nodes": T, "n_tiles": sum(i["n_tiles"] for i in infos), "batches": len(parts)}
+    batching = (f"one batch: all {starts.shape[0]} bigram partitions in one plan" if len(parts) == 1 else
+                f"{len(parts)} batches of whole bigram partitions ({starts.shape[0]} partitions), "
+                f"<= {batch_rows} rows each")
+    log(f"plan: {info}; {batching}; kernel: {parts[0].describe()}")
     q, k, v, d_o = make_inputs(tr, D, H, hd, dtype, seed=1234, dev=dev)
     o = torch.empty(T, D, device=dev, dtype=dtype)
     lse = torch.empty(T, H, device=dev, dtype=torch.float32)
@@ -413,9 +432,11 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"inputs resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
 
-    def step(fev=None, bev=None):
-        att.forward(q, k, v, out=o, lse=lse, events=fev)
-        att.backward(q, k, v, o, lse, d_o, out=grads, events=bev)
+    def step(evs=None):
+        # per batch: forward, then backward (the per-subtree trainer's order)
+        for j, att in enumerate(parts):
+            att.forward(q, k, v, out=o, lse=lse, events=None if evs is None else evs[j][0])
+            att.backward(q, k, v, o, lse, d_o, out=grads, events=None if evs is None else evs[j][1])
 
     for i in range(args.warmup):
         step()
@@ -423,35 +444,39 @@ def main() -> int:
         log(f"warmup step {i + 1}/{args.warmup} done")
 
     hev = HipEvents()
-    evs = [(hev.create(2), hev.create(5)) for _ in range(args.steps)]
+    evs = [[(hev.create(2), hev.create(5)) for _ in parts] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(*evs[i])
+        step(evs[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
-    desc = att.describe()
+    desc = parts[0].describe()
     split = "split backward" in desc
     carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce
     names = (["trie_fwd", "trie_bwd_q", "trie_bwd_kv"] if split else ["trie_fwd", "trie_bwd"])
     tail = ["trie_bwd_carry"] if carry else ["trie_bwd_chunk", "trie_bwd_reduce"]
     k_ms = {n: [] for n in names + tail}
-    for fe, be in evs:
-        k_ms["trie_fwd"].append(hev.ms(fe[0], fe[1]))
-        if split:
-            k_ms["trie_bwd_q"].append(hev.ms(be[0], be[1]))
-            k_ms["trie_bwd_kv"].append(hev.ms(be[1], be[2]))
-        else:
-            k_ms["trie_bwd"].append(hev.ms(be[0], be[2]))
-        if carry:
-            k_ms["trie_bwd_carry"].append(hev.ms(be[3], be[4]))
-        else:
-            k_ms["trie_bwd_chunk"].append(hev.ms(be[2], be[3]))
-            k_ms["trie_bwd_reduce"].append(hev.ms(be[3], be[4]))
-        hev.destroy(fe + be)
+    for step_evs in evs:
+        acc = {n: 0.0 for n in k_ms}  # per step: summed over the batches
+        for fe, be in step_evs:
+            acc["trie_fwd"] += hev.ms(fe[0], fe[1])
+            if split:
+                acc["trie_bwd_q"] += hev.ms(be[0], be[1])
+                acc["trie_bwd_kv"] += hev.ms(be[1], be[2])
+            else:
+                acc["trie_bwd"] += hev.ms(be[0], be[2])
+            if carry:
+                acc["trie_bwd_carry"] += hev.ms(be[3], be[4])
+            else:
+                acc["trie_bwd_chunk"] += hev.ms(be[2], be[3])
+                acc["trie_bwd_reduce"] += hev.ms(be[3], be[4])
+            hev.destroy(fe + be)
+        for n, x in acc.items():
+            k_ms[n].append(x)
     avg = {n: float(np.mean(x)) for n, x in k_ms.items()}
-    log("kernel avg ms: " + ", ".join(f"{n} {m:.3f}" for n, m in avg.items()))
+    log("kernel avg ms per step: " + ", ".join(f"{n} {m:.3f}" for n, m in avg.items()))
 
     bpt = bytes_per_token(D, H, b_in)
     kern_bytes = {n: bpt[n] * T for n in names}
@@ -486,7 +511,8 @@ def main() -> int:
             "workload": f"{args.workload}: single-layer trie attention fwd+bwd",
             "node_tokens": T, "radix_nodes": tr.n_radix, "sum_depth": tr.sum_depth,
             "max_depth": tr.max_depth, "d_model": D, "heads": H, "head_dim": hd,
-            "corpus_scale": args.scale, "tiles": info["n_tiles"], "kernel": att.describe(),
+            "corpus_scale": args.scale, "tiles": info["n_tiles"], "batching": batching,
+            "kernel": desc,
         },
         "roofline": {
             "bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS,
@@ -508,7 +534,8 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    att.close()
+    for att in parts:
+        att.close()
     return 0
 
 
