@@ -601,6 +601,7 @@ __global__ __launch_bounds__(256) void trie_ctx_kernel(PlanDev pl, const float* 
 
 #include "trie_fast.h"
 #include "trie_block.h"
+#include "trie_deep.h"
 
 // ===========================================================================
 // Host side: handle, plan, launches.
@@ -653,6 +654,7 @@ struct agpt_attn_s {
   bool fused = false;           // block kernels: one-pass backward (fp32)
   int fhg = 1;                  // heads per workgroup of the one-pass backward
   bool carry = false;           // one-pass backward carries path sums (E, F replace Pk, Pv)
+  bool deep = false;            // block kernels at head_dim 64: streamed key set (trie_deep.h)
   float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
   float* d_F = nullptr;
   size_t fb_lds = 0;
@@ -943,7 +945,13 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     h->fb_lds = agpt_blk::fused_lds_bytes(h->max_depth, h->fhg, hd, false);
     const int bbudget = lim - static_cast<int>(sizeof(agpt_blk::BlockTables<4>));
     // head_dim 64 runs one head per workgroup (a 256-byte fp32 / 128-byte
-    // bf16 row segment already fills whole lines).
+    // bf16 row segment already fills whole lines), its key set streamed
+    // through a ring (trie_deep.h) instead of held whole in LDS.
+    h->deep = hd == 64 && hg == 1 && env_int("AGPT_ATTN_DEEP", 1) != 0;
+    if (h->deep) {
+      h->fwd_lds = h->bq_lds = agpt_deep::ring_lds_bytes(hd, elem);
+      h->kv_lds = agpt_deep::rows_lds_bytes(hd, elem);
+    }
     const bool ok = (hd == 16 || hd == 32 || (hd == 64 && hg == 1)) && H % hg == 0 &&
                     (hg == 1 || hg == 2 || hg == 4) &&
                     (hg * hd * elem) % 16 == 0 && h->fwd_lds <= static_cast<size_t>(bbudget) &&
@@ -961,7 +969,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     }
     if (ok) return;
     h->variant = 5;  // try the chain-group walk
-    h->fused = h->carry = false;
+    h->fused = h->carry = h->deep = false;
   }
   if (h->variant != 5) {
     const int t = env_int("AGPT_ATTN_TILE", 64);
@@ -1309,7 +1317,12 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (!h) return "null handle";
   if (!h->planned) return "no plan";
   char buf[400];
-  if (h->variant == 6)
+  if (h->variant == 6 && h->deep)
+    snprintf(buf, sizeof(buf),
+             "streamed key ring (deep prefixes) 16x16 mfma, split backward: tile_rows=%d tiles=%d "
+             "heads_per_wg=1 key_chunk=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
+             h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds, h->kv_lds, h->max_lds);
+  else if (h->variant == 6)
     snprintf(buf, sizeof(buf),
              "streaming block-sparse 16x16 mfma, %s backward: tile_rows=%d tiles=%d heads_per_wg=%d "
              "heads_per_unit=%d/%d fwd_lds=%zu bwd_lds=%zu/%zu lds_limit=%d",
@@ -1460,7 +1473,16 @@ template <int HD, typename Tin>
 void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, void* o,
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
-  if (h->variant == 6) {
+  if (h->variant == 6 && h->deep) {
+    if constexpr (HD == 64) {
+      clear_sched(h, st);
+      auto fn = agpt_deep::fwd_kernel<HD, Tin, PlanDev>;
+      set_lds(fn, h->fwd_lds);
+      hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds, 1)), dim3(agpt_deep::kThreads), h->fwd_lds, st,
+                         plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                         static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+    }
+  } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32 || HD == 64) {
       clear_sched(h, st);
       with_block_heads(h, h->fwd_uh, [&](auto hgc, auto uhc) {
@@ -1558,6 +1580,23 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
     }
   }
   if (fused_done) {
+  } else if (h->variant == 6 && h->deep) {
+    if constexpr (HD == 64) {
+      clear_sched(h, st);
+      auto fq = agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs>;
+      set_lds(fq, h->bq_lds);
+      hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds, 1)), dim3(agpt_deep::kThreads), h->bq_lds, st,
+                         plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                         static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
+                         static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
+      pm.mark(1);
+      auto fk = agpt_deep::bwd_kv_kernel<HD, Tin, PlanDev, RopeArgs>;
+      set_lds(fk, h->kv_lds);
+      hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds, 1)), dim3(agpt_deep::kThreads), h->kv_lds, st,
+                         plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                         static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv,
+                         h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+    }
   } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32 || HD == 64) {
       clear_sched(h, st);

@@ -1,0 +1,595 @@
+// trie_deep.h — head_dim 64 trie-attention kernels for deep prefixes
+// (included by trie_attn.hip after trie_block.h).
+//
+// The block kernels of trie_block.h keep a tile's whole key set (the
+// prefix path of its first row and its own rows) in LDS. At head_dim 64 a
+// deep trie's key set is up to 255 + 64 rows, 80-110 KB of K and V per
+// workgroup: one workgroup per CU, one wave per SIMD, and every block pair
+// waits on the latency of the one before it. Here the key set streams:
+//
+//   query side (forward; backward dQ): a workgroup takes one (tile, head);
+//     each of its four waves owns one 16-row query block, whose Q (and dO)
+//     slices sit in registers. The tile's keys (prefix rows in depth order,
+//     then the tile rows) pass through a double-buffered LDS ring in chunks
+//     of 64: while the waves work on one chunk, the next is loaded from
+//     memory by row index (the plan's prefix list) into registers and
+//     written to the other buffer at the chunk's end.
+//   key side (backward dK, dV): the tile's Q and dO rows are staged in LDS;
+//     each wave takes key blocks of 16 keys, loads their K and V slices
+//     straight into registers, and walks the query blocks that see them.
+//
+// LDS per workgroup is 37 KB (bf16 ring) or 18 KB (bf16 staged rows)
+// instead of 80-110 KB. The block pairs, masks and lane layouts are those of
+// trie_block.h: 16x16 tiles on the matrix instructions, and per key the
+// interval of tile rows that see it (in DFS preorder the rows below a key
+// are consecutive). The key side leaves the partials bwd_kv_kernel leaves
+// (a prefix key's share over the tile in Pk/Pv at row pref_off[t] +
+// depth - 1; an open tile row's share in dK/dV), which
+// trie_bwd_chunk_kernel and trie_bwd_reduce_kernel finish.
+//
+// Units (tile, head) are claimed from one counter per kernel, tile-major;
+// the claim for the next unit is sent at the start of the current one. No
+// result depends on which workgroup takes a unit.
+#pragma once
+
+namespace agpt_deep {
+
+using namespace agpt;
+using agpt_blk::group_max;
+using agpt_blk::group_sum;
+using agpt_blk::in_interval;
+using agpt_blk::kBlk;
+using agpt_blk::kRescaleLog2;
+using agpt_blk::ld1;
+using agpt_blk::mfma16;
+using agpt_blk::mfma_rows_bf16;
+using agpt_blk::pack_bf16;
+using agpt_blk::Slice;
+using agpt_blk::slice_dot;
+using agpt_fast::f4;
+using agpt_fast::u4;
+using agpt_fast::uniform;
+
+constexpr int kTile = 64;
+constexpr int kThreads = 256;
+constexpr int kChunk = 64;  // keys per streamed chunk: one 16-key block per wave-sized step
+constexpr int kKeyCap = (kMaxDepth - 1 + kTile + kChunk - 1) / kChunk * kChunk;
+// Running max of a query before it has seen a key: finite, so that exp2 of
+// a masked score (-inf) minus it is 0, never NaN.
+constexpr float kNoMax = -1.0e30f;
+
+__host__ __device__ constexpr int row_stride(int hd, int elem) { return hd + 16 / elem; }
+// Dynamic LDS: the query-side ring [2 buffers][K, V][kChunk][WS] or the
+// key side's staged rows [Q, dO][kTile][WS].
+__host__ __device__ constexpr size_t ring_lds_bytes(int hd, int elem) {
+  return static_cast<size_t>(2 * 2 * kChunk) * row_stride(hd, elem) * elem;
+}
+__host__ __device__ constexpr size_t rows_lds_bytes(int hd, int elem) {
+  return static_cast<size_t>(2 * kTile) * row_stride(hd, elem) * elem;
+}
+
+// The tile's key list and row tables. Keys 0 .. A-1 are the prefix rows
+// (depth 1 .. A), keys A .. A+ntile-1 the tile rows; the list is padded to
+// whole chunks with empty keys that name row s (finite data, never live).
+struct alignas(16) Tables {
+  alignas(16) int32_t kint[kKeyCap];  // per key: lo | len << 16, the tile rows [lo, lo + len) that see it
+  int32_t krow[kKeyCap];  // per key: its row in the tensors (negative: a context row of a range plan)
+  int32_t blo[kKeyCap / kBlk];  // per key block: least lo of its live keys (kTile if none)
+  int32_t bhi[kKeyCap / kBlk];  // per key block: greatest lo + len
+  int32_t rdep[kTile];   // depth of the tile rows
+  int32_t rend[kTile];   // subtree end of the tile rows
+  alignas(16) float l2[kTile];  // lse * log2(e) of the tile rows (key side)
+  alignas(16) float dl[kTile];  // δ of the tile rows (key side)
+  int32_t next[2];       // claims, alternating by unit
+};
+
+// Unit u = (tile u / H, head u % H); fills the tables of its tile.
+struct Unit {
+  int t, h, s, ntile, A, poff, nk, nch;
+};
+
+template <typename PlanT>
+__device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int u, int H, bool row_tabs) {
+  Unit w;
+  w.t = u / H;
+  w.h = u - w.t * H;
+  w.s = w.t * kTile;
+  w.ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - w.s));
+  w.poff = pl.pref_off[w.t];
+  w.A = pl.pref_off[w.t + 1] - w.poff;
+  w.nk = w.A + w.ntile;
+  w.nch = (w.nk + kChunk - 1) / kChunk;
+  const int tid = threadIdx.x;
+  for (int j = tid; j < w.nch * kChunk; j += kThreads) {
+    int iv = 0, row = w.s;
+    if (j < w.A) {
+      row = pl.prefix[w.poff + j];
+      iv = min(pl.pref_end[w.poff + j] - w.s, w.ntile) << 16;
+    } else if (j < w.nk) {
+      const int r = j - w.A;
+      row = w.s + r;
+      const int e = pl.end[row];
+      iv = r | ((min(e - w.s, w.ntile) - r) << 16);
+      if (row_tabs) {
+        tb.rdep[r] = pl.depth[row];
+        tb.rend[r] = e;
+      }
+    }
+    tb.kint[j] = iv;
+    tb.krow[j] = row;
+  }
+  __syncthreads();
+  for (int b = tid; b < w.nch * (kChunk / kBlk); b += kThreads) {
+    int lo = kTile, hi = 0;
+    for (int x = 0; x < kBlk; ++x) {
+      const int iv = tb.kint[b * kBlk + x];
+      const int len = iv >> 16;
+      if (len > 0) {
+        lo = min(lo, iv & 0xffff);
+        hi = max(hi, (iv & 0xffff) + len);
+      }
+    }
+    tb.blo[b] = lo;
+    tb.bhi[b] = hi;
+  }
+  __syncthreads();
+  return w;
+}
+
+// Whether query block i (rows 16i .. 16i+15) has a live pair with key block b.
+__device__ __forceinline__ bool block_live(const Tables& tb, int b, int i) {
+  return kBlk * i < uniform(tb.bhi[b]) && kBlk * i + kBlk > uniform(tb.blo[b]);
+}
+
+// The double-buffered key ring of the query side: chunk c of the tile's key
+// list, K and V slices of one head, [buffer][K, V][kChunk][WS].
+template <int HD, typename Tin>
+struct KeyRing {
+  static constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));  // elements per 16-byte piece
+  static constexpr int WS = row_stride(HD, sizeof(Tin));
+  static constexpr int PIECES = HD / EPC;    // pieces per key slice
+  static constexpr int PER_T = kChunk * PIECES;  // pieces per tensor per chunk
+  static constexpr int PER = 2 * PER_T / kThreads;
+  static_assert(PER_T % kThreads == 0, "whole rounds of the workgroup per tensor");
+  Tin* base;
+  u4 r[PER];
+  __device__ __forceinline__ Tin* ks(int buf) const { return base + (2 * buf) * kChunk * WS; }
+  __device__ __forceinline__ Tin* vs(int buf) const { return base + (2 * buf + 1) * kChunk * WS; }
+  __device__ __forceinline__ void load(const Tables& tb, const Tin* K, const Tin* V, int D, int h, int c) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int ten = k * kThreads / PER_T;  // a constant once unrolled
+      const int j = static_cast<int>(threadIdx.x) + k * kThreads - ten * PER_T;
+      const int key = j / PIECES;
+      const int64_t row = tb.krow[c * kChunk + key];
+      r[k] = *reinterpret_cast<const u4*>((ten ? V : K) + row * D + h * HD + (j % PIECES) * EPC);
+    }
+  }
+  __device__ __forceinline__ void store(int buf) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int ten = k * kThreads / PER_T;
+      const int j = static_cast<int>(threadIdx.x) + k * kThreads - ten * PER_T;
+      *reinterpret_cast<u4*>((ten ? vs(buf) : ks(buf)) + (j / PIECES) * WS + (j % PIECES) * EPC) = r[k];
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Forward: O and lse. S^T = K Q^T puts query c in lane column c (keys
+// 4g .. 4g+3 in its registers); online softmax with the lazy rescale of
+// trie_block.h; O^T += V^T P^T.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, typename PlanT>
+__global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __restrict__ Q,
+                                                       const Tin* __restrict__ K, const Tin* __restrict__ V,
+                                                       Tin* __restrict__ O, float* __restrict__ lse, int H,
+                                                       float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  using Ring = KeyRing<HD, Tin>;
+  constexpr int WS = Ring::WS;
+  __shared__ Tables tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  Ring ring;
+  ring.base = reinterpret_cast<Tin*>(dyn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
+  int* ctr = pl.sched + 0;
+  if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(tb.next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
+    const Unit w = build_tables(pl, tb, u, H, false);
+    const int q = kBlk * wave + c;  // this lane's query row in the tile
+    const int64_t qrow = w.s + min(q, w.ntile - 1);
+    Slice<Tin, KD> qf;
+    qf.load(Q + qrow * D + w.h * HD + KD * g);
+    qf.scale(qscale);
+    float m = kNoMax, l = 0.0f;
+    f4 o[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    ring.load(tb, K, V, D, w.h, 0);
+    ring.store(0);
+    __syncthreads();
+    for (int ch = 0; ch < w.nch; ++ch) {
+      const bool more = ch + 1 < w.nch;
+      if (more) ring.load(tb, K, V, D, w.h, ch + 1);
+      const Tin* Ks = ring.ks(ch & 1);
+      const Tin* Vs = ring.vs(ch & 1);
+#pragma unroll
+      for (int bl = 0; bl < kChunk / kBlk; ++bl) {
+        const int b = ch * (kChunk / kBlk) + bl;
+        if (!block_live(tb, b, wave)) continue;
+        const int4 iv = *reinterpret_cast<const int4*>(tb.kint + kBlk * b + 4 * g);
+        const bool live[4] = {in_interval(q, iv.x), in_interval(q, iv.y), in_interval(q, iv.z),
+                              in_interval(q, iv.w)};
+        Slice<Tin, KD> kf;
+        kf.load(Ks + (kBlk * bl + c) * WS + KD * g);
+        f4 sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16b+4g+r against query q
+        if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = live[r] ? sv[r] : -__builtin_inff();
+        const float lmx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        if (__any(lmx > m + kRescaleLog2)) {
+          const float mx = group_max(lmx);
+          const bool resc = mx > m + kRescaleLog2;
+          const float a = resc ? fast_exp2(m - mx) : 1.0f;
+          m = resc ? mx : m;
+          l *= a;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) o[j] *= a;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = fast_exp2(sc[r] - m);  // masked: exp2(-inf) = 0
+          l += p[r];
+        }
+        if constexpr (sizeof(Tin) == 2) {
+          const uint2 pw = pack_bf16(p);
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+            o[j] = mfma_rows_bf16(Vs + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, pw, o[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              o[j] = mfma16(ld1(Vs + (kBlk * bl + 4 * g + r) * WS + kBlk * j + c), p[r], o[j]);
+        }
+      }
+      if (more) ring.store((ch + 1) & 1);
+      __syncthreads();
+    }
+    if (q < w.ntile) {
+      const int64_t row = static_cast<int64_t>(w.s) + q;
+      const float le = group_sum(l);
+      const float inv = __builtin_amdgcn_rcpf(le);
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
+        store_vec<4>(O + row * D + w.h * HD + kBlk * j + 4 * g, v);
+      }
+      if (g == 0) lse[row * H + w.h] = (m + fast_log2(le)) * kLn2;
+    }
+    u = uniform(tb.next[par]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, query side: δ and dQ. fp32 inputs: δ = dO·O from the fetched O
+// rows. bf16 inputs: O is a rounded output, so δ = Σ_j w_j dO·v_j is
+// recomputed over the path in fp32 (batched_depth_backward.cr:637-646), one
+// pass over the key chunks before the dQ pass. δ goes to Dl [T, H] for the
+// key side; dQ gets the inverse rotation at the query's depth.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_q_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
+    float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
+  using Ring = KeyRing<HD, Tin>;
+  constexpr int WS = Ring::WS;
+  __shared__ Tables tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  Ring ring;
+  ring.base = reinterpret_cast<Tin*>(dyn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
+  int* ctr = pl.sched + 1;
+  if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(tb.next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
+    const Unit w = build_tables(pl, tb, u, H, false);
+    const int q = kBlk * wave + c;
+    const int64_t qrow = w.s + min(q, w.ntile - 1);
+    const int64_t qoff = qrow * D + w.h * HD + KD * g;
+    Slice<Tin, KD> qf, gf;
+    qf.load(Q + qoff);
+    gf.load(dO + qoff);
+    qf.scale(qscale);
+    const float l2 = lse[qrow * H + w.h] * kLog2e;
+    // Scores and dO·v of key block bl of the buffer: register r holds key
+    // 16b+4g+r against query q.
+    auto scores = [&](const Tin* Ks, const Tin* Vs, int bl, f4& sv, f4& tv) {
+      Slice<Tin, KD> kf, vf;
+      kf.load(Ks + (kBlk * bl + c) * WS + KD * g);
+      vf.load(Vs + (kBlk * bl + c) * WS + KD * g);
+      sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+      tv = slice_dot(vf, gf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+      if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
+    };
+    auto mask = [&](int b, bool (&live)[4]) {
+      const int4 iv = *reinterpret_cast<const int4*>(tb.kint + kBlk * b + 4 * g);
+      live[0] = in_interval(q, iv.x);
+      live[1] = in_interval(q, iv.y);
+      live[2] = in_interval(q, iv.z);
+      live[3] = in_interval(q, iv.w);
+    };
+    float dl;
+    if constexpr (kDeltaFromO) {
+      float ov[KD], gv[KD];
+      load_vec<KD>(O + qoff, ov);
+      load_vec<KD>(dO + qoff, gv);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KD; ++j) acc += gv[j] * ov[j];
+      dl = group_sum(acc);
+    }
+    // bf16: pass 0 sums δ over the key chunks, pass 1 forms dQ.
+    constexpr int kPass0 = kDeltaFromO ? 1 : 0;
+    f4 dq[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int pass = kPass0; pass < 2; ++pass) {
+      float acc = 0.0f;
+      ring.load(tb, K, V, D, w.h, 0);
+      ring.store(0);
+      __syncthreads();
+      for (int ch = 0; ch < w.nch; ++ch) {
+        const bool more = ch + 1 < w.nch;
+        if (more) ring.load(tb, K, V, D, w.h, ch + 1);
+        const Tin* Ks = ring.ks(ch & 1);
+        const Tin* Vs = ring.vs(ch & 1);
+#pragma unroll
+        for (int bl = 0; bl < kChunk / kBlk; ++bl) {
+          const int b = ch * (kChunk / kBlk) + bl;
+          if (!block_live(tb, b, wave)) continue;
+          bool live[4];
+          mask(b, live);
+          f4 sv, tv;
+          scores(Ks, Vs, bl, sv, tv);
+          if (pass == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc += live[r] ? fast_exp2(sv[r] - l2) * tv[r] : 0.0f;
+            continue;
+          }
+          float ds[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ds[r] = live[r] ? fast_exp2(sv[r] - l2) * (tv[r] - dl) * scale : 0.0f;
+          if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per output tile
+            const uint2 dw = pack_bf16(ds);
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+              dq[j] = mfma_rows_bf16(Ks + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, dw, dq[j]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                dq[j] = mfma16(ld1(Ks + (kBlk * bl + 4 * g + r) * WS + kBlk * j + c), ds[r], dq[j]);
+          }
+        }
+        if (more) ring.store((ch + 1) & 1);
+        __syncthreads();
+      }
+      if (pass == 0) dl = group_sum(acc);
+    }
+    if (q < w.ntile) {
+      const int64_t row = static_cast<int64_t>(w.s) + q;
+      const int pos = rope.cos_t ? rope_pos(pl.depth[row], rope.seq_len) : 0;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        float v[4] = {dq[j][0], dq[j][1], dq[j][2], dq[j][3]};
+        if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
+        store_vec<4>(dQ + row * D + w.h * HD + kBlk * j + 4 * g, v);
+      }
+      if (g == 0) Dl[row * H + w.h] = dl;
+    }
+    u = uniform(tb.next[par]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, key side: dK, dV of the tile's key list. S = Q_i K^T puts key c
+// in lane column c (queries 4g .. 4g+3 in its registers); dV^T += dO^T P,
+// dK^T += Q^T dS. Key blocks are dealt to the waves in turn; a wave loads
+// the next block's K and V slices while it works on the current one.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
+    float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ Pk, float* __restrict__ Pv,
+    const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));
+  constexpr int WS = row_stride(HD, sizeof(Tin));
+  constexpr int PIECES = HD / EPC;
+  constexpr int ROWJ = kTile * PIECES;  // 16-byte pieces of one staged tensor
+  static_assert(ROWJ % kThreads == 0, "whole rounds of the workgroup per staged tensor");
+  __shared__ Tables tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  Tin* Qs = reinterpret_cast<Tin*>(dyn);
+  Tin* Gs = Qs + kTile * WS;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
+  int* ctr = pl.sched + 2;
+  if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(tb.next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
+    // The tile's Q and dO rows (rows past a short tile repeat its last row).
+    {
+      const int t = u / H, h = u - t * H;
+      const int64_t s = static_cast<int64_t>(t) * kTile;
+      const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s)) - 1;
+      u4 rq[ROWJ / kThreads], rg[ROWJ / kThreads];
+#pragma unroll
+      for (int k = 0; k < ROWJ / kThreads; ++k) {
+        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        const int64_t off = (s + min(j / PIECES, last)) * D + h * HD + (j % PIECES) * EPC;
+        rq[k] = *reinterpret_cast<const u4*>(Q + off);
+        rg[k] = *reinterpret_cast<const u4*>(dO + off);
+      }
+      const Unit w = build_tables(pl, tb, u, H, true);
+      if (threadIdx.x < kTile) {
+        const int r = min(static_cast<int>(threadIdx.x), w.ntile - 1);
+        tb.l2[threadIdx.x] = lse[(s + r) * H + h] * kLog2e;
+        tb.dl[threadIdx.x] = Dl[(s + r) * H + h];
+      }
+#pragma unroll
+      for (int k = 0; k < ROWJ / kThreads; ++k) {
+        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
+        *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
+      }
+      __syncthreads();
+    }
+    const int t = u / H, h = u - t * H;
+    const int s = t * kTile;
+    const int ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s));
+    const int poff = pl.pref_off[t];
+    const int A = pl.pref_off[t + 1] - poff;
+    const int nkb = (A + ntile + kBlk - 1) / kBlk;
+    // K and V slices of key block b (keys past the list name row s).
+    Slice<Tin, KD> kf, vf, nkf, nvf;
+    auto fetch = [&](int b, Slice<Tin, KD>& a, Slice<Tin, KD>& v) {
+      const int64_t row = tb.krow[kBlk * b + c];
+      a.load(K + row * D + h * HD + KD * g);
+      v.load(V + row * D + h * HD + KD * g);
+    };
+    if (wave < nkb) fetch(wave, nkf, nvf);
+    for (int b = wave; b < nkb; b += 4) {
+      kf = nkf;
+      vf = nvf;
+      if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
+      kf.scale(qscale);
+      f4 dk[MT], dv[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        dv[j] = dk[j];
+      }
+      const int key = kBlk * b + c;
+      const int iv = tb.kint[key];
+      const int i0 = uniform(tb.blo[b]) / kBlk;
+      const int i1 = (uniform(tb.bhi[b]) + kBlk - 1) / kBlk;
+      for (int i = i0; i < i1; ++i) {
+        const int qr = kBlk * i + c;  // query row this lane supplies
+        const int q0 = kBlk * i + 4 * g;
+        bool live[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) live[r] = in_interval(q0 + r, iv);
+        Slice<Tin, KD> qa, ga;
+        qa.load(Qs + qr * WS + KD * g);
+        ga.load(Gs + qr * WS + KD * g);
+        f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // sv[r]: query q0+r against key `key`
+        const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+        if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
+        const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
+        const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
+          ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+        }
+        if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
+          const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const int col = q0 * WS + kBlk * j + c;
+            dv[j] = mfma_rows_bf16(Gs + col, WS, pw, dv[j]);
+            dk[j] = mfma_rows_bf16(Qs + col, WS, dw, dk[j]);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = (q0 + r) * WS + kBlk * j + c;
+              dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
+              dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+            }
+        }
+      }
+      // Emit dims 16j+4g.. of the key.
+      if (key < A) {
+        const int64_t prow = static_cast<int64_t>(poff) + key;  // prefix entry `key` = depth key+1
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+          float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+          store_vec<4>(Pk + prow * D + h * HD + kBlk * j + 4 * g, a);
+          store_vec<4>(Pv + prow * D + h * HD + kBlk * j + 4 * g, v);
+        }
+      } else if (key < A + ntile) {
+        const int r = key - A;
+        const int64_t a = static_cast<int64_t>(s) + r;
+        const bool done = tb.rend[r] <= s + ntile;
+        const int pos = rope.cos_t ? rope_pos(tb.rdep[r], rope.seq_len) : 0;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          const int d0 = kBlk * j + 4 * g;
+          float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+          float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+          if (done) {
+            if (acc_dk) {
+              float y[4];
+              load_vec<4>(acc_dk + a * D + h * HD + d0, y);
+#pragma unroll
+              for (int x = 0; x < 4; ++x) gk[x] += y[x];
+            }
+            if (acc_dv) {
+              float y[4];
+              load_vec<4>(acc_dv + a * D + h * HD + d0, y);
+#pragma unroll
+              for (int x = 0; x < 4; ++x) gv[x] += y[x];
+            }
+            if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
+          }
+          store_vec<4>(dK + a * D + h * HD + d0, gk);
+          store_vec<4>(dV + a * D + h * HD + d0, gv);
+        }
+      }
+    }
+    __syncthreads();  // the staged rows and tables are free for the next unit
+    u = uniform(tb.next[par]);
+  }
+}
+
+}  // namespace agpt_deep

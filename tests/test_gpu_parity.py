@@ -27,6 +27,7 @@ VARIANTS = {
     "block_hg4_all_heads_chunk1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_HG": "4", "AGPT_ATTN_UH": "4",
                                    "AGPT_ATTN_FUH": "4", "AGPT_ATTN_CHUNK": "1"},
     "block_fwd_one_head_units": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUH": "1"},
+    "block_whole_key_set": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_DEEP": "0"},
     "chain": {"AGPT_ATTN_VARIANT": "5"},
     "chain_hg1_qb1_kb1": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "1", "AGPT_ATTN_QB": "1",
                           "AGPT_ATTN_KB": "1"},
@@ -42,7 +43,7 @@ def variant(request, monkeypatch):
     for k in ("AGPT_ATTN_VARIANT", "AGPT_ATTN_HG", "AGPT_ATTN_TILE", "AGPT_ATTN_NW",
               "AGPT_ATTN_QB", "AGPT_ATTN_KB", "AGPT_ATTN_SPLIT", "AGPT_ATTN_QSLOTS",
               "AGPT_ATTN_KSLOTS", "AGPT_ATTN_UH", "AGPT_ATTN_CHUNK", "AGPT_ATTN_FUSED",
-              "AGPT_ATTN_FHG", "AGPT_ATTN_CARRY", "AGPT_ATTN_FUH"):
+              "AGPT_ATTN_FHG", "AGPT_ATTN_CARRY", "AGPT_ATTN_FUH", "AGPT_ATTN_DEEP"):
         monkeypatch.delenv(k, raising=False)
     for k, v in VARIANTS[request.param].items():
         monkeypatch.setenv(k, v)
