@@ -1418,6 +1418,19 @@ int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds, int hg = 0) {
   return static_cast<int>(g);
 }
 
+// Heads per unit of the deep-prefix kernels: all heads of a tile when the
+// plan has tiles enough for ~16 units per CU (tables built once per tile,
+// heads streamed back to back), else one (units enough to fill the chip).
+// AGPT_ATTN_DHPU overrides (a divisor of the head count).
+int deep_heads_per_unit(const agpt_attn_s* h) {
+  const int H = h->cfg.n_heads;
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
+  int hpu = env_int("AGPT_ATTN_DHPU", h->n_tiles >= 16 * cus ? H : 1);
+  if (hpu < 1 || hpu > H || H % hpu != 0) hpu = 1;
+  return hpu;
+}
+
 // Clears the block kernels' chunk counters on the stream with a kernel, not
 // a memset node: the launch sequence stays valid under stream capture
 // (memset nodes in captured graphs have given wrong results on replays).
@@ -1476,11 +1489,12 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if (h->variant == 6 && h->deep) {
     if constexpr (HD == 64) {
       clear_sched(h, st);
+      const int hpu = deep_heads_per_unit(h);
       auto fn = agpt_deep::fwd_kernel<HD, Tin, PlanDev>;
       set_lds(fn, h->fwd_lds);
-      hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds, 1)), dim3(agpt_deep::kThreads), h->fwd_lds, st,
+      hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds, hpu)), dim3(agpt_deep::kThreads), h->fwd_lds, st,
                          plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
-                         static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+                         static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, hpu, scale);
     }
   } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32 || HD == 64) {
@@ -1583,19 +1597,20 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   } else if (h->variant == 6 && h->deep) {
     if constexpr (HD == 64) {
       clear_sched(h, st);
+      const int hpu = deep_heads_per_unit(h);
       auto fq = agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs>;
       set_lds(fq, h->bq_lds);
-      hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds, 1)), dim3(agpt_deep::kThreads), h->bq_lds, st,
+      hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds, hpu)), dim3(agpt_deep::kThreads), h->bq_lds, st,
                          plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
                          static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
-                         static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, scale);
+                         static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, hpu, scale);
       pm.mark(1);
       auto fk = agpt_deep::bwd_kv_kernel<HD, Tin, PlanDev, RopeArgs>;
       set_lds(fk, h->kv_lds);
-      hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds, 1)), dim3(agpt_deep::kThreads), h->kv_lds, st,
+      hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds, hpu)), dim3(agpt_deep::kThreads), h->kv_lds, st,
                          plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
                          static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv,
-                         h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, scale);
+                         h->d_Pk, h->d_Pv, acc_dk, acc_dv, rope, h->cfg.n_heads, hpu, scale);
     }
   } else if (h->variant == 6) {
     if constexpr (HD == 16 || HD == 32 || HD == 64) {

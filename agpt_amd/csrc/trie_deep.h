@@ -27,9 +27,13 @@
 // depth - 1; an open tile row's share in dK/dV), which
 // trie_bwd_chunk_kernel and trie_bwd_reduce_kernel finish.
 //
-// Units (tile, head) are claimed from one counter per kernel, tile-major;
-// the claim for the next unit is sent at the start of the current one. No
-// result depends on which workgroup takes a unit.
+// A workgroup takes a unit of one tile and hpu of its heads (all of them
+// when the plan has tiles enough to fill the chip, else one) and runs the
+// heads one after the other: the tables are built once per unit, and the
+// next head's operands are in flight while the current head is worked on.
+// Units are claimed from one counter per kernel; the claim for the next
+// unit is sent at the start of the current one. No result depends on which
+// workgroup takes a unit.
 #pragma once
 
 namespace agpt_deep {
@@ -83,16 +87,15 @@ struct alignas(16) Tables {
   int32_t next[2];       // claims, alternating by unit
 };
 
-// Unit u = (tile u / H, head u % H); fills the tables of its tile.
+// The tile of unit t; fills its key list and tables.
 struct Unit {
-  int t, h, s, ntile, A, poff, nk, nch;
+  int t, s, ntile, A, poff, nk, nch;
 };
 
 template <typename PlanT>
-__device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int u, int H, bool row_tabs) {
+__device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t, bool row_tabs) {
   Unit w;
-  w.t = u / H;
-  w.h = u - w.t * H;
+  w.t = t;
   w.s = w.t * kTile;
   w.ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - w.s));
   w.poff = pl.pref_off[w.t];
@@ -176,15 +179,19 @@ struct KeyRing {
 };
 
 // ---------------------------------------------------------------------------
-// Forward: O and lse. S^T = K Q^T puts query c in lane column c (keys
-// 4g .. 4g+3 in its registers); online softmax with the lazy rescale of
-// trie_block.h; O^T += V^T P^T.
+// Forward: O and lse. A workgroup takes a tile and runs its heads one after
+// the other as one stream of key chunks (the key list is the same for every
+// head): the chunk after the current one, in the next head or not, is in
+// flight while the current one is worked on, and the next head's Q slices
+// are fetched during the current head's last chunk. S^T = K Q^T puts query
+// c in lane column c (keys 4g .. 4g+3 in its registers); online softmax
+// with the lazy rescale of trie_block.h; O^T += V^T P^T.
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __restrict__ Q,
                                                        const Tin* __restrict__ K, const Tin* __restrict__ V,
                                                        Tin* __restrict__ O, float* __restrict__ lse, int H,
-                                                       float scale) {
+                                                       int hpu, float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
   using Ring = KeyRing<HD, Tin>;
@@ -198,31 +205,46 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
-  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
   int* ctr = pl.sched + 0;
   if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
   __syncthreads();
   int u = uniform(tb.next[1]);
+  const int ngr = H / hpu;  // head groups: unit u = (tile u / ngr, heads hpu * (u % ngr) ..)
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * ngr;
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
-    const Unit w = build_tables(pl, tb, u, H, false);
+    const int h0 = (u % ngr) * hpu;
+    const Unit w = build_tables(pl, tb, u / ngr, false);
     const int q = kBlk * wave + c;  // this lane's query row in the tile
-    const int64_t qrow = w.s + min(q, w.ntile - 1);
-    Slice<Tin, KD> qf;
-    qf.load(Q + qrow * D + w.h * HD + KD * g);
-    qf.scale(qscale);
-    float m = kNoMax, l = 0.0f;
-    f4 o[MT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    ring.load(tb, K, V, D, w.h, 0);
+    const int64_t qbase = (w.s + min(q, w.ntile - 1)) * static_cast<int64_t>(D) + KD * g;
+    Slice<Tin, KD> qf, qn;
+    qf.load(Q + qbase + h0 * HD);
+    ring.load(tb, K, V, D, h0, 0);
     ring.store(0);
     __syncthreads();
-    for (int ch = 0; ch < w.nch; ++ch) {
-      const bool more = ch + 1 < w.nch;
-      if (more) ring.load(tb, K, V, D, w.h, ch + 1);
-      const Tin* Ks = ring.ks(ch & 1);
-      const Tin* Vs = ring.vs(ch & 1);
+    float m = kNoMax, l = 0.0f;
+    f4 o[MT];
+    const int nsteps = hpu * w.nch;
+    for (int st = 0; st < nsteps; ++st) {
+      const int hl = st / w.nch;
+      const int h = h0 + hl;
+      const int ch = st - hl * w.nch;
+      if (ch == 0) {
+        qf.scale(qscale);
+        m = kNoMax;
+        l = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      const bool more = st + 1 < nsteps;
+      if (more) {
+        const int h2 = (st + 1) / w.nch;
+        ring.load(tb, K, V, D, h0 + h2, st + 1 - h2 * w.nch);
+      }
+      const bool last = ch + 1 == w.nch;
+      if (last && hl + 1 < hpu) qn.load(Q + qbase + (h + 1) * HD);
+      const Tin* Ks = ring.ks(st & 1);
+      const Tin* Vs = ring.vs(st & 1);
 #pragma unroll
       for (int bl = 0; bl < kChunk / kBlk; ++bl) {
         const int b = ch * (kChunk / kBlk) + bl;
@@ -266,39 +288,44 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
               o[j] = mfma16(ld1(Vs + (kBlk * bl + 4 * g + r) * WS + kBlk * j + c), p[r], o[j]);
         }
       }
-      if (more) ring.store((ch + 1) & 1);
-      __syncthreads();
-    }
-    if (q < w.ntile) {
-      const int64_t row = static_cast<int64_t>(w.s) + q;
-      const float le = group_sum(l);
-      const float inv = __builtin_amdgcn_rcpf(le);
+      if (more) ring.store((st + 1) & 1);
+      if (last) {
+        if (q < w.ntile) {
+          const int64_t row = static_cast<int64_t>(w.s) + q;
+          const float le = group_sum(l);
+          const float inv = __builtin_amdgcn_rcpf(le);
 #pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
-        store_vec<4>(O + row * D + w.h * HD + kBlk * j + 4 * g, v);
+          for (int j = 0; j < MT; ++j) {
+            float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
+            store_vec<4>(O + row * D + h * HD + kBlk * j + 4 * g, v);
+          }
+          if (g == 0) lse[row * H + h] = (m + fast_log2(le)) * kLn2;
+        }
+        qf = qn;
       }
-      if (g == 0) lse[row * H + w.h] = (m + fast_log2(le)) * kLn2;
+      __syncthreads();
     }
     u = uniform(tb.next[par]);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward, query side: δ and dQ. fp32 inputs: δ = dO·O from the fetched O
-// rows. bf16 inputs: O is a rounded output, so δ = Σ_j w_j dO·v_j is
-// recomputed over the path in fp32 (batched_depth_backward.cr:637-646), one
-// pass over the key chunks before the dQ pass. δ goes to Dl [T, H] for the
-// key side; dQ gets the inverse rotation at the query's depth.
+// Backward, query side: δ and dQ, a tile's heads as one stream of key chunks
+// as in the forward. fp32 inputs: δ = dO·O from the O rows. bf16 inputs: O
+// is a rounded output, so δ = Σ_j w_j dO·v_j is recomputed over the path in
+// fp32 (batched_depth_backward.cr:637-646): each head makes one pass over
+// the key chunks for δ, then one for dQ. δ goes to Dl [T, H] for the key
+// side; dQ gets the inverse rotation at the query's depth.
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT, typename RopeT>
 __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
-    float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, float scale) {
+    float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, int hpu, float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
   constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
+  constexpr int NP = kDeltaFromO ? 1 : 2;  // passes over the key chunks per head
   using Ring = KeyRing<HD, Tin>;
   constexpr int WS = Ring::WS;
   __shared__ Tables tb;
@@ -310,22 +337,34 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
-  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
   int* ctr = pl.sched + 1;
   if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
   __syncthreads();
   int u = uniform(tb.next[1]);
+  const int ngr = H / hpu;  // head groups: unit u = (tile u / ngr, heads hpu * (u % ngr) ..)
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * ngr;
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
-    const Unit w = build_tables(pl, tb, u, H, false);
+    const int h0 = (u % ngr) * hpu;
+    const Unit w = build_tables(pl, tb, u / ngr, false);
     const int q = kBlk * wave + c;
     const int64_t qrow = w.s + min(q, w.ntile - 1);
-    const int64_t qoff = qrow * D + w.h * HD + KD * g;
-    Slice<Tin, KD> qf, gf;
-    qf.load(Q + qoff);
-    gf.load(dO + qoff);
-    qf.scale(qscale);
-    const float l2 = lse[qrow * H + w.h] * kLog2e;
+    const int64_t qbase = qrow * D + KD * g;
+    // This lane's query of head h: Q, dO slices, lse (and O for δ, fp32).
+    Slice<Tin, KD> qf, gf, qn, gn;
+    float l2, l2n = 0.0f, dl = 0.0f;
+    float ov[kDeltaFromO ? KD : 1], on[kDeltaFromO ? KD : 1];
+    auto fetch = [&](int h, Slice<Tin, KD>& a, Slice<Tin, KD>& b, float& le, float (&oo)[kDeltaFromO ? KD : 1]) {
+      a.load(Q + qbase + h * HD);
+      b.load(dO + qbase + h * HD);
+      le = lse[qrow * H + h] * kLog2e;
+      if constexpr (kDeltaFromO) load_vec<KD>(reinterpret_cast<const float*>(O) + qbase + h * HD, oo);
+    };
+    fetch(h0, qf, gf, l2, ov);
+    const int qdep = pl.depth[qrow];
+    ring.load(tb, K, V, D, h0, 0);
+    ring.store(0);
+    __syncthreads();
     // Scores and dO·v of key block bl of the buffer: register r holds key
     // 16b+4g+r against query q.
     auto scores = [&](const Tin* Ks, const Tin* Vs, int bl, f4& sv, f4& tv) {
@@ -343,98 +382,117 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       live[2] = in_interval(q, iv.z);
       live[3] = in_interval(q, iv.w);
     };
-    float dl;
-    if constexpr (kDeltaFromO) {
-      float ov[KD], gv[KD];
-      load_vec<KD>(O + qoff, ov);
-      load_vec<KD>(dO + qoff, gv);
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < KD; ++j) acc += gv[j] * ov[j];
-      dl = group_sum(acc);
-    }
-    // bf16: pass 0 sums δ over the key chunks, pass 1 forms dQ.
-    constexpr int kPass0 = kDeltaFromO ? 1 : 0;
     f4 dq[MT];
+    float acc = 0.0f;
+    const int per = NP * w.nch;  // steps per head
+    const int nsteps = hpu * per;
+    for (int st = 0; st < nsteps; ++st) {
+      const int hl = st / per;
+      const int h = h0 + hl;
+      const int r0 = st - hl * per;
+      const int pass = NP == 2 ? r0 / w.nch : 1;  // 0: δ (bf16 only), 1: dQ
+      const int ch = r0 % w.nch;
+      if (r0 == 0) {
+        qf.scale(qscale);
+        acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MT; ++j) dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int pass = kPass0; pass < 2; ++pass) {
-      float acc = 0.0f;
-      ring.load(tb, K, V, D, w.h, 0);
-      ring.store(0);
-      __syncthreads();
-      for (int ch = 0; ch < w.nch; ++ch) {
-        const bool more = ch + 1 < w.nch;
-        if (more) ring.load(tb, K, V, D, w.h, ch + 1);
-        const Tin* Ks = ring.ks(ch & 1);
-        const Tin* Vs = ring.vs(ch & 1);
+        for (int j = 0; j < MT; ++j) dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (kDeltaFromO) {
+          float x = 0.0f;
 #pragma unroll
-        for (int bl = 0; bl < kChunk / kBlk; ++bl) {
-          const int b = ch * (kChunk / kBlk) + bl;
-          if (!block_live(tb, b, wave)) continue;
-          bool live[4];
-          mask(b, live);
-          f4 sv, tv;
-          scores(Ks, Vs, bl, sv, tv);
-          if (pass == 0) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc += live[r] ? fast_exp2(sv[r] - l2) * tv[r] : 0.0f;
-            continue;
-          }
-          float ds[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) ds[r] = live[r] ? fast_exp2(sv[r] - l2) * (tv[r] - dl) * scale : 0.0f;
-          if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per output tile
-            const uint2 dw = pack_bf16(ds);
-#pragma unroll
-            for (int j = 0; j < MT; ++j)
-              dq[j] = mfma_rows_bf16(Ks + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, dw, dq[j]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < MT; ++j)
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                dq[j] = mfma16(ld1(Ks + (kBlk * bl + 4 * g + r) * WS + kBlk * j + c), ds[r], dq[j]);
-          }
+          for (int j = 0; j < KD; ++j) x += gf.v[j] * ov[j];
+          dl = group_sum(x);
         }
-        if (more) ring.store((ch + 1) & 1);
-        __syncthreads();
       }
-      if (pass == 0) dl = group_sum(acc);
-    }
-    if (q < w.ntile) {
-      const int64_t row = static_cast<int64_t>(w.s) + q;
-      const int pos = rope.cos_t ? rope_pos(pl.depth[row], rope.seq_len) : 0;
+      const bool more = st + 1 < nsteps;
+      if (more) {
+        const int h2 = (st + 1) / per;
+        ring.load(tb, K, V, D, h0 + h2, (st + 1 - h2 * per) % w.nch);
+      }
+      const bool last = r0 + 1 == per;
+      if (last && hl + 1 < hpu) fetch(h + 1, qn, gn, l2n, on);
+      const Tin* Ks = ring.ks(st & 1);
+      const Tin* Vs = ring.vs(st & 1);
 #pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        float v[4] = {dq[j][0], dq[j][1], dq[j][2], dq[j][3]};
-        if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
-        store_vec<4>(dQ + row * D + w.h * HD + kBlk * j + 4 * g, v);
+      for (int bl = 0; bl < kChunk / kBlk; ++bl) {
+        const int b = ch * (kChunk / kBlk) + bl;
+        if (!block_live(tb, b, wave)) continue;
+        bool live[4];
+        mask(b, live);
+        f4 sv, tv;
+        scores(Ks, Vs, bl, sv, tv);
+        if (pass == 0) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc += live[r] ? fast_exp2(sv[r] - l2) * tv[r] : 0.0f;
+          continue;
+        }
+        float ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ds[r] = live[r] ? fast_exp2(sv[r] - l2) * (tv[r] - dl) * scale : 0.0f;
+        if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per output tile
+          const uint2 dw = pack_bf16(ds);
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+            dq[j] = mfma_rows_bf16(Ks + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, dw, dq[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              dq[j] = mfma16(ld1(Ks + (kBlk * bl + 4 * g + r) * WS + kBlk * j + c), ds[r], dq[j]);
+        }
       }
-      if (g == 0) Dl[row * H + w.h] = dl;
+      if (pass == 0 && ch + 1 == w.nch) dl = group_sum(acc);
+      if (more) ring.store((st + 1) & 1);
+      if (last) {
+        if (q < w.ntile) {
+          const int64_t row = static_cast<int64_t>(w.s) + q;
+          const int pos = rope.cos_t ? rope_pos(qdep, rope.seq_len) : 0;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            float v[4] = {dq[j][0], dq[j][1], dq[j][2], dq[j][3]};
+            if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
+            store_vec<4>(dQ + row * D + h * HD + kBlk * j + 4 * g, v);
+          }
+          if (g == 0) Dl[row * H + h] = dl;
+        }
+        qf = qn;
+        gf = gn;
+        l2 = l2n;
+        if constexpr (kDeltaFromO) {
+#pragma unroll
+          for (int j = 0; j < KD; ++j) ov[j] = on[j];
+        }
+      }
+      __syncthreads();
     }
     u = uniform(tb.next[par]);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward, key side: dK, dV of the tile's key list. S = Q_i K^T puts key c
-// in lane column c (queries 4g .. 4g+3 in its registers); dV^T += dO^T P,
-// dK^T += Q^T dS. Key blocks are dealt to the waves in turn; a wave loads
-// the next block's K and V slices while it works on the current one.
+// Backward, key side: dK, dV of the tile's key list, head after head. The
+// head's Q and dO rows, lse and δ are staged in LDS (the next head's are
+// fetched into registers while the current one is worked on). S = Q_i K^T
+// puts key c in lane column c (queries 4g .. 4g+3 in its registers);
+// dV^T += dO^T P, dK^T += Q^T dS. Key blocks are dealt to the waves in
+// turn; a wave loads the K and V slices of its next (head, key block) while
+// it works on the current one.
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT, typename RopeT>
 __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
     float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ Pk, float* __restrict__ Pv,
-    const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+    const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeT rope, int H, int hpu,
+    float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
   constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));
   constexpr int WS = row_stride(HD, sizeof(Tin));
   constexpr int PIECES = HD / EPC;
   constexpr int ROWJ = kTile * PIECES;  // 16-byte pieces of one staged tensor
+  constexpr int RPER = ROWJ / kThreads;
   static_assert(ROWJ % kThreads == 0, "whole rounds of the workgroup per staged tensor");
   __shared__ Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -445,149 +503,166 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
-  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
   int* ctr = pl.sched + 2;
   if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
   __syncthreads();
   int u = uniform(tb.next[1]);
+  const int ngr = H / hpu;  // head groups: unit u = (tile u / ngr, heads hpu * (u % ngr) ..)
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * ngr;
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
-    // The tile's Q and dO rows (rows past a short tile repeat its last row).
-    {
-      const int t = u / H, h = u - t * H;
-      const int64_t s = static_cast<int64_t>(t) * kTile;
-      const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s)) - 1;
-      u4 rq[ROWJ / kThreads], rg[ROWJ / kThreads];
+    const int t = u / ngr;
+    const int h0 = (u % ngr) * hpu;
+    const int h1 = h0 + hpu;
+    const int s = t * kTile;
+    const int ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s));
+    // Staged rows of head h (rows past a short tile repeat its last row).
+    u4 rq[RPER], rg[RPER];
+    float rl = 0.0f, rd = 0.0f;
+    auto fetch_rows = [&](int h) {
 #pragma unroll
-      for (int k = 0; k < ROWJ / kThreads; ++k) {
+      for (int k = 0; k < RPER; ++k) {
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
-        const int64_t off = (s + min(j / PIECES, last)) * D + h * HD + (j % PIECES) * EPC;
+        const int64_t off = (static_cast<int64_t>(s) + min(j / PIECES, ntile - 1)) * D + h * HD + (j % PIECES) * EPC;
         rq[k] = *reinterpret_cast<const u4*>(Q + off);
         rg[k] = *reinterpret_cast<const u4*>(dO + off);
       }
-      const Unit w = build_tables(pl, tb, u, H, true);
       if (threadIdx.x < kTile) {
-        const int r = min(static_cast<int>(threadIdx.x), w.ntile - 1);
-        tb.l2[threadIdx.x] = lse[(s + r) * H + h] * kLog2e;
-        tb.dl[threadIdx.x] = Dl[(s + r) * H + h];
+        const int64_t r = static_cast<int64_t>(s) + min(static_cast<int>(threadIdx.x), ntile - 1);
+        rl = lse[r * H + h];
+        rd = Dl[r * H + h];
       }
+    };
+    auto stage_rows = [&]() {
 #pragma unroll
-      for (int k = 0; k < ROWJ / kThreads; ++k) {
+      for (int k = 0; k < RPER; ++k) {
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
         *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
         *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
       }
-      __syncthreads();
-    }
-    const int t = u / H, h = u - t * H;
-    const int s = t * kTile;
-    const int ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s));
-    const int poff = pl.pref_off[t];
-    const int A = pl.pref_off[t + 1] - poff;
+      if (threadIdx.x < kTile) {
+        tb.l2[threadIdx.x] = rl * kLog2e;
+        tb.dl[threadIdx.x] = rd;
+      }
+    };
+    fetch_rows(h0);
+    const Unit w = build_tables(pl, tb, t, true);
+    stage_rows();
+    __syncthreads();
+    const int poff = w.poff;
+    const int A = w.A;
     const int nkb = (A + ntile + kBlk - 1) / kBlk;
-    // K and V slices of key block b (keys past the list name row s).
+    // K and V slices of (head h, key block b); keys past the list name row s.
     Slice<Tin, KD> kf, vf, nkf, nvf;
-    auto fetch = [&](int b, Slice<Tin, KD>& a, Slice<Tin, KD>& v) {
+    auto fetch = [&](int h, int b, Slice<Tin, KD>& a, Slice<Tin, KD>& v) {
       const int64_t row = tb.krow[kBlk * b + c];
       a.load(K + row * D + h * HD + KD * g);
       v.load(V + row * D + h * HD + KD * g);
     };
-    if (wave < nkb) fetch(wave, nkf, nvf);
-    for (int b = wave; b < nkb; b += 4) {
-      kf = nkf;
-      vf = nvf;
-      if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
-      kf.scale(qscale);
-      f4 dk[MT], dv[MT];
+    if (wave < nkb) fetch(h0, wave, nkf, nvf);
+    for (int h = h0; h < h1; ++h) {
+      if (h + 1 < h1) fetch_rows(h + 1);
+      for (int b = wave; b < nkb; b += 4) {
+        kf = nkf;
+        vf = nvf;
+        if (b + 4 < nkb) fetch(h, b + 4, nkf, nvf);
+        else if (h + 1 < h1) fetch(h + 1, wave, nkf, nvf);
+        kf.scale(qscale);
+        f4 dk[MT], dv[MT];
 #pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        dv[j] = dk[j];
-      }
-      const int key = kBlk * b + c;
-      const int iv = tb.kint[key];
-      const int i0 = uniform(tb.blo[b]) / kBlk;
-      const int i1 = (uniform(tb.bhi[b]) + kBlk - 1) / kBlk;
-      for (int i = i0; i < i1; ++i) {
-        const int qr = kBlk * i + c;  // query row this lane supplies
-        const int q0 = kBlk * i + 4 * g;
-        bool live[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) live[r] = in_interval(q0 + r, iv);
-        Slice<Tin, KD> qa, ga;
-        qa.load(Qs + qr * WS + KD * g);
-        ga.load(Gs + qr * WS + KD * g);
-        f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // sv[r]: query q0+r against key `key`
-        const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
-        if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
-        const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
-        const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
-        float p[4], ds[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
-          ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+        for (int j = 0; j < MT; ++j) {
+          dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+          dv[j] = dk[j];
         }
-        if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
-          const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
+        const int key = kBlk * b + c;
+        const int iv = tb.kint[key];
+        const int i0 = uniform(tb.blo[b]) / kBlk;
+        const int i1 = (uniform(tb.bhi[b]) + kBlk - 1) / kBlk;
+        for (int i = i0; i < i1; ++i) {
+          const int qr = kBlk * i + c;  // query row this lane supplies
+          const int q0 = kBlk * i + 4 * g;
+          bool live[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) live[r] = in_interval(q0 + r, iv);
+          Slice<Tin, KD> qa, ga;
+          qa.load(Qs + qr * WS + KD * g);
+          ga.load(Gs + qr * WS + KD * g);
+          f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // sv[r]: query q0+r against key `key`
+          const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+          if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
+          const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
+          const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
+          float p[4], ds[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
+            ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+          }
+          if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
+            const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              const int col = q0 * WS + kBlk * j + c;
+              dv[j] = mfma_rows_bf16(Gs + col, WS, pw, dv[j]);
+              dk[j] = mfma_rows_bf16(Qs + col, WS, dw, dk[j]);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int row = (q0 + r) * WS + kBlk * j + c;
+                dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
+                dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+              }
+          }
+        }
+        // Emit dims 16j+4g.. of the key.
+        if (key < A) {
+          const int64_t prow = static_cast<int64_t>(poff) + key;  // prefix entry `key` = depth key+1
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
-            const int col = q0 * WS + kBlk * j + c;
-            dv[j] = mfma_rows_bf16(Gs + col, WS, pw, dv[j]);
-            dk[j] = mfma_rows_bf16(Qs + col, WS, dw, dk[j]);
+            float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+            float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+            store_vec<4>(Pk + prow * D + h * HD + kBlk * j + 4 * g, a);
+            store_vec<4>(Pv + prow * D + h * HD + kBlk * j + 4 * g, v);
           }
-        } else {
+        } else if (key < A + ntile) {
+          const int r = key - A;
+          const int64_t a = static_cast<int64_t>(s) + r;
+          const bool done = tb.rend[r] <= s + ntile;
+          const int pos = rope.cos_t ? rope_pos(tb.rdep[r], rope.seq_len) : 0;
 #pragma unroll
-          for (int j = 0; j < MT; ++j)
+          for (int j = 0; j < MT; ++j) {
+            const int d0 = kBlk * j + 4 * g;
+            float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+            float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+            if (done) {
+              if (acc_dk) {
+                float y[4];
+                load_vec<4>(acc_dk + a * D + h * HD + d0, y);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = (q0 + r) * WS + kBlk * j + c;
-              dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
-              dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+                for (int x = 0; x < 4; ++x) gk[x] += y[x];
+              }
+              if (acc_dv) {
+                float y[4];
+                load_vec<4>(acc_dv + a * D + h * HD + d0, y);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) gv[x] += y[x];
+              }
+              if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
             }
+            store_vec<4>(dK + a * D + h * HD + d0, gk);
+            store_vec<4>(dV + a * D + h * HD + d0, gv);
+          }
         }
       }
-      // Emit dims 16j+4g.. of the key.
-      if (key < A) {
-        const int64_t prow = static_cast<int64_t>(poff) + key;  // prefix entry `key` = depth key+1
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          float a[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
-          float v[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
-          store_vec<4>(Pk + prow * D + h * HD + kBlk * j + 4 * g, a);
-          store_vec<4>(Pv + prow * D + h * HD + kBlk * j + 4 * g, v);
-        }
-      } else if (key < A + ntile) {
-        const int r = key - A;
-        const int64_t a = static_cast<int64_t>(s) + r;
-        const bool done = tb.rend[r] <= s + ntile;
-        const int pos = rope.cos_t ? rope_pos(tb.rdep[r], rope.seq_len) : 0;
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          const int d0 = kBlk * j + 4 * g;
-          float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
-          float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
-          if (done) {
-            if (acc_dk) {
-              float y[4];
-              load_vec<4>(acc_dk + a * D + h * HD + d0, y);
-#pragma unroll
-              for (int x = 0; x < 4; ++x) gk[x] += y[x];
-            }
-            if (acc_dv) {
-              float y[4];
-              load_vec<4>(acc_dv + a * D + h * HD + d0, y);
-#pragma unroll
-              for (int x = 0; x < 4; ++x) gv[x] += y[x];
-            }
-            if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
-          }
-          store_vec<4>(dK + a * D + h * HD + d0, gk);
-          store_vec<4>(dV + a * D + h * HD + d0, gv);
-        }
+      __syncthreads();  // the head's staged rows are no longer read
+      if (h + 1 < h1) {
+        stage_rows();
+        __syncthreads();
       }
     }
-    __syncthreads();  // the staged rows and tables are free for the next unit
     u = uniform(tb.next[par]);
   }
 }
