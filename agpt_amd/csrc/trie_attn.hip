@@ -493,20 +493,43 @@ __global__ __launch_bounds__(256) void trie_bwd_reduce_kernel(
       float sk[VW], sv[VW];
       ld_cols<VW>(dK + a * D + col0, sk);
       ld_cols<VW>(dV + a * D + col0, sv);
+      // The parts in tile order (a chunk sum for each whole chunk, else the
+      // tile's partial), kR rows of each tensor in flight at a time.
+      constexpr int kR = 4;
       int u = t + 1;
       while (u <= u_last) {
-        const int c = u / kChunkTiles;
-        if (u == c * kChunkTiles && u + kChunkTiles - 1 <= u_last) {
-          const int64_t o = (static_cast<int64_t>(c) * pl.max_depth + k) * D + col0;
-          add_cols<VW>(sk, Ck + o);
-          add_cols<VW>(sv, Cv + o);
-          u += kChunkTiles;
-        } else {
-          const int64_t o = (static_cast<int64_t>(pl.pref_off[u]) + k) * D + col0;
-          add_cols<VW>(sk, Pk + o);
-          add_cols<VW>(sv, Pv + o);
-          ++u;
+        const float* srck[kR];
+        const float* srcv[kR];
+        int n = 0;
+        for (; n < kR && u <= u_last; ++n) {
+          const int c = u / kChunkTiles;
+          if (u == c * kChunkTiles && u + kChunkTiles - 1 <= u_last) {
+            const int64_t o = (static_cast<int64_t>(c) * pl.max_depth + k) * D + col0;
+            srck[n] = Ck + o;
+            srcv[n] = Cv + o;
+            u += kChunkTiles;
+          } else {
+            const int64_t o = (static_cast<int64_t>(pl.pref_off[u]) + k) * D + col0;
+            srck[n] = Pk + o;
+            srcv[n] = Pv + o;
+            ++u;
+          }
         }
+        float yk[kR][VW], yv[kR][VW];
+#pragma unroll
+        for (int x = 0; x < kR; ++x)
+          if (x < n) {
+            ld_cols<VW>(srck[x], yk[x]);
+            ld_cols<VW>(srcv[x], yv[x]);
+          }
+#pragma unroll
+        for (int x = 0; x < kR; ++x)
+          if (x < n)
+#pragma unroll
+            for (int i = 0; i < VW; ++i) {
+              sk[i] += yk[x][i];
+              sv[i] += yv[x][i];
+            }
       }
       if (acc_dk) add_cols<VW>(sk, acc_dk + a * D + col0);
       if (acc_dv) add_cols<VW>(sv, acc_dv + a * D + col0);
