@@ -678,6 +678,9 @@ struct agpt_attn_s {
   int fhg = 1;                  // heads per workgroup of the one-pass backward
   bool carry = false;           // one-pass backward carries path sums (E, F replace Pk, Pv)
   bool deep = false;            // block kernels at head_dim 64: streamed key set (trie_deep.h)
+  bool deep_carry = false;      // deep key side carries path sums (E, F replace Pk, Pv)
+  float* d_Cs = nullptr;        // deep carry: per-workgroup carry rows [slot][2][P][2][head_dim]
+  int cs_slots = 0;             // workgroups the carry rows are sized for
   float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
   float* d_F = nullptr;
   size_t fb_lds = 0;
@@ -705,7 +708,7 @@ void free_plan(agpt_attn_s* h) {
       if (own) (void)hipFree(*p);
       *p = nullptr;
     }
-  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv, &h->d_Dl, &h->d_E, &h->d_F};
+  float** fp[] = {&h->d_Pk, &h->d_Pv, &h->d_Ck, &h->d_Cv, &h->d_Dl, &h->d_E, &h->d_F, &h->d_Cs};
   for (auto p : fp)
     if (*p) {
       if (own) (void)hipFree(*p);
@@ -971,6 +974,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     // bf16 row segment already fills whole lines), its key set streamed
     // through a ring (trie_deep.h) instead of held whole in LDS.
     h->deep = hd == 64 && hg == 1 && env_int("AGPT_ATTN_DEEP", 1) != 0;
+    h->deep_carry = h->deep && env_int("AGPT_ATTN_CARRY", 1) != 0;
     if (h->deep) {
       h->fwd_lds = h->bq_lds = agpt_deep::ring_lds_bytes(hd, elem);
       h->kv_lds = agpt_deep::rows_lds_bytes(hd, elem);
@@ -992,7 +996,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     }
     if (ok) return;
     h->variant = 5;  // try the chain-group walk
-    h->fused = h->carry = h->deep = false;
+    h->fused = h->carry = h->deep = h->deep_carry = false;
   }
   if (h->variant != 5) {
     const int t = env_int("AGPT_ATTN_TILE", 64);
@@ -1065,6 +1069,9 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
   h->max_depth = maxd;
   int tile = 64;
   choose_variant(h, tile);
+  // A static plan (fixed scratch) keeps the deep key side's per-tile
+  // partials: the carry's per-workgroup rows would not fit beside them.
+  if (ar.base) h->deep_carry = false;
   const int32_t n_tiles = static_cast<int32_t>((n + tile - 1) / tile);
   std::vector<int32_t> pref_off(static_cast<size_t>(n_tiles) + 2, 0);
   for (int32_t t = 0; t < n_tiles; ++t) pref_off[t + 1] = pref_off[t] + depth[static_cast<int64_t>(t) * tile] - 1;
@@ -1190,14 +1197,26 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
     // workgroups without a chunk.
     int cus = 256;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
-    const int dflt = static_cast<int>(std::min<int64_t>(24, std::max<int64_t>(1, n_tiles / (8 * std::max(cus, 1)))));
+    // The deep key side's units are (chunk, head): ~8 per CU.
+    const int64_t per_claim = h->deep_carry ? static_cast<int64_t>(n_tiles) * h->cfg.n_heads : n_tiles;
+    const int dflt = static_cast<int>(std::min<int64_t>(24, std::max<int64_t>(1, per_claim / (8 * std::max(cus, 1)))));
     h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", dflt));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
+    // Chunks of one tile would carry nothing: the per-tile partials serve.
+    if (h->chunk_tiles < 2) h->deep_carry = false;
+    h->cs_slots = h->deep_carry ? static_cast<int>(std::min<int64_t>(static_cast<int64_t>(h->n_chunks_sched) *
+                                                                          h->cfg.n_heads,
+                                                                      8LL * std::max(cus, 1)))
+                                : 0;
   }
   auto fl = [&](float** p, size_t bytes) { return ar.get(reinterpret_cast<void**>(p), bytes); };
-  if (h->carry) {
+  if (h->carry || h->deep_carry) {
     const size_t ebytes = static_cast<size_t>(h->n_chunks_sched) * agpt_blk::prefix_cap(maxd) * 2 * D * sizeof(float);
     if ((rc = fl(&h->d_E, ebytes)) != AGPT_OK || (rc = fl(&h->d_F, ebytes)) != AGPT_OK) return rc;
+    if (h->deep_carry &&
+        (rc = fl(&h->d_Cs, static_cast<size_t>(h->cs_slots) * 2 * agpt_blk::prefix_cap(maxd) * 2 *
+                               h->cfg.head_dim * sizeof(float))) != AGPT_OK)
+      return rc;
   } else {
     const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
     if ((rc = fl(&h->d_Pk, pbytes)) != AGPT_OK || (rc = fl(&h->d_Pv, pbytes)) != AGPT_OK) return rc;
@@ -1342,9 +1361,10 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   char buf[400];
   if (h->variant == 6 && h->deep)
     snprintf(buf, sizeof(buf),
-             "streamed key ring (deep prefixes) 16x16 mfma, split backward: tile_rows=%d tiles=%d "
+             "streamed key ring (deep prefixes) 16x16 mfma, split backward%s: tile_rows=%d tiles=%d "
              "heads_per_wg=1 key_chunk=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
-             h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds, h->kv_lds, h->max_lds);
+             h->deep_carry ? " with path-carry" : "", h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds,
+             h->kv_lds, h->max_lds);
   else if (h->variant == 6)
     snprintf(buf, sizeof(buf),
              "streaming block-sparse 16x16 mfma, %s backward: tile_rows=%d tiles=%d heads_per_wg=%d "
@@ -1559,7 +1579,7 @@ template <int HD>
 void launch_ctx(const agpt_attn_s* h, float* dk, float* dv, RopeArgs rope, hipStream_t st) {
   if (h->n_ctx <= 0) return;
   const int D = h->cfg.n_heads * HD;
-  const bool chunks = h->variant == 6 && h->fused && h->carry;
+  const bool chunks = h->variant == 6 && ((h->fused && h->carry) || h->deep_carry);
   const int P = agpt_blk::prefix_cap(h->max_depth);
   const int rows = chunks ? h->chunk_tiles * agpt_blk::kTile : h->tile;
   const int parts = chunks ? h->n_chunks_sched : h->n_tiles;
@@ -1628,6 +1648,26 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                          static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
                          static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, hpu, scale);
       pm.mark(1);
+      if (h->deep_carry) {
+        auto fc = agpt_deep::bwd_kv_carry_kernel<HD, Tin, PlanDev, RopeArgs>;
+        set_lds(fc, h->kv_lds);
+        int cus = 256;
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
+        const int grid = std::max(1, std::min(wg_per_cu(fc, h->kv_lds, h->max_lds) * cus, h->cs_slots));
+        hipLaunchKernelGGL(fc, dim3(grid), dim3(agpt_deep::kThreads), h->kv_lds, st, plan_dev(h),
+                           static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v), lse,
+                           h->d_Dl, static_cast<const Tin*>(dO), dk, dv, h->d_E, h->d_F, h->d_Cs, acc_dk, acc_dv,
+                           rope, h->cfg.n_heads, scale);
+        pm.mark(2);
+        pm.mark(3);
+        if (h->n_chunks_sched > 1)
+          hipLaunchKernelGGL((agpt_blk::bwd_carry_kernel<HD, PlanDev, RopeArgs>), dim3(h->n_chunks_sched - 1),
+                             dim3(256), 0, st, plan_dev(h), h->d_E, h->d_F, dk, dv, acc_dk, acc_dv, rope,
+                             h->cfg.n_heads);
+        launch_ctx<HD>(h, dk, dv, rope, st);
+        pm.mark(4);
+        return;
+      }
       auto fk = agpt_deep::bwd_kv_kernel<HD, Tin, PlanDev, RopeArgs>;
       set_lds(fk, h->kv_lds);
       hipLaunchKernelGGL(fk, dim3(stream_grid(h, fk, h->kv_lds, hpu)), dim3(agpt_deep::kThreads), h->kv_lds, st,

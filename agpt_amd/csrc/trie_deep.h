@@ -80,6 +80,7 @@ struct alignas(16) Tables {
   int32_t krow[kKeyCap];  // per key: its row in the tensors (negative: a context row of a range plan)
   int32_t blo[kKeyCap / kBlk];  // per key block: least lo of its live keys (kTile if none)
   int32_t bhi[kKeyCap / kBlk];  // per key block: greatest lo + len
+  int32_t pend[kKeyCap];  // per prefix key: its subtree end (rows of the plan)
   int32_t rdep[kTile];   // depth of the tile rows
   int32_t rend[kTile];   // subtree end of the tile rows
   alignas(16) float l2[kTile];  // lse * log2(e) of the tile rows (key side)
@@ -107,7 +108,9 @@ __device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t,
     int iv = 0, row = w.s;
     if (j < w.A) {
       row = pl.prefix[w.poff + j];
-      iv = min(pl.pref_end[w.poff + j] - w.s, w.ntile) << 16;
+      const int e = pl.pref_end[w.poff + j];
+      iv = min(e - w.s, w.ntile) << 16;
+      if (row_tabs) tb.pend[j] = e;
     } else if (j < w.nk) {
       const int r = j - w.A;
       row = w.s + r;
@@ -662,6 +665,242 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
         stage_rows();
         __syncthreads();
       }
+    }
+    u = uniform(tb.next[par]);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Key side with a path carry. A unit is (chunk of consecutive tiles, head);
+// the workgroup walks the chunk's tiles in order. The keys a tile leaves
+// open (subtree not finished) are exactly the next tile's prefix, one per
+// depth, so the sums of the current path's keys are carried from tile to
+// tile by depth instead of being left as per-tile partials: in this
+// workgroup's carry rows Cs [parity][depth][dK, dV][HD] (global memory,
+// read and written only by this workgroup; a tile reads the rows of its
+// parity and writes the next tile's into the other, with a barrier between
+// tiles). A prefix key the next tile still sees adds its tile sum to the
+// carry; one it does not see is finished: to dK/dV (a key first seen in the
+// chunk whose subtree ended), to the chunk partial E[chunk][depth] (a key
+// from before the chunk), or at the chunk's last tile to F[chunk][depth]
+// (a key of this chunk still open). Open tile rows start their depth's
+// sum. agpt_blk::bwd_carry_kernel then finishes the keys whose sums cross
+// chunks (F of their chunk plus E of the later chunks, in chunk order).
+// E, F: [n_chunks][P][2][D].
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_kv_carry_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
+    float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ E, float* __restrict__ F,
+    float* __restrict__ Cs, const float* __restrict__ acc_dk, const float* __restrict__ acc_dv, RopeT rope,
+    int H, float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));
+  constexpr int WS = row_stride(HD, sizeof(Tin));
+  constexpr int PIECES = HD / EPC;
+  constexpr int ROWJ = kTile * PIECES;  // 16-byte pieces of one staged tensor
+  constexpr int RPER = ROWJ / kThreads;
+  static_assert(ROWJ % kThreads == 0, "whole rounds of the workgroup per staged tensor");
+  __shared__ Tables tb;
+  extern __shared__ __align__(16) unsigned char dyn[];
+  Tin* Qs = reinterpret_cast<Tin*>(dyn);
+  Tin* Gs = Qs + kTile * WS;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const int P = agpt_blk::prefix_cap(pl.max_depth);
+  const float qscale = scale * kLog2e;
+  float* const cs = Cs + static_cast<int64_t>(blockIdx.x) * 2 * P * 2 * HD;
+  const int64_t n_units = static_cast<int64_t>(pl.n_chunks) * H;
+  int* ctr = pl.sched + 2;
+  if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(tb.next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
+    const int chunk = u / H;
+    const int h = u - chunk * H;
+    const int t0 = chunk * pl.chunk_tiles;
+    const int t1 = chunk + 1 == pl.n_chunks ? pl.n_tiles : t0 + pl.chunk_tiles;
+    const int64_t s_first = static_cast<int64_t>(t0) * kTile;  // keys with rows before it come from before the chunk
+    // Staged rows of tile t (rows past a short tile repeat its last row).
+    u4 rq[RPER], rg[RPER];
+    float rl = 0.0f, rd = 0.0f;
+    auto fetch_rows = [&](int t) {
+      const int64_t s = static_cast<int64_t>(t) * kTile;
+      const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s)) - 1;
+#pragma unroll
+      for (int k = 0; k < RPER; ++k) {
+        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        const int64_t off = (s + min(j / PIECES, last)) * D + h * HD + (j % PIECES) * EPC;
+        rq[k] = *reinterpret_cast<const u4*>(Q + off);
+        rg[k] = *reinterpret_cast<const u4*>(dO + off);
+      }
+      if (threadIdx.x < kTile) {
+        const int64_t r = s + min(static_cast<int>(threadIdx.x), last);
+        rl = lse[r * H + h];
+        rd = Dl[r * H + h];
+      }
+    };
+    fetch_rows(t0);
+    for (int t = t0; t < t1; ++t) {
+      const bool first = t == t0;
+      const bool last = t + 1 == t1;
+      const int cur = (t - t0) & 1;
+      const Unit w = build_tables(pl, tb, t, true);
+#pragma unroll
+      for (int k = 0; k < RPER; ++k) {
+        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
+        *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
+      }
+      if (threadIdx.x < kTile) {
+        tb.l2[threadIdx.x] = rl * kLog2e;
+        tb.dl[threadIdx.x] = rd;
+      }
+      __syncthreads();
+      if (!last) fetch_rows(t + 1);
+      const int s = w.s, ntile = w.ntile, A = w.A;
+      const int nkb = (A + ntile + kBlk - 1) / kBlk;
+      Slice<Tin, KD> kf, vf, nkf, nvf;
+      auto fetch = [&](int b, Slice<Tin, KD>& a, Slice<Tin, KD>& v) {
+        const int64_t row = tb.krow[kBlk * b + c];
+        a.load(K + row * D + h * HD + KD * g);
+        v.load(V + row * D + h * HD + KD * g);
+      };
+      if (wave < nkb) fetch(wave, nkf, nvf);
+      for (int b = wave; b < nkb; b += 4) {
+        kf = nkf;
+        vf = nvf;
+        if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
+        kf.scale(qscale);
+        f4 dk[MT], dv[MT];
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+          dv[j] = dk[j];
+        }
+        const int key = kBlk * b + c;
+        const int iv = tb.kint[key];
+        const int i0 = uniform(tb.blo[b]) / kBlk;
+        const int i1 = (uniform(tb.bhi[b]) + kBlk - 1) / kBlk;
+        for (int i = i0; i < i1; ++i) {
+          const int qr = kBlk * i + c;
+          const int q0 = kBlk * i + 4 * g;
+          bool live[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) live[r] = in_interval(q0 + r, iv);
+          Slice<Tin, KD> qa, ga;
+          qa.load(Qs + qr * WS + KD * g);
+          ga.load(Gs + qr * WS + KD * g);
+          f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+          const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+          if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
+          const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
+          const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
+          float p[4], ds[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
+            ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+          }
+          if constexpr (sizeof(Tin) == 2) {
+            const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              const int col = q0 * WS + kBlk * j + c;
+              dv[j] = mfma_rows_bf16(Gs + col, WS, pw, dv[j]);
+              dk[j] = mfma_rows_bf16(Qs + col, WS, dw, dk[j]);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int row = (q0 + r) * WS + kBlk * j + c;
+                dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
+                dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+              }
+          }
+        }
+        // This lane's share of the key: dims 16j+4g.. of dK (gk) and dV (gv).
+        float gk[MT][4], gv[MT][4];
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            gk[j][x] = dk[j][x];
+            gv[j][x] = dv[j][x];
+          }
+        auto slot = [&](int parity, int d) { return cs + ((parity * P + d) * 2) * HD + 4 * g; };
+        auto put = [&](float* o, int stride) {  // o: the key's dK row (dims), dV row `stride` floats on
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            store_vec<4>(o + kBlk * j, gk[j]);
+            store_vec<4>(o + stride + kBlk * j, gv[j]);
+          }
+        };
+        auto chunk_part = [&](float* base, int d) {
+          put(base + (static_cast<int64_t>(chunk) * P + d) * 2 * D + h * HD + 4 * g, D);
+        };
+        // Final dK/dV of row a at depth dep: + seeds, inverse RoPE of dK.
+        auto finish = [&](int64_t a, int dep) {
+          const int pos = rope.cos_t ? rope_pos(dep, rope.seq_len) : 0;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const int d0 = kBlk * j + 4 * g;
+            if (acc_dk) {
+              float y[4];
+              load_vec<4>(acc_dk + a * D + h * HD + d0, y);
+#pragma unroll
+              for (int x = 0; x < 4; ++x) gk[j][x] += y[x];
+            }
+            if (acc_dv) {
+              float y[4];
+              load_vec<4>(acc_dv + a * D + h * HD + d0, y);
+#pragma unroll
+              for (int x = 0; x < 4; ++x) gv[j][x] += y[x];
+            }
+            if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk[j], rope.cos_t, rope.sin_t, pos, d0);
+            store_vec<4>(dK + a * D + h * HD + d0, gk[j]);
+            store_vec<4>(dV + a * D + h * HD + d0, gv[j]);
+          }
+        };
+        if (key < A) {
+          const int d = key;  // prefix entry d = depth d+1
+          const int e = tb.pend[d];
+          if (!first) {
+            const float* cp = slot(cur, d);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              float yk[4], yv[4];
+              load_vec<4>(cp + kBlk * j, yk);
+              load_vec<4>(cp + HD + kBlk * j, yv);
+#pragma unroll
+              for (int x = 0; x < 4; ++x) {
+                gk[j][x] = yk[x] + gk[j][x];
+                gv[j][x] = yv[x] + gv[j][x];
+              }
+            }
+          }
+          const bool cont = !last && e > s + ntile;  // the next tile of the chunk sees it
+          if (cont) put(slot(cur ^ 1, d), HD);
+          else if (tb.krow[key] < s_first) chunk_part(E, d);  // a key from before the chunk
+          else if (e > s + ntile) chunk_part(F, d);           // the chunk ends, the key's subtree does not
+          else finish(tb.krow[key], d + 1);
+        } else if (key < A + ntile) {
+          const int r = key - A;
+          const int64_t a = static_cast<int64_t>(s) + r;
+          if (tb.rend[r] <= s + ntile) finish(a, tb.rdep[r]);
+          else if (last) chunk_part(F, tb.rdep[r] - 1);
+          else put(slot(cur ^ 1, tb.rdep[r] - 1), HD);  // the next tile's prefix entry at its depth
+        }
+      }
+      __syncthreads();  // the tile's staged rows, tables and carry rows are done with
     }
     u = uniform(tb.next[par]);
   }
