@@ -46,7 +46,6 @@ using agpt_blk::kBlk;
 using agpt_blk::kRescaleLog2;
 using agpt_blk::ld1;
 using agpt_blk::mfma16;
-using agpt_blk::mfma_rows_bf16;
 using agpt_blk::pack_bf16;
 using agpt_blk::Slice;
 using agpt_blk::slice_dot;
@@ -63,13 +62,53 @@ constexpr int kKeyCap = (kMaxDepth - 1 + kTile + kChunk - 1) / kChunk * kChunk;
 constexpr float kNoMax = -1.0e30f;
 
 __host__ __device__ constexpr int row_stride(int hd, int elem) { return hd + 16 / elem; }
-// Dynamic LDS: the query-side ring [2 buffers][K, V][kChunk][WS] or the
-// key side's staged rows [Q, dO][kTile][WS].
-__host__ __device__ constexpr size_t ring_lds_bytes(int hd, int elem) {
-  return static_cast<size_t>(2 * 2 * kChunk) * row_stride(hd, elem) * elem;
+// bf16 operands of the second products (P·V, dS·K, P^T·dO, dS^T·Q) are
+// also staged transposed, [dim][row] with rows 64 + 4 apart: four
+// consecutive rows of one dim are then one 8-byte LDS read, the operand
+// slot of v_mfma_f32_16x16x16_bf16, instead of four 2-byte reads and two
+// packing instructions.
+constexpr int kTStride = kTile + 4;
+// Query-side ring layouts: K rows and V rows (fp32); K rows and V^T
+// (bf16 forward); K rows, V rows and K^T (bf16 dQ).
+constexpr int kRingKV = 0, kRingKVt = 1, kRingKVKt = 2;
+// (The dQ kernel keeps K and V rows: a third tile in the ring costs more
+// in workgroups per CU than its 8-byte reads save.)
+__host__ __device__ constexpr int ring_layout(int elem, bool dq) { return elem == 4 || dq ? kRingKV : kRingKVt; }
+__host__ __device__ constexpr size_t ring_buf_elems(int hd, int elem, int layout) {
+  return static_cast<size_t>(kChunk) * row_stride(hd, elem) +
+         (layout == kRingKVt ? static_cast<size_t>(hd) * kTStride : static_cast<size_t>(kChunk) * row_stride(hd, elem)) +
+         (layout == kRingKVKt ? static_cast<size_t>(hd) * kTStride : 0);
+}
+// Dynamic LDS: the query-side ring (two buffers) or the key side's staged
+// rows [Q, dO][kTile][WS] (bf16: and Q^T, dO^T [HD][kTStride]).
+__host__ __device__ constexpr size_t ring_lds_bytes(int hd, int elem, bool dq) {
+  return 2 * ring_buf_elems(hd, elem, ring_layout(elem, dq)) * elem;
 }
 __host__ __device__ constexpr size_t rows_lds_bytes(int hd, int elem) {
-  return static_cast<size_t>(2 * kTile) * row_stride(hd, elem) * elem;
+  return (static_cast<size_t>(2 * kTile) * row_stride(hd, elem) + (elem == 2 ? 2 * static_cast<size_t>(hd) * kTStride : 0)) *
+         elem;
+}
+
+// Stores 8 consecutive dims (d0 ..) of row `col` into a transposed bf16 tile.
+__device__ __forceinline__ void store_tr(bf16_t* t, int col, int d0, u4 x) {
+  uint16_t* p = reinterpret_cast<uint16_t*>(t) + d0 * kTStride + col;
+  p[0] = static_cast<uint16_t>(x.x);
+  p[kTStride] = static_cast<uint16_t>(x.x >> 16);
+  p[2 * kTStride] = static_cast<uint16_t>(x.y);
+  p[3 * kTStride] = static_cast<uint16_t>(x.y >> 16);
+  p[4 * kTStride] = static_cast<uint16_t>(x.z);
+  p[5 * kTStride] = static_cast<uint16_t>(x.z >> 16);
+  p[6 * kTStride] = static_cast<uint16_t>(x.w);
+  p[7 * kTStride] = static_cast<uint16_t>(x.w >> 16);
+}
+
+// One 16-deep bf16 step whose A operand is four consecutive rows of one dim
+// of a transposed tile (p = &T[dim][row 4g]) and whose B operand is this
+// lane's four weights (pack_bf16).
+__device__ __forceinline__ f4 mfma_tr_bf16(const bf16_t* p, uint2 wb, f4 acc) {
+  const uint2 a = *reinterpret_cast<const uint2*>(p);
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(agpt_blk::bf16x4_bits, a),
+                                                    __builtin_bit_cast(agpt_blk::bf16x4_bits, wb), acc, 0, 0, 0);
 }
 
 // The tile's key list and row tables. Keys 0 .. A-1 are the prefix rows
@@ -148,19 +187,23 @@ __device__ __forceinline__ bool block_live(const Tables& tb, int b, int i) {
 }
 
 // The double-buffered key ring of the query side: chunk c of the tile's key
-// list, K and V slices of one head, [buffer][K, V][kChunk][WS].
-template <int HD, typename Tin>
+// list, K and V slices of one head; per buffer K rows [kChunk][WS], then V
+// rows [kChunk][WS] or V^T [HD][kTStride], then (kRingKVKt) K^T.
+template <int HD, typename Tin, int kLayout>
 struct KeyRing {
   static constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));  // elements per 16-byte piece
   static constexpr int WS = row_stride(HD, sizeof(Tin));
   static constexpr int PIECES = HD / EPC;    // pieces per key slice
   static constexpr int PER_T = kChunk * PIECES;  // pieces per tensor per chunk
   static constexpr int PER = 2 * PER_T / kThreads;
+  static constexpr int BUF = static_cast<int>(ring_buf_elems(HD, sizeof(Tin), kLayout));
   static_assert(PER_T % kThreads == 0, "whole rounds of the workgroup per tensor");
+  static_assert(kLayout == kRingKV || sizeof(Tin) == 2, "transposed tiles are bf16");
   Tin* base;
   u4 r[PER];
-  __device__ __forceinline__ Tin* ks(int buf) const { return base + (2 * buf) * kChunk * WS; }
-  __device__ __forceinline__ Tin* vs(int buf) const { return base + (2 * buf + 1) * kChunk * WS; }
+  __device__ __forceinline__ Tin* ks(int buf) const { return base + buf * BUF; }
+  __device__ __forceinline__ Tin* vs(int buf) const { return base + buf * BUF + kChunk * WS; }  // V rows or V^T
+  __device__ __forceinline__ Tin* kt(int buf) const { return base + buf * BUF + 2 * kChunk * WS; }
   __device__ __forceinline__ void load(const Tables& tb, const Tin* K, const Tin* V, int D, int h, int c) {
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -176,7 +219,16 @@ struct KeyRing {
     for (int k = 0; k < PER; ++k) {
       const int ten = k * kThreads / PER_T;
       const int j = static_cast<int>(threadIdx.x) + k * kThreads - ten * PER_T;
-      *reinterpret_cast<u4*>((ten ? vs(buf) : ks(buf)) + (j / PIECES) * WS + (j % PIECES) * EPC) = r[k];
+      const int key = j / PIECES, d0 = (j % PIECES) * EPC;
+      if constexpr (kLayout == kRingKVt) {
+        if (ten) store_tr(vs(buf), key, d0, r[k]);
+        else *reinterpret_cast<u4*>(ks(buf) + key * WS + d0) = r[k];
+      } else {
+        *reinterpret_cast<u4*>((ten ? vs(buf) : ks(buf)) + key * WS + d0) = r[k];
+        if constexpr (kLayout == kRingKVKt) {
+          if (!ten) store_tr(kt(buf), key, d0, r[k]);
+        }
+      }
     }
   }
 };
@@ -197,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
                                                        int hpu, float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
-  using Ring = KeyRing<HD, Tin>;
+  using Ring = KeyRing<HD, Tin, ring_layout(sizeof(Tin), false)>;
   constexpr int WS = Ring::WS;
   __shared__ Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -279,10 +331,10 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
           l += p[r];
         }
         if constexpr (sizeof(Tin) == 2) {
-          const uint2 pw = pack_bf16(p);
+          const uint2 pw = pack_bf16(p);  // V^T in the ring: dim 16j+c, keys 16bl+4g ..
 #pragma unroll
           for (int j = 0; j < MT; ++j)
-            o[j] = mfma_rows_bf16(Vs + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, pw, o[j]);
+            o[j] = mfma_tr_bf16(Vs + (kBlk * j + c) * kTStride + kBlk * bl + 4 * g, pw, o[j]);
         } else {
 #pragma unroll
           for (int j = 0; j < MT; ++j)
@@ -329,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   constexpr int MT = HD / 16;
   constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
   constexpr int NP = kDeltaFromO ? 1 : 2;  // passes over the key chunks per head
-  using Ring = KeyRing<HD, Tin>;
+  using Ring = KeyRing<HD, Tin, ring_layout(sizeof(Tin), true)>;
   constexpr int WS = Ring::WS;
   __shared__ Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -436,7 +488,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           const uint2 dw = pack_bf16(ds);
 #pragma unroll
           for (int j = 0; j < MT; ++j)
-            dq[j] = mfma_rows_bf16(Ks + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, dw, dq[j]);
+            dq[j] = agpt_blk::mfma_rows_bf16(Ks + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, dw, dq[j]);
         } else {
 #pragma unroll
           for (int j = 0; j < MT; ++j)
@@ -501,6 +553,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   extern __shared__ __align__(16) unsigned char dyn[];
   Tin* Qs = reinterpret_cast<Tin*>(dyn);
   Tin* Gs = Qs + kTile * WS;
+  Tin* Qt = Gs + kTile * WS;  // bf16: Q^T, dO^T [HD][kTStride]
+  Tin* Gt = Qt + HD * kTStride;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -542,6 +596,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
         *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
         *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
+        if constexpr (sizeof(Tin) == 2) {
+          store_tr(Qt, j / PIECES, (j % PIECES) * EPC, rq[k]);
+          store_tr(Gt, j / PIECES, (j % PIECES) * EPC, rg[k]);
+        }
       }
       if (threadIdx.x < kTile) {
         tb.l2[threadIdx.x] = rl * kLog2e;
@@ -604,10 +662,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
             const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {
-              const int col = q0 * WS + kBlk * j + c;
-              dv[j] = mfma_rows_bf16(Gs + col, WS, pw, dv[j]);
-              dk[j] = mfma_rows_bf16(Qs + col, WS, dw, dk[j]);
+            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T: dim 16j+c, queries q0 ..
+              const int at = (kBlk * j + c) * kTStride + q0;
+              dv[j] = mfma_tr_bf16(Gt + at, pw, dv[j]);
+              dk[j] = mfma_tr_bf16(Qt + at, dw, dk[j]);
             }
           } else {
 #pragma unroll
@@ -690,7 +748,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 // E, F: [n_chunks][P][2][D].
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT, typename RopeT>
-__global__ __launch_bounds__(kThreads) void bwd_kv_carry_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void bwd_kv_carry_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
     float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ E, float* __restrict__ F,
@@ -708,6 +766,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_carry_kernel(
   extern __shared__ __align__(16) unsigned char dyn[];
   Tin* Qs = reinterpret_cast<Tin*>(dyn);
   Tin* Gs = Qs + kTile * WS;
+  Tin* Qt = Gs + kTile * WS;  // bf16: Q^T, dO^T [HD][kTStride]
+  Tin* Gt = Qt + HD * kTStride;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -757,6 +817,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_carry_kernel(
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
         *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
         *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
+        if constexpr (sizeof(Tin) == 2) {
+          store_tr(Qt, j / PIECES, (j % PIECES) * EPC, rq[k]);
+          store_tr(Gt, j / PIECES, (j % PIECES) * EPC, rg[k]);
+        }
       }
       if (threadIdx.x < kTile) {
         tb.l2[threadIdx.x] = rl * kLog2e;
@@ -811,10 +875,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_carry_kernel(
           if constexpr (sizeof(Tin) == 2) {
             const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {
-              const int col = q0 * WS + kBlk * j + c;
-              dv[j] = mfma_rows_bf16(Gs + col, WS, pw, dv[j]);
-              dk[j] = mfma_rows_bf16(Qs + col, WS, dw, dk[j]);
+            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T: dim 16j+c, queries q0 ..
+              const int at = (kBlk * j + c) * kTStride + q0;
+              dv[j] = mfma_tr_bf16(Gt + at, pw, dv[j]);
+              dk[j] = mfma_tr_bf16(Qt + at, dw, dk[j]);
             }
           } else {
 #pragma unroll
