@@ -100,6 +100,7 @@ TRIE_SYMBOLS = {
     "agpt_uniform_tokens": (C.c_int, [C.c_uint64, C.c_int, C.c_int64, _i32p]),
     "agpt_trie_build": (C.c_int, [_i32p, C.c_int64, C.c_int, C.c_int64, C.POINTER(_vp)]),
     "agpt_trie_build_radix": (C.c_int, [_i32p, C.c_int64, C.c_int, C.POINTER(_vp)]),
+    "agpt_trie_build_radix_part": (C.c_int, [_i32p, C.c_int64, C.c_int, C.c_int32, C.POINTER(_vp)]),
     "agpt_trie_build_chains": (C.c_int, [_i32p, C.c_int64, C.c_int, C.POINTER(_vp)]),
     "agpt_trie_stats": (C.c_int, [_vp, _i64p, _i64p, _i64p, _i32p, _i64p, _i64p]),
     "agpt_trie_export": (C.c_int, [_vp, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]),

@@ -355,6 +355,23 @@ extern "C" int agpt_trie_build_radix(const int32_t* tokens, int64_t n, int max_d
   return 0;
 }
 
+extern "C" int agpt_trie_build_radix_part(const int32_t* tokens, int64_t n, int max_depth,
+                                          int32_t first_token, agpt_trie_handle* out) {
+  if (!out || (!tokens && n > 0) || max_depth < 1) return 1;
+  *out = nullptr;
+  auto* h = new agpt_trie_s();
+  Trie& t = h->t;
+  std::vector<int64_t> starts;
+  for (const int64_t s : starts_of(n, 0))
+    if (tokens[s] == first_token) starts.push_back(s);
+  build_nodes(t, tokens, n, max_depth, starts, Paths::kStreaming);
+  count_heads(t);
+  drop_dead_edges(t);
+  finish(&t, true);
+  *out = h;
+  return 0;
+}
+
 extern "C" int agpt_trie_build_chains(const int32_t* tokens, int64_t n_chains, int chain_len,
                                       agpt_trie_handle* out) {
   if (!out || !tokens || n_chains < 0 || chain_len < 1) return 1;

@@ -125,6 +125,16 @@ def build_radix_trie(tokens: np.ndarray, max_depth: int, counts: bool = False) -
     return _export(h, counts)
 
 
+def build_radix_part(tokens: np.ndarray, max_depth: int, first_token: int) -> Trie:
+    """build_radix_trie's subtree of one root child (the starts whose first
+    token is first_token): the whole trie is these subtrees in token order."""
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    h = C.c_void_p()
+    if trie_lib().agpt_trie_build_radix_part(_ptr(tok), tok.shape[0], max_depth, int(first_token), C.byref(h)):
+        raise ValueError("agpt_trie_build_radix_part: bad arguments")
+    return _export(h)
+
+
 def build_chains(tokens: np.ndarray, n_chains: int, chain_len: int) -> Trie:
     tok = np.ascontiguousarray(tokens, dtype=np.int32)
     assert tok.shape[0] >= n_chains * chain_len

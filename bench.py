@@ -312,6 +312,146 @@ def bench_c3(args) -> int:
     return 0
 
 
+FULL_METRIC = ("trie-attn fwd+bwd node-tokens/sec over a whole corpus's trie, batch by batch "
+               "(1 GPU, exact range batches)")
+
+
+def bench_full(args) -> int:
+    """A corpus whose trie does not fit one GPU (full-size C4: ~6e8
+    node-tokens, 0.6 TB per bf16 [T, 512] tensor), processed batch by batch
+    on one GPU. The trie is built one root-child subtree at a time
+    (agpt_trie_build_radix_part, on host threads ahead of the GPU); each
+    subtree is cut at its bigram partitions into batches of at most
+    --batch-rows rows, each planned alone with its context rows (the
+    ancestors before it) packed in front (agpt_attn_plan_range, packed: the
+    batch returns the context rows' dK/dV share, for their owner batch to
+    add). Per batch: its inputs are made on the GPU, then W untimed and K
+    timed fwd+bwd steps with HIP events; the job's time is the sum over the
+    batches of their mean step, and value = node-tokens / that time."""
+    import gc
+    from concurrent.futures import ThreadPoolExecutor
+
+    import torch
+    from agpt_amd import trie as trie_mod
+    from agpt_amd.attention import TrieAttention, partition_starts, range_batches
+
+    dev = torch.device("cuda:0")
+    cfg = trie_mod.CONFIGS[args.workload]
+    H, hd = cfg["H"], cfg["hd"]
+    D = H * hd
+    dtype = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
+    b_in = 4 if cfg["dtype"] == "f32" else 2
+    batch_rows = args.batch_rows or (12 << 20)
+    n = max(2, int(cfg["n"] * args.scale))
+    log(f"{args.workload} full: corpus of {n} tokens")
+    t0 = time.time()
+    tok = trie_mod.markov_corpus(n, cfg["order"], cfg["vocab"], cfg["zipf"], cfg["seed"])
+    log(f"corpus in {time.time() - t0:.1f}s; building {cfg['vocab']} root-child subtrees on host threads")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    tok_emb = torch.randn(cfg["vocab"], D, generator=g, device=dev)
+    pos_emb = torch.randn(cfg["depth"], D, generator=g, device=dev)
+    ws = [torch.randn(D, D, generator=g, device=dev) * 0.02 for _ in range(3)]
+    hev = HipEvents()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    total_rows, total_ms, n_batches, sum_depth, max_rows = 0, 0.0, 0, 0, 0
+    k_sum = {}
+    desc = ""
+    pool = ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1))
+    futs = [pool.submit(trie_mod.build_radix_part, tok, cfg["depth"], x) for x in range(cfg["vocab"])]
+    t_job = time.time()
+    for x, fut in enumerate(futs):
+        tr = fut.result()
+        futs[x] = None
+        if tr.n_nodes == 0:
+            continue
+        ranges = range_batches(tr.n_nodes, batch_rows, partition_starts(tr.radix_head, tr.depth))
+        tk = torch.from_numpy(tr.token.astype(np.int64))
+        dp = torch.from_numpy((tr.depth - 1).astype(np.int64))
+        for a, b in ranges:
+            att = TrieAttention(H, hd, max_depth=cfg["depth"], dtype=dtype)
+            att.plan_range(tr.parent, a, b, packed=True)
+            ctx = []
+            r = int(tr.parent[a])
+            while r >= 0:
+                ctx.append(r)
+                r = int(tr.parent[r])
+            rows = torch.cat([torch.tensor(ctx[::-1], dtype=torch.int64), torch.arange(a, b)])
+            T = int(rows.shape[0])
+            ti, di = tk[rows].to(dev), dp[rows].to(dev)
+            qkv = []
+            for w in ws:
+                y = torch.empty(T, D, device=dev, dtype=dtype)
+                for s0 in range(0, T, 1 << 22):
+                    xe = tok_emb[ti[s0:s0 + (1 << 22)]] + pos_emb[di[s0:s0 + (1 << 22)]]
+                    y[s0:s0 + (1 << 22)] = (xe @ w).to(dtype)
+                qkv.append(y)
+            d_o = torch.empty(T, D, device=dev, dtype=dtype)
+            for s0 in range(0, T, 1 << 22):
+                d_o[s0:s0 + (1 << 22)] = torch.randn(min(1 << 22, T - s0), D, generator=g, device=dev).to(dtype)
+            o = torch.empty(T, D, device=dev, dtype=dtype)
+            lse = torch.empty(T, H, device=dev, dtype=torch.float32)
+            grads = tuple(torch.empty(T, D, device=dev, dtype=torch.float32) for _ in range(3))
+            q, k, v = qkv
+            for _ in range(args.warmup):
+                att.forward(q, k, v, out=o, lse=lse)
+                att.backward(q, k, v, o, lse, d_o, out=grads)
+            evs = [(hev.create(2), hev.create(5)) for _ in range(args.steps)]
+            steps = []
+            for fe, be in evs:
+                e0, e1 = hev.create(2)
+                hev.record(e0, stream)
+                att.forward(q, k, v, out=o, lse=lse, events=fe)
+                att.backward(q, k, v, o, lse, d_o, out=grads, events=be)
+                hev.record(e1, stream)
+                steps.append((e0, e1))
+            torch.cuda.synchronize()
+            ms = float(np.mean([hev.ms(e0, e1) for e0, e1 in steps]))
+            desc = att.describe()
+            for fe, be in evs:
+                for name, (i, j) in (("trie_fwd", (fe[0], fe[1])), ("trie_bwd_q", (be[0], be[1])),
+                                     ("trie_bwd_kv", (be[1], be[2])), ("trie_bwd_tail", (be[2], be[4]))):
+                    k_sum[name] = k_sum.get(name, 0.0) + hev.ms(i, j) / args.steps
+                hev.destroy(fe + be)
+            for e0, e1 in steps:
+                hev.destroy([e0, e1])
+            nb = b - a
+            total_rows += nb
+            total_ms += ms
+            sum_depth += int(tr.depth[a:b].astype(np.int64).sum())
+            max_rows = max(max_rows, nb)
+            n_batches += 1
+            att.close()
+            del q, k, v, d_o, o, lse, grads, qkv, ti, di, att
+            gc.collect()
+            torch.cuda.empty_cache()
+            if n_batches % 8 == 0:
+                log(f"{n_batches} batches, {total_rows} node-tokens, {total_ms:.0f} ms of steps")
+        del tr, tk, dp
+    pool.shutdown()
+    log(f"{n_batches} batches over {total_rows} node-tokens in {time.time() - t_job:.0f}s of job time")
+    bpt = bytes_per_token(D, H, b_in)
+    value = total_rows / (total_ms * 1e-3)
+    gbs = bpt["step"] * total_rows / (total_ms * 1e-3) / 1e9
+    out = {
+        "metric": FULL_METRIC, "value": value, "unit": "node-tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": total_ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": cfg["dtype"],
+        "data": "synthetic (seeded Markov corpus -> radix trie built per root child; random-init projections)",
+        "config": {"workload": f"{args.workload} at corpus scale {args.scale}, batch by batch",
+                   "node_tokens": total_rows, "sum_depth": sum_depth, "batches": n_batches,
+                   "largest_batch_rows": max_rows, "batch_rows": batch_rows, "d_model": D, "heads": H,
+                   "head_dim": hd, "kernel": desc,
+                   "timing": "per batch: inputs made on the GPU, then warmup and timed steps; "
+                             "ms_per_step = sum over batches of the mean step"},
+        "step_roofline": {"bytes_per_node_token": bpt["step"], "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS},
+        "kernel_ms_per_pass": k_sum,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def load_traffic(name: str):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
@@ -357,6 +497,9 @@ def main() -> int:
     ap.add_argument("--batch-rows", type=int, default=None,
                     help="attn path: batches of whole bigram partitions of at most this many rows, "
                          "one plan each, run in row order (default 0: every partition in one plan)")
+    ap.add_argument("--full", action="store_true",
+                    help="attn path: build the trie one root-child subtree at a time and run it batch "
+                         "by batch (for a corpus whose trie does not fit one GPU, e.g. C4 at --scale 1)")
     ap.add_argument("--cpu-rows", type=int, default=250_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -390,6 +533,13 @@ def main() -> int:
             args.scale = 1.0
         return bench_c3(args)
     cfg = trie_mod.CONFIGS[args.workload]
+    if args.full:
+        if args.scale is None:
+            args.scale = 1.0
+        if "chains" in cfg:
+            print("bench.py: --full needs a corpus workload (C1, C2, C4)", file=sys.stderr)
+            return 2
+        return bench_full(args)
     if args.scale is None:
         args.scale = cfg.get("one_gpu_scale", 1.0)
     H, hd = cfg["H"], cfg["hd"]

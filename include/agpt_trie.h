@@ -54,6 +54,15 @@ int agpt_trie_build(const int32_t* tokens, int64_t n, int max_depth,
 int agpt_trie_build_radix(const int32_t* tokens, int64_t n, int max_depth,
                           agpt_trie_handle* out);
 
+/* One root child's subtree of agpt_trie_build_radix's trie: the same
+ * pipeline over the starts whose first token is first_token only, so a
+ * corpus whose whole trie does not fit is built (and batched) one root
+ * child at a time; the subtrees in token order are the whole trie's rows
+ * in order (the reference's per-subtree files, streaming_radix_builder.cr:
+ * 388-426, hold the same subtrees). */
+int agpt_trie_build_radix_part(const int32_t* tokens, int64_t n, int max_depth,
+                               int32_t first_token, agpt_trie_handle* out);
+
 /* `n_chains` independent unary chains of `chain_len` nodes each (never
  * merged); chain c takes tokens[c*chain_len ...]. The dense-causal control. */
 int agpt_trie_build_chains(const int32_t* tokens, int64_t n_chains, int chain_len,
