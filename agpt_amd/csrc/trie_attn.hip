@@ -1198,9 +1198,11 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
     // workgroups without a chunk.
     int cus = 256;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
-    // The deep key side's units are (chunk, head): ~8 per CU.
+    // The deep key side's units are (chunk, head): ~8 per CU, and chunks up
+    // to 48 tiles (fewer chunk partials: C4 83.0 -> 81.6 ms).
     const int64_t per_claim = h->deep_carry ? static_cast<int64_t>(n_tiles) * h->cfg.n_heads : n_tiles;
-    const int dflt = static_cast<int>(std::min<int64_t>(24, std::max<int64_t>(1, per_claim / (8 * std::max(cus, 1)))));
+    const int cap = h->deep_carry ? 48 : 24;
+    const int dflt = static_cast<int>(std::min<int64_t>(cap, std::max<int64_t>(1, per_claim / (8 * std::max(cus, 1)))));
     h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", dflt));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
     // Chunks of one tile would carry nothing: the per-tile partials serve.
