@@ -57,6 +57,11 @@ constexpr int kTile = 64;
 constexpr int kThreads = 256;
 constexpr int kChunk = 64;  // keys per streamed chunk: one 16-key block per wave-sized step
 constexpr int kKeyCap = (kMaxDepth - 1 + kTile + kChunk - 1) / kChunk * kChunk;
+// Key blocks per wave of the carry key side with its sums in registers:
+// every key slot of a tile of a plan to depth kRegDepth (prefix_cap + 64
+// keys in 4 kRegIters blocks of 16).
+constexpr int kRegIters = 3;
+constexpr int kRegDepth = 4 * kRegIters * 16 - kTile;  // 128
 // Running max of a query before it has seen a key: finite, so that exp2 of
 // a masked score (-inf) minus it is 0, never NaN.
 constexpr float kNoMax = -1.0e30f;
@@ -181,6 +186,14 @@ __device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t,
   return w;
 }
 
+// Waits until every vector-memory load of this wave has returned (vmcnt 0,
+// expcnt and lgkmcnt left alone). Placed after the loads of a unit's
+// register slices, before its step loop: the compiler's wait bookkeeping
+// then knows the slices are in at the loop head. Without it the first use
+// of a slice inside the loop carries a vmcnt(0) wait on every pass, which
+// also waits for the key-ring prefetch issued at the top of that pass.
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 // Whether query block i (rows 16i .. 16i+15) has a live pair with key block b.
 __device__ __forceinline__ bool block_live(const Tables& tb, int b, int i) {
   return kBlk * i < uniform(tb.bhi[b]) && kBlk * i + kBlk > uniform(tb.blo[b]);
@@ -275,11 +288,13 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
     Slice<Tin, KD> qf, qn;
     qf.load(Q + qbase + h0 * HD);
     ring.load(tb, K, V, D, h0, 0);
+    wait_loads();
     ring.store(0);
     __syncthreads();
     float m = kNoMax, l = 0.0f;
     f4 o[MT];
     const int nsteps = hpu * w.nch;
+    __builtin_assume(nsteps > 0);  // no guard block for the slice loads to sink into
     for (int st = 0; st < nsteps; ++st) {
       const int hl = st / w.nch;
       const int h = h0 + hl;
@@ -406,18 +421,22 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     const int64_t qrow = w.s + min(q, w.ntile - 1);
     const int64_t qbase = qrow * D + KD * g;
     // This lane's query of head h: Q, dO slices, lse (and O for δ, fp32).
+    // lse is taken to log2 units where it is first used, not where it is
+    // fetched, so that the next head's fetch does not wait for its load.
     Slice<Tin, KD> qf, gf, qn, gn;
     float l2, l2n = 0.0f, dl = 0.0f;
     float ov[kDeltaFromO ? KD : 1], on[kDeltaFromO ? KD : 1];
     auto fetch = [&](int h, Slice<Tin, KD>& a, Slice<Tin, KD>& b, float& le, float (&oo)[kDeltaFromO ? KD : 1]) {
       a.load(Q + qbase + h * HD);
       b.load(dO + qbase + h * HD);
-      le = lse[qrow * H + h] * kLog2e;
+      le = lse[qrow * H + h];
       if constexpr (kDeltaFromO) load_vec<KD>(reinterpret_cast<const float*>(O) + qbase + h * HD, oo);
     };
     fetch(h0, qf, gf, l2, ov);
     const int qdep = pl.depth[qrow];
     ring.load(tb, K, V, D, h0, 0);
+    wait_loads();
+    l2 *= kLog2e;
     ring.store(0);
     __syncthreads();
     // Scores and dO·v of key block bl of the buffer: register r holds key
@@ -441,6 +460,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     float acc = 0.0f;
     const int per = NP * w.nch;  // steps per head
     const int nsteps = hpu * per;
+    __builtin_assume(nsteps > 0);
     for (int st = 0; st < nsteps; ++st) {
       const int hl = st / per;
       const int h = h0 + hl;
@@ -513,7 +533,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         }
         qf = qn;
         gf = gn;
-        l2 = l2n;
+        l2 = l2n * kLog2e;
         if constexpr (kDeltaFromO) {
 #pragma unroll
           for (int j = 0; j < KD; ++j) ov[j] = on[j];
@@ -734,21 +754,30 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 // the workgroup walks the chunk's tiles in order. The keys a tile leaves
 // open (subtree not finished) are exactly the next tile's prefix, one per
 // depth, so the sums of the current path's keys are carried from tile to
-// tile by depth instead of being left as per-tile partials: in this
-// workgroup's carry rows Cs [parity][depth][dK, dV][HD] (global memory,
-// read and written only by this workgroup; a tile reads the rows of its
-// parity and writes the next tile's into the other, with a barrier between
-// tiles). A prefix key the next tile still sees adds its tile sum to the
-// carry; one it does not see is finished: to dK/dV (a key first seen in the
-// chunk whose subtree ended), to the chunk partial E[chunk][depth] (a key
-// from before the chunk), or at the chunk's last tile to F[chunk][depth]
-// (a key of this chunk still open). Open tile rows start their depth's
-// sum. agpt_blk::bwd_carry_kernel then finishes the keys whose sums cross
-// chunks (F of their chunk plus E of the later chunks, in chunk order).
+// tile by depth instead of being left as per-tile partials. A prefix key
+// sits at the same key slot (depth - 1) in every tile that sees it, and so
+// does a tile row that continues a chain from the tile's first row (row r
+// at slot A + r = depth - 1; in a deep trie most tiles lie inside such
+// chains). With NI > 0 (plans to depth kRegDepth: every key slot of a tile
+// in 4 NI blocks) the wave that owns a key block keeps the block's sums in
+// registers, as the accumulators of its matrix products, from one tile to
+// the next: a key that stays in its slot never leaves them. The others go
+// through this workgroup's carry rows Cs [parity][depth][dK, dV][HD]
+// (global memory, read and written only by this workgroup; a tile reads
+// the rows of its parity and writes the next tile's into the other, with a
+// barrier between tiles): open tile rows whose slot changes, and with
+// NI == 0 every carried sum. A prefix key the next tile still sees adds its
+// tile sum to the carry; one it does not see is finished: to dK/dV (a key
+// first seen in the chunk whose subtree ended), to the chunk partial
+// E[chunk][depth] (a key from before the chunk), or at the chunk's last
+// tile to F[chunk][depth] (a key of this chunk still open). Open tile rows
+// start their depth's sum. agpt_blk::bwd_carry_kernel then finishes the
+// keys whose sums cross chunks (F of their chunk plus E of the later
+// chunks, in chunk order).
 // E, F: [n_chunks][P][2][D].
 // ---------------------------------------------------------------------------
-template <int HD, typename Tin, typename PlanT, typename RopeT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void bwd_kv_carry_kernel(
+template <int HD, typename Tin, int NI, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0 ? 2 : 3))) void bwd_kv_carry_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
     float* __restrict__ dK, float* __restrict__ dV, float* __restrict__ E, float* __restrict__ F,
@@ -807,6 +836,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
       }
     };
     fetch_rows(t0);
+    // Carry registers: the sums of key block wave + 4i (i < NI), one lane
+    // column per key slot; zero in the lanes of keys that do not continue.
+    constexpr int NR = NI > 0 ? NI : 1;
+    f4 ck[NR][MT], cv[NR][MT];
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        ck[i][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        cv[i][j] = ck[i][j];
+      }
+    int a_prev = 0;  // the previous tile's prefix length
     for (int t = t0; t < t1; ++t) {
       const bool first = t == t0;
       const bool last = t + 1 == t1;
@@ -836,18 +877,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
         a.load(K + row * D + h * HD + KD * g);
         v.load(V + row * D + h * HD + KD * g);
       };
-      if (wave < nkb) fetch(wave, nkf, nvf);
-      for (int b = wave; b < nkb; b += 4) {
+      // Key block b, accumulated into dk, dv: with reg, this wave's carry
+      // registers of the block (the carried sums of its prefix keys, zero in
+      // every other lane), which keep the sums that continue into the next
+      // tile and are zero again in every other lane at the end.
+      auto key_block = [&](int b, f4 (&dk)[MT], f4 (&dv)[MT], bool reg) {
         kf = nkf;
         vf = nvf;
         if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
         kf.scale(qscale);
-        f4 dk[MT], dv[MT];
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-          dv[j] = dk[j];
-        }
         const int key = kBlk * b + c;
         const int iv = tb.kint[key];
         const int i0 = uniform(tb.blo[b]) / kBlk;
@@ -934,10 +972,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
             store_vec<4>(dV + a * D + h * HD + d0, gv[j]);
           }
         };
+        bool keep = false;  // the lane's key sum continues in the carry registers
         if (key < A) {
           const int d = key;  // prefix entry d = depth d+1
           const int e = tb.pend[d];
-          if (!first) {
+          // The sum so far is in the registers when the key had this key
+          // slot in the previous tile too: a key of its prefix, or one of its
+          // rows that continued a chain from its first row (row r' at slot
+          // a_prev + r' = its depth - 1). Else it is in the carry row.
+          const int pr = tb.krow[key] - (s - kTile);  // row in the previous tile, < 0: its prefix
+          if (!first && (!reg || (pr >= 0 && a_prev + pr != d))) {
             const float* cp = slot(cur, d);
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
@@ -952,18 +996,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
             }
           }
           const bool cont = !last && e > s + ntile;  // the next tile of the chunk sees it
-          if (cont) put(slot(cur ^ 1, d), HD);
-          else if (tb.krow[key] < s_first) chunk_part(E, d);  // a key from before the chunk
-          else if (e > s + ntile) chunk_part(F, d);           // the chunk ends, the key's subtree does not
-          else finish(tb.krow[key], d + 1);
+          if (cont) {
+            if (reg) keep = true;
+            else put(slot(cur ^ 1, d), HD);
+          } else if (tb.krow[key] < s_first) {
+            chunk_part(E, d);  // a key from before the chunk
+          } else if (e > s + ntile) {
+            chunk_part(F, d);  // the chunk ends, the key's subtree does not
+          } else {
+            finish(tb.krow[key], d + 1);
+          }
         } else if (key < A + ntile) {
           const int r = key - A;
           const int64_t a = static_cast<int64_t>(s) + r;
           if (tb.rend[r] <= s + ntile) finish(a, tb.rdep[r]);
           else if (last) chunk_part(F, tb.rdep[r] - 1);
+          else if (reg && tb.rdep[r] - 1 == key) keep = true;  // the next tile's prefix entry in this slot
           else put(slot(cur ^ 1, tb.rdep[r] - 1), HD);  // the next tile's prefix entry at its depth
         }
+        if (reg) {
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+              dk[j][x] = keep ? gk[j][x] : 0.0f;
+              dv[j][x] = keep ? gv[j][x] : 0.0f;
+            }
+        }
+      };
+      if (wave < nkb) fetch(wave, nkf, nvf);
+      if constexpr (NI > 0) {  // every key block of the tile in registers
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if (wave + 4 * i < nkb) key_block(wave + 4 * i, ck[i], cv[i], true);
+      } else {
+        for (int b = wave; b < nkb; b += 4) {
+          f4 dk[MT], dv[MT];
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            dv[j] = dk[j];
+          }
+          key_block(b, dk, dv, false);
+        }
       }
+      a_prev = A;
       __syncthreads();  // the tile's staged rows, tables and carry rows are done with
     }
     u = uniform(tb.next[par]);
