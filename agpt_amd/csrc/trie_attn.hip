@@ -1652,13 +1652,14 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                          static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, hpu, scale);
       pm.mark(1);
       if (h->deep_carry) {
-        // Key slots of a tile: prefix_cap + 64; with all of them in 4 NI
-        // blocks of 16 the sums stay in registers.
-        const bool in_regs = agpt_blk::prefix_cap(h->max_depth) + agpt_deep::kTile <=
-                                 64 * agpt_deep::kRegIters &&
-                             env_int("AGPT_ATTN_REGCARRY", 1) != 0;
-        auto fc = in_regs ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegIters, PlanDev, RopeArgs>
-                          : agpt_deep::bwd_kv_carry_kernel<HD, Tin, 0, PlanDev, RopeArgs>;
+        // Key slots of a tile: prefix_cap + 64. With all of them in 4 NI
+        // blocks of 16 every sum stays in registers; deeper plans keep the
+        // first 4 kRegItersDeep blocks there.
+        const bool regs = env_int("AGPT_ATTN_REGCARRY", 1) != 0;
+        const bool all_regs = agpt_blk::prefix_cap(h->max_depth) + agpt_deep::kTile <= 64 * agpt_deep::kRegIters;
+        auto fc = !regs      ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, 0, PlanDev, RopeArgs>
+                  : all_regs ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegIters, PlanDev, RopeArgs>
+                             : agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegItersDeep, PlanDev, RopeArgs>;
         set_lds(fc, h->kv_lds);
         int cus = 256;
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);

@@ -59,9 +59,11 @@ constexpr int kChunk = 64;  // keys per streamed chunk: one 16-key block per wav
 constexpr int kKeyCap = (kMaxDepth - 1 + kTile + kChunk - 1) / kChunk * kChunk;
 // Key blocks per wave of the carry key side with its sums in registers:
 // every key slot of a tile of a plan to depth kRegDepth (prefix_cap + 64
-// keys in 4 kRegIters blocks of 16).
+// keys in 4 kRegIters blocks of 16); deeper plans keep kRegItersDeep
+// blocks per wave (key slots 0 .. 16 * 4 * kRegItersDeep - 1) in registers.
 constexpr int kRegIters = 3;
 constexpr int kRegDepth = 4 * kRegIters * 16 - kTile;  // 128
+constexpr int kRegItersDeep = 2;
 // Running max of a query before it has seen a key: finite, so that exp2 of
 // a masked score (-inf) minus it is 0, never NaN.
 constexpr float kNoMax = -1.0e30f;
@@ -758,15 +760,17 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 // sits at the same key slot (depth - 1) in every tile that sees it, and so
 // does a tile row that continues a chain from the tile's first row (row r
 // at slot A + r = depth - 1; in a deep trie most tiles lie inside such
-// chains). With NI > 0 (plans to depth kRegDepth: every key slot of a tile
-// in 4 NI blocks) the wave that owns a key block keeps the block's sums in
-// registers, as the accumulators of its matrix products, from one tile to
-// the next: a key that stays in its slot never leaves them. The others go
-// through this workgroup's carry rows Cs [parity][depth][dK, dV][HD]
-// (global memory, read and written only by this workgroup; a tile reads
-// the rows of its parity and writes the next tile's into the other, with a
-// barrier between tiles): open tile rows whose slot changes, and with
-// NI == 0 every carried sum. A prefix key the next tile still sees adds its
+// chains). With NI > 0 the wave that owns a key block keeps the block's
+// sums in registers, as the accumulators of its matrix products, from one
+// tile to the next: a key that stays in its slot never leaves them. NI ==
+// kRegIters (plans to depth kRegDepth) covers every key slot of a tile;
+// NI == kRegItersDeep covers the first 16 * 4 NI slots of deeper plans.
+// The other sums go through this workgroup's carry rows Cs
+// [parity][depth][dK, dV][HD] (global memory, read and written only by this
+// workgroup; a tile reads the rows of its parity and writes the next
+// tile's into the other, with a barrier between tiles): open tile rows
+// whose slot changes, keys past the register slots, and with NI == 0 every
+// carried sum. A prefix key the next tile still sees adds its
 // tile sum to the carry; one it does not see is finished: to dK/dV (a key
 // first seen in the chunk whose subtree ended), to the chunk partial
 // E[chunk][depth] (a key from before the chunk), or at the chunk's last
@@ -1025,10 +1029,35 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         }
       };
       if (wave < nkb) fetch(wave, nkf, nvf);
-      if constexpr (NI > 0) {  // every key block of the tile in registers
+      if constexpr (NI == kRegIters) {  // every key block of the tile in registers
 #pragma unroll
         for (int i = 0; i < NI; ++i)
           if (wave + 4 * i < nkb) key_block(wave + 4 * i, ck[i], cv[i], true);
+      } else if constexpr (NI > 0) {
+        // Deeper plans: the wave's first NI blocks in registers (selected by
+        // the block's turn i, a uniform value), the blocks after them through
+        // the carry rows.
+        for (int b = wave, i = 0; b < nkb; b += 4, ++i) {
+          f4 dk[MT], dv[MT];
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            dv[j] = dk[j];
+#pragma unroll
+            for (int x = 0; x < NI; ++x) {
+              dk[j] = i == x ? ck[x][j] : dk[j];
+              dv[j] = i == x ? cv[x][j] : dv[j];
+            }
+          }
+          key_block(b, dk, dv, i < NI);
+#pragma unroll
+          for (int x = 0; x < NI; ++x)
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              ck[x][j] = i == x ? dk[j] : ck[x][j];
+              cv[x][j] = i == x ? dv[j] : cv[x][j];
+            }
+        }
       } else {
         for (int b = wave; b < nkb; b += 4) {
           f4 dk[MT], dv[MT];
