@@ -84,6 +84,9 @@ struct PlanDev {
   int32_t chunk_tiles;
   int32_t n_chunks;
   int32_t n_prefix;  // pref_off[n_tiles]
+  // Deep query side: the tile of claim i is tile_order[i] (tiles of more key
+  // chunks first, DFS order within), or tile i when null.
+  const int32_t* tile_order;
 };
 
 // ---------------------------------------------------------------------------
@@ -667,6 +670,7 @@ struct agpt_attn_s {
   int32_t* d_k_items = nullptr;
   int32_t* d_q_item_off = nullptr;
   int32_t* d_k_item_off = nullptr;
+  int32_t* d_tile_order = nullptr;  // deep query side: claim order of the tiles (null: tile order)
   // kernel family chosen at plan time: 0 = global-memory walk (any shape),
   // 5 = streaming chain-group walk (trie_fast.h), 6 = streaming block-sparse
   // 16x16 matrix tiles (trie_block.h)
@@ -702,7 +706,8 @@ void free_plan(agpt_attn_s* h) {
   // dropped, not freed.
   const bool own = !h->static_plan;
   int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
-                    &h->d_prefix,   &h->d_pref_end,    &h->d_q_item_off,  &h->d_k_item_off};
+                    &h->d_prefix,   &h->d_pref_end,    &h->d_q_item_off,  &h->d_k_item_off,
+                    &h->d_tile_order};
   for (auto p : ip)
     if (*p) {
       if (own) (void)hipFree(*p);
@@ -798,6 +803,7 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.chunk_tiles = h->chunk_tiles;
   p.n_chunks = h->n_chunks_sched;
   p.n_prefix = static_cast<int32_t>(h->n_prefix_rows);
+  p.tile_order = h->d_tile_order;
   return p;
 }
 
@@ -1193,6 +1199,25 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
   }
   if (h->variant == 6) {
     if ((rc = ar.get(reinterpret_cast<void**>(&h->d_sched), kSchedBytes)) != AGPT_OK) return rc;
+    // Deep query side with few units per workgroup (plans of < 16 tiles per
+    // CU, one head per unit): tiles of more key chunks are claimed first, so
+    // that the last claims of the launch are the short ones. Larger plans
+    // keep the tile order, in which neighbouring claims share their prefix.
+    {
+      int cus0 = 256;
+      (void)hipDeviceGetAttribute(&cus0, hipDeviceAttributeMultiprocessorCount, h->device);
+      if (h->deep && env_int("AGPT_ATTN_LPT", n_tiles < 16 * cus0 ? 1 : 0) != 0) {
+        std::vector<int32_t> order(n_tiles);
+        std::vector<int32_t> nch(n_tiles);
+        for (int32_t t = 0; t < n_tiles; ++t) {
+          order[t] = t;
+          const int64_t nk = (pref_off[t + 1] - pref_off[t]) + std::min<int64_t>(tile, n - int64_t(t) * tile);
+          nch[t] = static_cast<int32_t>((nk + agpt_deep::kChunk - 1) / agpt_deep::kChunk);
+        }
+        std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return nch[a] > nch[b]; });
+        if ((rc = upload(ar, &h->d_tile_order, order)) != AGPT_OK) return rc;
+      }
+    }
     // Up to 24 tiles per claim (the carry's reach), but at least ~8 chunks
     // per CU: a plan of few tiles (C5: 2048) would otherwise leave most
     // workgroups without a chunk.

@@ -196,6 +196,12 @@ __device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t,
 // also waits for the key-ring prefetch issued at the top of that pass.
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+// The tile of claim i of a query-side or per-tile key-side kernel.
+template <typename PlanT>
+__device__ __forceinline__ int tile_of(const PlanT& pl, int i) {
+  return pl.tile_order ? pl.tile_order[i] : i;
+}
+
 // Whether query block i (rows 16i .. 16i+15) has a live pair with key block b.
 __device__ __forceinline__ bool block_live(const Tables& tb, int b, int i) {
   return kBlk * i < uniform(tb.bhi[b]) && kBlk * i + kBlk > uniform(tb.blo[b]);
@@ -284,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
     const int h0 = (u % ngr) * hpu;
-    const Unit w = build_tables(pl, tb, u / ngr, false);
+    const Unit w = build_tables(pl, tb, tile_of(pl, u / ngr), false);
     const int q = kBlk * wave + c;  // this lane's query row in the tile
     const int64_t qbase = (w.s + min(q, w.ntile - 1)) * static_cast<int64_t>(D) + KD * g;
     Slice<Tin, KD> qf, qn;
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
     const int h0 = (u % ngr) * hpu;
-    const Unit w = build_tables(pl, tb, u / ngr, false);
+    const Unit w = build_tables(pl, tb, tile_of(pl, u / ngr), false);
     const int q = kBlk * wave + c;
     const int64_t qrow = w.s + min(q, w.ntile - 1);
     const int64_t qbase = qrow * D + KD * g;
@@ -590,7 +596,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * ngr;
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
-    const int t = u / ngr;
+    const int t = tile_of(pl, u / ngr);
     const int h0 = (u % ngr) * hpu;
     const int h1 = h0 + hpu;
     const int s = t * kTile;
