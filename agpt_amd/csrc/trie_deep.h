@@ -124,8 +124,8 @@ __device__ __forceinline__ f4 mfma_tr_bf16(const bf16_t* p, uint2 wb, f4 acc) {
 struct alignas(16) Tables {
   alignas(16) int32_t kint[kKeyCap];  // per key: lo | len << 16, the tile rows [lo, lo + len) that see it
   int32_t krow[kKeyCap];  // per key: its row in the tensors (negative: a context row of a range plan)
-  int32_t blo[kKeyCap / kBlk];  // per key block: least lo of its live keys (kTile if none)
-  int32_t bhi[kKeyCap / kBlk];  // per key block: greatest lo + len
+  alignas(16) int32_t blo[kKeyCap / kBlk];  // per key block: least lo of its live keys (kTile if none)
+  alignas(16) int32_t bhi[kKeyCap / kBlk];  // per key block: greatest lo + len
   int32_t pend[kKeyCap];  // per prefix key: its subtree end (rows of the plan)
   int32_t rdep[kTile];   // depth of the tile rows
   int32_t rend[kTile];   // subtree end of the tile rows
@@ -200,6 +200,20 @@ __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0f70
 template <typename PlanT>
 __device__ __forceinline__ int tile_of(const PlanT& pl, int i) {
   return pl.tile_order ? pl.tile_order[i] : i;
+}
+
+// The key blocks of chunk ch with a live pair for query block i (rows 16i ..
+// 16i+15): bit bl for key block 4 ch + bl, a wave-uniform value. One pair of
+// 16-byte reads per chunk, and a scalar bit test per block, where a test per
+// block would make two dependent LDS round trips and an exec-mask branch.
+static_assert(kChunk / kBlk == 4, "four key blocks per chunk");
+__device__ __forceinline__ int chunk_live(const Tables& tb, int ch, int i) {
+  const int4 lo = *reinterpret_cast<const int4*>(tb.blo + 4 * ch);
+  const int4 hi = *reinterpret_cast<const int4*>(tb.bhi + 4 * ch);
+  const int r0 = kBlk * i, r1 = r0 + kBlk;
+  const int m = static_cast<int>(r0 < hi.x && r1 > lo.x) | static_cast<int>(r0 < hi.y && r1 > lo.y) << 1 |
+                static_cast<int>(r0 < hi.z && r1 > lo.z) << 2 | static_cast<int>(r0 < hi.w && r1 > lo.w) << 3;
+  return uniform(m);
 }
 
 // Whether query block i (rows 16i .. 16i+15) has a live pair with key block b.
@@ -323,10 +337,11 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
       if (last && hl + 1 < hpu) qn.load(Q + qbase + (h + 1) * HD);
       const Tin* Ks = ring.ks(st & 1);
       const Tin* Vs = ring.vs(st & 1);
+      const int lmask = chunk_live(tb, ch, wave);
 #pragma unroll
       for (int bl = 0; bl < kChunk / kBlk; ++bl) {
         const int b = ch * (kChunk / kBlk) + bl;
-        if (!block_live(tb, b, wave)) continue;
+        if (!((lmask >> bl) & 1)) continue;
         const int4 iv = *reinterpret_cast<const int4*>(tb.kint + kBlk * b + 4 * g);
         const bool live[4] = {in_interval(q, iv.x), in_interval(q, iv.y), in_interval(q, iv.z),
                               in_interval(q, iv.w)};
@@ -496,10 +511,11 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       if (last && hl + 1 < hpu) fetch(h + 1, qn, gn, l2n, on);
       const Tin* Ks = ring.ks(st & 1);
       const Tin* Vs = ring.vs(st & 1);
+      const int lmask = chunk_live(tb, ch, wave);
 #pragma unroll
       for (int bl = 0; bl < kChunk / kBlk; ++bl) {
         const int b = ch * (kChunk / kBlk) + bl;
-        if (!block_live(tb, b, wave)) continue;
+        if (!((lmask >> bl) & 1)) continue;
         bool live[4];
         mask(b, live);
         f4 sv, tv;
