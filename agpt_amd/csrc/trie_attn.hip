@@ -982,8 +982,8 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     h->deep = hd == 64 && hg == 1 && env_int("AGPT_ATTN_DEEP", 1) != 0;
     h->deep_carry = h->deep && env_int("AGPT_ATTN_CARRY", 1) != 0;
     if (h->deep) {
-      h->fwd_lds = agpt_deep::ring_lds_bytes(hd, elem, false);
-      h->bq_lds = agpt_deep::ring_lds_bytes(hd, elem, true);
+      h->fwd_lds = agpt_deep::ring_lds_bytes(hd, elem);
+      h->bq_lds = agpt_deep::ring_lds_bytes(hd, elem);
       h->kv_lds = agpt_deep::rows_lds_bytes(hd, elem);
     }
     const bool ok = (hd == 16 || hd == 32 || (hd == 64 && hg == 1)) && H % hg == 0 &&

@@ -19,7 +19,9 @@
 //     straight into registers, and walks the query blocks that see them.
 //
 // LDS per workgroup is 37 KB (bf16 ring) or 18 KB (bf16 staged rows)
-// instead of 80-110 KB. The block pairs, masks and lane layouts are those of
+// instead of 80-110 KB; every tile in it is row-major, and the bf16
+// operands that a product needs transposed are read with ds_read_b64_tr_b16
+// (read_tr). The block pairs, masks and lane layouts are those of
 // trie_block.h: 16x16 tiles on the matrix instructions, and per key the
 // interval of tile rows that see it (in DFS preorder the rows below a key
 // are consecutive). The key side leaves the partials bwd_kv_kernel leaves
@@ -69,53 +71,39 @@ constexpr int kRegItersDeep = 2;
 constexpr float kNoMax = -1.0e30f;
 
 __host__ __device__ constexpr int row_stride(int hd, int elem) { return hd + 16 / elem; }
-// bf16 operands of the second products (P·V, dS·K, P^T·dO, dS^T·Q) are
-// also staged transposed, [dim][row] with rows 64 + 4 apart: four
-// consecutive rows of one dim are then one 8-byte LDS read, the operand
-// slot of v_mfma_f32_16x16x16_bf16, instead of four 2-byte reads and two
-// packing instructions.
-constexpr int kTStride = kTile + 4;
-// Query-side ring layouts: K rows and V rows (fp32); K rows and V^T
-// (bf16 forward); K rows, V rows and K^T (bf16 dQ).
-constexpr int kRingKV = 0, kRingKVt = 1, kRingKVKt = 2;
-// (The dQ kernel keeps K and V rows: a third tile in the ring costs more
-// in workgroups per CU than its 8-byte reads save.)
-__host__ __device__ constexpr int ring_layout(int elem, bool dq) { return elem == 4 || dq ? kRingKV : kRingKVt; }
-__host__ __device__ constexpr size_t ring_buf_elems(int hd, int elem, int layout) {
-  return static_cast<size_t>(kChunk) * row_stride(hd, elem) +
-         (layout == kRingKVt ? static_cast<size_t>(hd) * kTStride : static_cast<size_t>(kChunk) * row_stride(hd, elem)) +
-         (layout == kRingKVKt ? static_cast<size_t>(hd) * kTStride : 0);
+// One buffer of the query side's key ring: K rows, then V rows [kChunk][WS].
+// (bf16 operands of the second products, P·V and dS·K, are read from the
+// row-major tiles with read_tr.)
+__host__ __device__ constexpr size_t ring_buf_elems(int hd, int elem) {
+  return 2 * static_cast<size_t>(kChunk) * row_stride(hd, elem);
 }
 // Dynamic LDS: the query-side ring (two buffers) or the key side's staged
-// rows [Q, dO][kTile][WS] (bf16: and Q^T, dO^T [HD][kTStride]).
-__host__ __device__ constexpr size_t ring_lds_bytes(int hd, int elem, bool dq) {
-  return 2 * ring_buf_elems(hd, elem, ring_layout(elem, dq)) * elem;
+// rows [Q, dO][kTile][WS] (bf16 operands of P^T·dO and dS^T·Q read from
+// them transposed, read_tr).
+__host__ __device__ constexpr size_t ring_lds_bytes(int hd, int elem) {
+  return 2 * ring_buf_elems(hd, elem) * elem;
 }
 __host__ __device__ constexpr size_t rows_lds_bytes(int hd, int elem) {
-  return (static_cast<size_t>(2 * kTile) * row_stride(hd, elem) + (elem == 2 ? 2 * static_cast<size_t>(hd) * kTStride : 0)) *
-         elem;
+  return static_cast<size_t>(2 * kTile) * row_stride(hd, elem) * elem;
 }
 
-// Stores 8 consecutive dims (d0 ..) of row `col` into a transposed bf16 tile.
-__device__ __forceinline__ void store_tr(bf16_t* t, int col, int d0, u4 x) {
-  uint16_t* p = reinterpret_cast<uint16_t*>(t) + d0 * kTStride + col;
-  p[0] = static_cast<uint16_t>(x.x);
-  p[kTStride] = static_cast<uint16_t>(x.x >> 16);
-  p[2 * kTStride] = static_cast<uint16_t>(x.y);
-  p[3 * kTStride] = static_cast<uint16_t>(x.y >> 16);
-  p[4 * kTStride] = static_cast<uint16_t>(x.z);
-  p[5 * kTStride] = static_cast<uint16_t>(x.z >> 16);
-  p[6 * kTStride] = static_cast<uint16_t>(x.w);
-  p[7 * kTStride] = static_cast<uint16_t>(x.w >> 16);
+// The A operand of v_mfma_f32_16x16x16_bf16 for the 16 x 16 block
+// M[m][k] = R[k0 + k][m0 + m] of a row-major bf16 tile R in LDS (row stride
+// ws elements, 8-byte aligned rows): lane (l = lane % 16, g = lane / 16)
+// needs R[k0 + 4g + i][m0 + l], i = 0 .. 3. ds_read_b64_tr_b16 transposes
+// within each 16-lane group: lane l receives element l % 4 of the 8 bytes
+// read by lane 4i + l / 4 of its group, so lane l reads
+// R[k0 + 4g + l / 4][m0 + 4 (l % 4) ..]. One read per operand where a gather
+// of four rows takes four 2-byte reads and two packing instructions.
+__device__ __forceinline__ agpt_blk::bf16x4_bits read_tr(const bf16_t* R, int ws, int k0, int m0, int lane) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  const int l = lane & 15, g = lane >> 4;
+  const bf16_t* p = R + (k0 + 4 * g + (l >> 2)) * ws + m0 + 4 * (l & 3);
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p));
+  return __builtin_bit_cast(agpt_blk::bf16x4_bits, v);
 }
-
-// One 16-deep bf16 step whose A operand is four consecutive rows of one dim
-// of a transposed tile (p = &T[dim][row 4g]) and whose B operand is this
-// lane's four weights (pack_bf16).
-__device__ __forceinline__ f4 mfma_tr_bf16(const bf16_t* p, uint2 wb, f4 acc) {
-  const uint2 a = *reinterpret_cast<const uint2*>(p);
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(agpt_blk::bf16x4_bits, a),
-                                                    __builtin_bit_cast(agpt_blk::bf16x4_bits, wb), acc, 0, 0, 0);
+__device__ __forceinline__ f4 mfma_a_bf16(agpt_blk::bf16x4_bits a, uint2 wb, f4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(agpt_blk::bf16x4_bits, wb), acc, 0, 0, 0);
 }
 
 // The tile's key list and row tables. Keys 0 .. A-1 are the prefix rows
@@ -223,22 +211,20 @@ __device__ __forceinline__ bool block_live(const Tables& tb, int b, int i) {
 
 // The double-buffered key ring of the query side: chunk c of the tile's key
 // list, K and V slices of one head; per buffer K rows [kChunk][WS], then V
-// rows [kChunk][WS] or V^T [HD][kTStride], then (kRingKVKt) K^T.
-template <int HD, typename Tin, int kLayout>
+// rows [kChunk][WS].
+template <int HD, typename Tin>
 struct KeyRing {
   static constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));  // elements per 16-byte piece
   static constexpr int WS = row_stride(HD, sizeof(Tin));
   static constexpr int PIECES = HD / EPC;    // pieces per key slice
   static constexpr int PER_T = kChunk * PIECES;  // pieces per tensor per chunk
   static constexpr int PER = 2 * PER_T / kThreads;
-  static constexpr int BUF = static_cast<int>(ring_buf_elems(HD, sizeof(Tin), kLayout));
+  static constexpr int BUF = static_cast<int>(ring_buf_elems(HD, sizeof(Tin)));
   static_assert(PER_T % kThreads == 0, "whole rounds of the workgroup per tensor");
-  static_assert(kLayout == kRingKV || sizeof(Tin) == 2, "transposed tiles are bf16");
   Tin* base;
   u4 r[PER];
   __device__ __forceinline__ Tin* ks(int buf) const { return base + buf * BUF; }
-  __device__ __forceinline__ Tin* vs(int buf) const { return base + buf * BUF + kChunk * WS; }  // V rows or V^T
-  __device__ __forceinline__ Tin* kt(int buf) const { return base + buf * BUF + 2 * kChunk * WS; }
+  __device__ __forceinline__ Tin* vs(int buf) const { return base + buf * BUF + kChunk * WS; }
   __device__ __forceinline__ void load(const Tables& tb, const Tin* K, const Tin* V, int D, int h, int c) {
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -255,15 +241,7 @@ struct KeyRing {
       const int ten = k * kThreads / PER_T;
       const int j = static_cast<int>(threadIdx.x) + k * kThreads - ten * PER_T;
       const int key = j / PIECES, d0 = (j % PIECES) * EPC;
-      if constexpr (kLayout == kRingKVt) {
-        if (ten) store_tr(vs(buf), key, d0, r[k]);
-        else *reinterpret_cast<u4*>(ks(buf) + key * WS + d0) = r[k];
-      } else {
-        *reinterpret_cast<u4*>((ten ? vs(buf) : ks(buf)) + key * WS + d0) = r[k];
-        if constexpr (kLayout == kRingKVKt) {
-          if (!ten) store_tr(kt(buf), key, d0, r[k]);
-        }
-      }
+      *reinterpret_cast<u4*>((ten ? vs(buf) : ks(buf)) + key * WS + d0) = r[k];
     }
   }
 };
@@ -275,7 +253,8 @@ struct KeyRing {
 // flight while the current one is worked on, and the next head's Q slices
 // are fetched during the current head's last chunk. S^T = K Q^T puts query
 // c in lane column c (keys 4g .. 4g+3 in its registers); online softmax
-// with the lazy rescale of trie_block.h; O^T += V^T P^T.
+// with the lazy rescale of trie_block.h; O^T += V^T P^T (V^T blocks read
+// transposed from the ring's V rows).
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __restrict__ Q,
@@ -284,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
                                                        int hpu, float scale) {
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
-  using Ring = KeyRing<HD, Tin, ring_layout(sizeof(Tin), false)>;
+  using Ring = KeyRing<HD, Tin>;
   constexpr int WS = Ring::WS;
   __shared__ Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -369,10 +348,9 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
           l += p[r];
         }
         if constexpr (sizeof(Tin) == 2) {
-          const uint2 pw = pack_bf16(p);  // V^T in the ring: dim 16j+c, keys 16bl+4g ..
+          const uint2 pw = pack_bf16(p);  // V^T block: dims 16j .., keys 16bl ..
 #pragma unroll
-          for (int j = 0; j < MT; ++j)
-            o[j] = mfma_tr_bf16(Vs + (kBlk * j + c) * kTStride + kBlk * bl + 4 * g, pw, o[j]);
+          for (int j = 0; j < MT; ++j) o[j] = mfma_a_bf16(read_tr(Vs, WS, kBlk * bl, kBlk * j, lane), pw, o[j]);
         } else {
 #pragma unroll
           for (int j = 0; j < MT; ++j)
@@ -419,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   constexpr int MT = HD / 16;
   constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
   constexpr int NP = kDeltaFromO ? 1 : 2;  // passes over the key chunks per head
-  using Ring = KeyRing<HD, Tin, ring_layout(sizeof(Tin), true)>;
+  using Ring = KeyRing<HD, Tin>;
   constexpr int WS = Ring::WS;
   __shared__ Tables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -522,17 +500,18 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         scores(Ks, Vs, bl, sv, tv);
         if (pass == 0) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc += live[r] ? fast_exp2(sv[r] - l2) * tv[r] : 0.0f;
+          for (int r = 0; r < 4; ++r) acc += fast_exp2(live[r] ? sv[r] - l2 : -__builtin_inff()) * tv[r];
           continue;
         }
         float ds[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ds[r] = live[r] ? fast_exp2(sv[r] - l2) * (tv[r] - dl) * scale : 0.0f;
+        for (int r = 0; r < 4; ++r)  // masked: exp2(-inf) = 0, no branch per pair
+          ds[r] = fast_exp2(live[r] ? sv[r] - l2 : -__builtin_inff()) * (tv[r] - dl) * scale;
         if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per output tile
           const uint2 dw = pack_bf16(ds);
 #pragma unroll
           for (int j = 0; j < MT; ++j)
-            dq[j] = agpt_blk::mfma_rows_bf16(Ks + (kBlk * bl + 4 * g) * WS + kBlk * j + c, WS, dw, dq[j]);
+            dq[j] = mfma_a_bf16(read_tr(Ks, WS, kBlk * bl, kBlk * j, lane), dw, dq[j]);
         } else {
 #pragma unroll
           for (int j = 0; j < MT; ++j)
@@ -597,8 +576,6 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   extern __shared__ __align__(16) unsigned char dyn[];
   Tin* Qs = reinterpret_cast<Tin*>(dyn);
   Tin* Gs = Qs + kTile * WS;
-  Tin* Qt = Gs + kTile * WS;  // bf16: Q^T, dO^T [HD][kTStride]
-  Tin* Gt = Qt + HD * kTStride;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -640,10 +617,6 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
         *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
         *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
-        if constexpr (sizeof(Tin) == 2) {
-          store_tr(Qt, j / PIECES, (j % PIECES) * EPC, rq[k]);
-          store_tr(Gt, j / PIECES, (j % PIECES) * EPC, rg[k]);
-        }
       }
       if (threadIdx.x < kTile) {
         tb.l2[threadIdx.x] = rl * kLog2e;
@@ -699,17 +672,16 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
           float p[4], ds[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
-            ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+          for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
+            p[r] = fast_exp2(live[r] ? sv[r] - l2v[r] : -__builtin_inff());
+            ds[r] = p[r] * (tv[r] - dlv[r]) * scale;
           }
           if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
             const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T: dim 16j+c, queries q0 ..
-              const int at = (kBlk * j + c) * kTStride + q0;
-              dv[j] = mfma_tr_bf16(Gt + at, pw, dv[j]);
-              dk[j] = mfma_tr_bf16(Qt + at, dw, dk[j]);
+            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T blocks: dims 16j .., queries 16i ..
+              dv[j] = mfma_a_bf16(read_tr(Gs, WS, kBlk * i, kBlk * j, lane), pw, dv[j]);
+              dk[j] = mfma_a_bf16(read_tr(Qs, WS, kBlk * i, kBlk * j, lane), dw, dk[j]);
             }
           } else {
 #pragma unroll
@@ -821,8 +793,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
   extern __shared__ __align__(16) unsigned char dyn[];
   Tin* Qs = reinterpret_cast<Tin*>(dyn);
   Tin* Gs = Qs + kTile * WS;
-  Tin* Qt = Gs + kTile * WS;  // bf16: Q^T, dO^T [HD][kTStride]
-  Tin* Gt = Qt + HD * kTStride;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -884,10 +854,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
         *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
         *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
-        if constexpr (sizeof(Tin) == 2) {
-          store_tr(Qt, j / PIECES, (j % PIECES) * EPC, rq[k]);
-          store_tr(Gt, j / PIECES, (j % PIECES) * EPC, rg[k]);
-        }
       }
       if (threadIdx.x < kTile) {
         tb.l2[threadIdx.x] = rl * kLog2e;
@@ -932,17 +898,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
           const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
           float p[4], ds[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            p[r] = live[r] ? fast_exp2(sv[r] - l2v[r]) : 0.0f;
-            ds[r] = live[r] ? p[r] * (tv[r] - dlv[r]) * scale : 0.0f;
+          for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
+            p[r] = fast_exp2(live[r] ? sv[r] - l2v[r] : -__builtin_inff());
+            ds[r] = p[r] * (tv[r] - dlv[r]) * scale;
           }
           if constexpr (sizeof(Tin) == 2) {
             const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T: dim 16j+c, queries q0 ..
-              const int at = (kBlk * j + c) * kTStride + q0;
-              dv[j] = mfma_tr_bf16(Gt + at, pw, dv[j]);
-              dk[j] = mfma_tr_bf16(Qt + at, dw, dk[j]);
+            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T blocks: dims 16j .., queries 16i ..
+              dv[j] = mfma_a_bf16(read_tr(Gs, WS, kBlk * i, kBlk * j, lane), pw, dv[j]);
+              dk[j] = mfma_a_bf16(read_tr(Qs, WS, kBlk * i, kBlk * j, lane), dw, dk[j]);
             }
           } else {
 #pragma unroll
