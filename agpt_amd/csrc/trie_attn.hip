@@ -984,7 +984,9 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     if (h->deep) {
       h->fwd_lds = agpt_deep::ring_lds_bytes(hd, elem);
       h->bq_lds = agpt_deep::ring_lds_bytes(hd, elem);
-      h->kv_lds = agpt_deep::rows_lds_bytes(hd, elem);
+      // the key side's staged rows, and the carry kernel's prefetched table
+      // inputs of the next tile
+      h->kv_lds = agpt_deep::rows_lds_bytes(hd, elem) + agpt_deep::RawTabs::kBytes;
     }
     const bool ok = (hd == 16 || hd == 32 || (hd == 64 && hg == 1)) && H % hg == 0 &&
                     (hg == 1 || hg == 2 || hg == 4) &&

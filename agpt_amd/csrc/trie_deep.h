@@ -127,31 +127,35 @@ struct Unit {
   int t, s, ntile, A, poff, nk, nch;
 };
 
-template <typename PlanT>
-__device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t, bool row_tabs) {
+// Fills the tables of tile t, whose prefix list is entries poff .. poff+A-1
+// of the plan's; src gives the prefix rows and their subtree ends (entry j
+// of the tile's list) and the tile rows' subtree ends and depths.
+template <typename Src>
+__device__ __forceinline__ Unit fill_tables(Tables& tb, int t, int64_t T, int poff, int A, bool row_tabs,
+                                            const Src& src) {
   Unit w;
   w.t = t;
   w.s = w.t * kTile;
-  w.ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - w.s));
-  w.poff = pl.pref_off[w.t];
-  w.A = pl.pref_off[w.t + 1] - w.poff;
+  w.ntile = static_cast<int>(min(static_cast<int64_t>(kTile), T - w.s));
+  w.poff = poff;
+  w.A = A;
   w.nk = w.A + w.ntile;
   w.nch = (w.nk + kChunk - 1) / kChunk;
   const int tid = threadIdx.x;
   for (int j = tid; j < w.nch * kChunk; j += kThreads) {
     int iv = 0, row = w.s;
     if (j < w.A) {
-      row = pl.prefix[w.poff + j];
-      const int e = pl.pref_end[w.poff + j];
+      row = src.pre(j);
+      const int e = src.pend(j);
       iv = min(e - w.s, w.ntile) << 16;
       if (row_tabs) tb.pend[j] = e;
     } else if (j < w.nk) {
       const int r = j - w.A;
       row = w.s + r;
-      const int e = pl.end[row];
+      const int e = src.end(r);
       iv = r | ((min(e - w.s, w.ntile) - r) << 16);
       if (row_tabs) {
-        tb.rdep[r] = pl.depth[row];
+        tb.rdep[r] = src.dep(r);
         tb.rend[r] = e;
       }
     }
@@ -175,6 +179,61 @@ __device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t,
   __syncthreads();
   return w;
 }
+
+// The plan's tables in global memory as the source.
+template <typename PlanT>
+struct PlanSrc {
+  const PlanT& pl;
+  int poff, s;
+  __device__ __forceinline__ int pre(int j) const { return pl.prefix[poff + j]; }
+  __device__ __forceinline__ int pend(int j) const { return pl.pref_end[poff + j]; }
+  __device__ __forceinline__ int end(int r) const { return pl.end[s + r]; }
+  __device__ __forceinline__ int dep(int r) const { return pl.depth[s + r]; }
+};
+
+template <typename PlanT>
+__device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t, bool row_tabs) {
+  const int poff = pl.pref_off[t];
+  const int A = pl.pref_off[t + 1] - poff;
+  return fill_tables(tb, t, pl.T, poff, A, row_tabs, PlanSrc<PlanT>{pl, poff, t * kTile});
+}
+
+// A tile's table inputs copied into LDS ahead of use (RawTabs::gather), as
+// the source of fill_tables: prefix rows and their subtree ends, then the
+// tile rows' subtree ends and depths.
+struct RawTabs {
+  int32_t* base;  // [2][kKeyCap] prefix rows, subtree ends; [2][kTile] row ends, depths
+  __device__ __forceinline__ int pre(int j) const { return base[j]; }
+  __device__ __forceinline__ int pend(int j) const { return base[kKeyCap + j]; }
+  __device__ __forceinline__ int end(int r) const { return base[2 * kKeyCap + r]; }
+  __device__ __forceinline__ int dep(int r) const { return base[2 * kKeyCap + kTile + r]; }
+  static constexpr size_t kBytes = (2 * kKeyCap + 2 * kTile) * sizeof(int32_t);
+  // Issues the copies of tile t's inputs (prefix entries poff .. poff+A-1)
+  // with direct-to-LDS loads: the waves take 64-entry segments in turn; lane
+  // L of a segment writes entry 64 seg + L (its source index clamped to the
+  // list, so every address is in bounds). They complete under vmcnt: wait
+  // for them (wait_loads) before the barrier after which they are read.
+  template <typename PlanT>
+  __device__ __forceinline__ void gather(const PlanT& pl, int t, int poff, int A, int wave, int lane) const {
+    const int64_t s = static_cast<int64_t>(t) * kTile;
+    const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s)) - 1;
+    const int nseg = (A + 63) / 64;
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    for (int k = wave; k < 2 * nseg + 2; k += kThreads / 64) {
+      if (k < 2 * nseg) {
+        const int seg = k >> 1;
+        const int j = min(64 * seg + lane, A - 1);
+        const int32_t* src = (k & 1) ? pl.pref_end : pl.prefix;
+        int32_t* dst = base + ((k & 1) ? kKeyCap : 0) + 64 * seg;
+        __builtin_amdgcn_global_load_lds(src + poff + j, (lds_ptr)(dst), 4, 0, 0);
+      } else {
+        const int32_t* src = (k & 1) ? pl.depth : pl.end;
+        int32_t* dst = base + 2 * kKeyCap + ((k & 1) ? kTile : 0);
+        __builtin_amdgcn_global_load_lds(src + s + min(lane, last), (lds_ptr)(dst), 4, 0, 0);
+      }
+    }
+  }
+};
 
 // Waits until every vector-memory load of this wave has returned (vmcnt 0,
 // expcnt and lgkmcnt left alone). Placed after the loads of a unit's
@@ -793,6 +852,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
   extern __shared__ __align__(16) unsigned char dyn[];
   Tin* Qs = reinterpret_cast<Tin*>(dyn);
   Tin* Gs = Qs + kTile * WS;
+  const RawTabs raw{reinterpret_cast<int32_t*>(dyn + rows_lds_bytes(HD, sizeof(Tin)))};
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -844,11 +904,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         cv[i][j] = ck[i][j];
       }
     int a_prev = 0;  // the previous tile's prefix length
+    // The next tile's prefix list: pref_off[t + 1], pref_off[t + 2], loaded
+    // a tile ahead; its table inputs are copied into LDS (raw) during the
+    // current tile's key blocks, so only the chunk's first tile waits on
+    // the plan's tables in global memory.
+    int po1 = pl.pref_off[min(t0 + 1, pl.n_tiles)], po2 = pl.pref_off[min(t0 + 2, pl.n_tiles)];
     for (int t = t0; t < t1; ++t) {
       const bool first = t == t0;
       const bool last = t + 1 == t1;
       const int cur = (t - t0) & 1;
-      const Unit w = build_tables(pl, tb, t, true);
+      const Unit w = first ? build_tables(pl, tb, t, true) : fill_tables(tb, t, pl.T, po1, po2 - po1, true, raw);
+      if (!first) {
+        po1 = po2;
+        po2 = pl.pref_off[min(t + 2, pl.n_tiles)];
+      }
 #pragma unroll
       for (int k = 0; k < RPER; ++k) {
         const int j = static_cast<int>(threadIdx.x) + k * kThreads;
@@ -860,7 +929,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         tb.dl[threadIdx.x] = rd;
       }
       __syncthreads();
-      if (!last) fetch_rows(t + 1);
+      if (!last) {
+        raw.gather(pl, t + 1, po1, po2 - po1, wave, lane);
+        fetch_rows(t + 1);
+      }
       const int s = w.s, ntile = w.ntile, A = w.A;
       const int nkb = (A + ntile + kBlk - 1) / kBlk;
       Slice<Tin, KD> kf, vf, nkf, nvf;
@@ -1057,6 +1129,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         }
       }
       a_prev = A;
+      wait_loads();     // the next tile's table inputs are in LDS
       __syncthreads();  // the tile's staged rows, tables and carry rows are done with
     }
     u = uniform(tb.next[par]);
