@@ -1493,13 +1493,14 @@ int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds, int hg = 0) {
 
 // Heads per unit of the deep-prefix kernels: all heads of a tile when the
 // plan has tiles enough for ~16 units per CU (tables built once per tile,
-// heads streamed back to back), else one (units enough to fill the chip).
+// heads streamed back to back), else two (units enough to fill the chip,
+// each unit's tables shared by two heads; one for an odd head count).
 // AGPT_ATTN_DHPU overrides (a divisor of the head count).
 int deep_heads_per_unit(const agpt_attn_s* h) {
   const int H = h->cfg.n_heads;
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
-  int hpu = env_int("AGPT_ATTN_DHPU", h->n_tiles >= 16 * cus ? H : 1);
+  int hpu = env_int("AGPT_ATTN_DHPU", h->n_tiles >= 16 * cus ? H : H % 2 == 0 ? 2 : 1);
   if (hpu < 1 || hpu > H || H % hpu != 0) hpu = 1;
   return hpu;
 }
