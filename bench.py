@@ -249,6 +249,142 @@ def bench_loss(args, tr, V: int) -> int:
     return 0
 
 
+VARLEN_METRIC = ("packed varlen drop-ins (agpt_varlen_attention + _backward) fwd+bwd node-tokens/sec "
+                 "(1 GPU, the reference's packed layout)")
+
+
+def pack_paths(parent: np.ndarray, depth: np.ndarray):
+    """The reference's packed layout (batched_depth_forward.cr:668-742): node
+    n's rows are its root-to-node path, depth[n] of them, nodes in order.
+    Returns (kv_offsets, kv_lengths, rows)."""
+    T = parent.shape[0]
+    maxd = int(depth.max())
+    anc = np.full((T, maxd), -1, np.int64)
+    cur = np.arange(T, dtype=np.int64)
+    pos = depth.astype(np.int64) - 1
+    for _ in range(maxd):
+        ok = pos >= 0
+        if not ok.any():
+            break
+        anc[np.flatnonzero(ok), pos[ok]] = cur[ok]
+        cur = np.where(ok, parent[np.maximum(cur, 0)], cur)
+        pos = pos - 1
+    rows = anc[anc >= 0]  # row-major: node by node, root first
+    lens = depth.astype(np.int32)
+    offs = np.zeros(T, np.int64)
+    offs[1:] = np.cumsum(lens.astype(np.int64))[:-1]
+    return offs, lens, rows
+
+
+def bench_varlen(args, tr) -> int:
+    """One step = agpt_varlen_attention then agpt_varlen_attention_backward
+    over every node of the trie in the reference's packed layout (each node
+    carries its own copy of its path's K/V rows: L = Σ depth packed rows).
+    Algorithmic bytes per step, fp32: forward q, packed K, V read, O and the
+    saved weights written; backward q, dO, packed K, V and the weights read,
+    dQ and the packed dK, dV written: 20·T·D + 24·L·D + 8·L·H."""
+    import torch
+    from agpt_amd import attention as A
+
+    dev = torch.device("cuda:0")
+    from agpt_amd import trie as trie_mod
+    cfg = trie_mod.CONFIGS[args.workload]
+    H, hd = cfg["H"], cfg["hd"]
+    D = H * hd
+    T = tr.n_nodes
+    offs, lens, rows = pack_paths(tr.parent, tr.depth)
+    if offs[-1] + lens[-1] >= 2**31:
+        print("bench.py: --path varlen: packed rows exceed the int32 offsets of the drop-in API; "
+              "use a smaller --scale", file=sys.stderr)
+        return 2
+    L = int(rows.shape[0])
+    max_len = int(lens.max())
+    q, k, v, d_o = make_inputs(tr, D, H, hd, torch.float32, seed=1234, dev=dev)
+    ridx = torch.from_numpy(rows).to(dev)
+    kp = k.index_select(0, ridx)
+    vp = v.index_select(0, ridx)
+    del k, v, ridx
+    offs_d = torch.from_numpy(offs.astype(np.int32)).to(dev)
+    lens_d = torch.from_numpy(lens).to(dev)
+    out = torch.empty(T * D, device=dev)
+    w = torch.zeros(T * H * max_len, device=dev)
+    dq = torch.empty(T * D, device=dev)
+    dk = torch.empty(L * D, device=dev)
+    dv = torch.empty(L * D, device=dev)
+    scale = A.default_scale(hd)
+    torch.cuda.synchronize()
+    log(f"varlen inputs resident: T {T}, packed rows {L}, max_len {max_len}, "
+        f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step(e=None):
+        if e is not None:
+            hev.record(e[0], stream)
+        A.batched_varlen_attention(q, kp, vp, offs_d, lens_d, out, w, T, H, hd, max_len, scale)
+        if e is not None:
+            hev.record(e[1], stream)
+        A.batched_varlen_attention_backward(q, kp, vp, w, d_o, offs_d, lens_d, dq, dk, dv, T, H, hd,
+                                            max_len, scale)
+        if e is not None:
+            hev.record(e[2], stream)
+
+    hev = HipEvents()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [hev.create(3) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    f_ms = float(np.mean([hev.ms(e[0], e[1]) for e in evs]))
+    b_ms = float(np.mean([hev.ms(e[1], e[2]) for e in evs]))
+    for e in evs:
+        hev.destroy(e)
+    fwd_bytes = 4 * (2 * T * D + 2 * L * D + L * H)
+    bwd_bytes = 4 * (3 * T * D + 4 * L * D + L * H)
+    dom, dom_ms, dom_bytes = ("varlen_bwd", b_ms, bwd_bytes) if b_ms >= f_ms else ("varlen_fwd", f_ms, fwd_bytes)
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    step_ms = elapsed / args.steps * 1e3
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as ORC
+        M = min(args.cpu_rows // 8, T)
+        Lm = int(offs[M - 1] + lens[M - 1]) if M < T else L
+        qm = q[:M].cpu().numpy()
+        km = kp[:Lm].cpu().numpy()
+        vm = vp[:Lm].cpu().numpy()
+        gm = d_o[:M].cpu().numpy()
+        t0c = time.perf_counter()
+        o_r, w_r = ORC.varlen_fwd(qm, km, vm, offs[:M].astype(np.int32), lens[:M], M, H, hd, max_len, scale)
+        ORC.varlen_bwd(qm, km, vm, w_r, gm, offs[:M].astype(np.int32), lens[:M], M, H, hd, max_len, scale, Lm)
+        dt = time.perf_counter() - t0c
+        cpu = {"value": M / dt, "unit": "node-tokens/s", "cores": 1, "kind": "port",
+               "sample": f"first {M} nodes ({Lm} packed rows) of the same layout, oracle varlen "
+                         f"forward + backward (C restatement of the packed path), 1 thread, {dt:.1f} s",
+               "cpu_model": cpu_model()}
+    res = {
+        "metric": VARLEN_METRIC, "value": T * args.steps / elapsed, "unit": "node-tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": step_ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded Markov corpus -> radix trie, packed per node; random-init projections)",
+        "config": {"workload": f"{args.workload} packed varlen drop-ins", "node_tokens": T,
+                   "packed_rows": L, "max_len": max_len, "d_model": D, "heads": H, "head_dim": hd,
+                   "corpus_scale": args.scale},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": dom_ms},
+        "step_roofline": {"bytes_per_step": fwd_bytes + bwd_bytes,
+                          "achieved_GBps": (fwd_bytes + bwd_bytes) / (step_ms * 1e-3) / 1e9,
+                          "frac": (fwd_bytes + bwd_bytes) / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "kernel_avg_ms": {"varlen_fwd": f_ms, "varlen_bwd": b_ms},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 C3_METRIC = "C3 training step node-tokens/sec (4-layer µGPT over the C1 trie: fwd+bwd+RMSProp, 1 GPU)"
 
 
@@ -487,9 +623,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C4", "C5"])
-    ap.add_argument("--path", default="attn", choices=["attn", "loss", "c3"],
+    ap.add_argument("--path", default="attn", choices=["attn", "loss", "c3", "varlen"],
                     help="attn: trie attention fwd+bwd (the headline); loss: per-query AGPT loss; "
-                         "c3: the 4-layer training step of config C3 (C1 trie)")
+                         "c3: the 4-layer training step of config C3 (C1 trie); varlen: the packed "
+                         "varlen drop-ins a renaming caller gets (fp32 workloads)")
     ap.add_argument("--vocab", type=int, default=65, help="loss path: vocabulary size V")
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
@@ -541,7 +678,8 @@ def main() -> int:
             return 2
         return bench_full(args)
     if args.scale is None:
-        args.scale = cfg.get("one_gpu_scale", 1.0)
+        # the packed layout repeats every path row per node (C2 in full: 0.3 TB per tensor)
+        args.scale = 0.05 if args.path == "varlen" else cfg.get("one_gpu_scale", 1.0)
     H, hd = cfg["H"], cfg["hd"]
     D = H * hd
     dtype = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
@@ -554,6 +692,8 @@ def main() -> int:
         f"max depth {tr.max_depth} ({time.time() - t0:.1f}s)")
     if args.path == "loss":
         return bench_loss(args, tr, args.vocab)
+    if args.path == "varlen":
+        return bench_varlen(args, tr)
     dev = torch.device("cuda:0")
     # One plan per batch: the whole trie, or contiguous runs of whole bigram
     # partitions of at most --batch-rows rows (each reads its context rows,
