@@ -6,10 +6,14 @@
 // batched_depth_forward.cr:767 and agpt_train.cu:4740/4988 can switch by
 // renaming. The trie-native path (trie_attn.hip) avoids that duplication.
 //
-// Forward: thread per (query, head); scores are staged in weights_out (the
-// saved weights the reference's backward reads), softmax, P·V.
-// Backward from saved weights, with the reference's Float64 softmax-backward
-// dot (batched_depth_backward.cr:637-651). The L-query backward accumulates
+// Forward and node-level backward: a wave per query and group of heads,
+// its lanes over head-slice dims, heads and packed rows (VLanes), so a
+// query's contiguous packed rows are read in whole, coalesced rows; an
+// online softmax per lane, merged across lanes, and the saved weights
+// (weights_out, which the reference's backward reads) normalized in a second
+// pass. Backward from saved weights, with the reference's Float64
+// softmax-backward dot (batched_depth_backward.cr:637-651). The L-query
+// backward accumulates
 // each packed row over the radix node's queries in a fixed order inside one
 // workgroup: no atomics.
 
@@ -40,102 +44,218 @@ __device__ __forceinline__ int visible_len(int qi, const int* q2n, const int* qo
   return len < 0 ? 0 : (len > max_len ? max_len : len);
 }
 
+// Lane layout of the forward and node-level backward: a wave takes one
+// query and a group of HW of its heads (HW a power of two). Lane
+// L = dsub + NS (hl + HW pg): sub-lane dsub holds dims DS dsub .. of the head
+// slice (NS = HD / 16 sub-lanes at head_dim 32 and 64, else one), hl is the
+// head in the group and pg the lane's key group: it takes packed rows
+// p = pg, pg + PG, .. (PG = 64 / (NS HW) groups). For one p the lanes of a
+// wave read HW whole head slices of PG consecutive packed rows, and the rows
+// of a query are contiguous in the packed layout, so the reads coalesce.
+template <int HD>
+struct VLanes {
+  static constexpr int NS = HD > 16 ? HD / 16 : 1;
+  static constexpr int DS = HD / NS;
+  int hw, pgs, slots;  // heads per wave, key groups, waves per query
+  __host__ __device__ VLanes(int H) {
+    hw = 1;
+    while (hw * 2 <= H && hw * 2 * NS <= 64) hw *= 2;
+    pgs = 64 / (NS * hw);
+    slots = (H + hw - 1) / hw;
+  }
+};
+
+// Sum (or max) over the lanes that share (dsub, hl): a butterfly over the
+// key-group bits of the lane index.
+template <int NS>
+__device__ __forceinline__ float pg_sum(float x, int hw, int pgs) {
+  for (int m = NS * hw; m < NS * hw * pgs; m <<= 1) x += __shfl_xor(x, m);
+  return x;
+}
+template <int NS>
+__device__ __forceinline__ double pg_sum_d(double x, int hw, int pgs) {
+  for (int m = NS * hw; m < NS * hw * pgs; m <<= 1) x += __shfl_xor(x, m);
+  return x;
+}
+template <int NS>
+__device__ __forceinline__ float pg_max(float x, int hw, int pgs) {
+  for (int m = NS * hw; m < NS * hw * pgs; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+// Sum over the NS sub-lanes of one head slice.
+template <int NS>
+__device__ __forceinline__ float sub_sum(float x) {
+#pragma unroll
+  for (int m = 1; m < NS; m <<= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+// Forward of one query (node, or L-query slot) and HW heads per wave: each
+// lane keeps an online softmax over its key group (running max m, sum l and
+// the weighted V sum), writing raw scores to the weights; the key groups
+// merge by log-sum-exp, and a second pass over the lane's keys turns the
+// raw scores into the normalized weights the backward reads.
 template <int HD>
 __global__ __launch_bounds__(256) void varlen_fwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const int* __restrict__ kv_off, const int* __restrict__ kv_len, const int* __restrict__ q2n,
     const int* __restrict__ qoff, float* __restrict__ out, float* __restrict__ weights, int n_q,
     int H, int max_len, float scale) {
-  const int item = blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= n_q * H) return;
-  const int qi = item / H, h = item - (item / H) * H;
+  using LN = VLanes<HD>;
+  constexpr int NS = LN::NS, DS = LN::DS;
+  const LN ln(H);
+  const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= n_q * ln.slots) return;  // uniform per wave
+  const int qi = item / ln.slots;
+  const int lane = threadIdx.x & 63;
+  const int dsub = lane % NS, hl = (lane / NS) % ln.hw, pg = lane / (NS * ln.hw);
+  const int h = (item - qi * ln.slots) * ln.hw + hl;
+  const bool act = h < H && pg < ln.pgs;
+  const int hh = act ? h : 0;
   int node;
   const int len = visible_len(qi, q2n, qoff, kv_len, max_len, &node);
   const int64_t off = kv_off[node];
-  float qq[HD], acc[HD];
-  load_vec<HD>(q + (static_cast<int64_t>(qi) * H + h) * HD, qq);
+  float qq[DS], acc[DS];
+  load_vec<DS>(q + (static_cast<int64_t>(qi) * H + hh) * HD + DS * dsub, qq);
 #pragma unroll
-  for (int i = 0; i < HD; ++i) acc[i] = 0.0f;
-  float* w = weights + (static_cast<int64_t>(qi) * H + h) * max_len;
-  float m = -INFINITY;
-  for (int p = 0; p < len; ++p) {
-    float kk[HD];
-    load_vec<HD>(k + ((off + p) * H + h) * HD, kk);
+  for (int i = 0; i < DS; ++i) acc[i] = 0.0f;
+  float* w = weights + (static_cast<int64_t>(qi) * H + hh) * max_len;
+  float m = -INFINITY, l = 0.0f;
+  const int np = act ? (len - pg + ln.pgs - 1) / ln.pgs : 0;  // this lane's keys
+  const int np_max = (len + ln.pgs - 1) / ln.pgs;               // the wave's trip count
+  for (int i = 0; i < np_max; ++i) {
+    const int p = pg + i * ln.pgs;
+    const bool on = i < np;
+    const int64_t row = (off + (on ? p : 0)) * H + hh;
+    float kk[DS], vv[DS];
+    load_vec<DS>(k + row * HD + DS * dsub, kk);
+    load_vec<DS>(v + row * HD + DS * dsub, vv);
     float sc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < HD; ++i) sc += qq[i] * kk[i];
-    sc *= scale;
-    w[p] = sc;
-    m = fmaxf(m, sc);
-  }
-  float sum = 0.0f;
-  for (int p = 0; p < len; ++p) {
-    const float ex = fast_exp2((w[p] - m) * kLog2e);
-    w[p] = ex;
-    sum += ex;
-  }
-  const float inv = len > 0 ? 1.0f / sum : 0.0f;
-  for (int p = 0; p < len; ++p) {
-    const float wp = w[p] * inv;
-    w[p] = wp;
-    float vv[HD];
-    load_vec<HD>(v + ((off + p) * H + h) * HD, vv);
+    for (int x = 0; x < DS; ++x) sc += qq[x] * kk[x];
+    sc = sub_sum<NS>(sc) * scale;
+    if (on && dsub == 0) w[p] = sc;
+    const float s2 = on ? sc * kLog2e : -INFINITY;
+    const float mn = fmaxf(m, s2);
+    const float corr = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+    const float e = on ? fast_exp2(s2 - mn) : 0.0f;
+    l = l * corr + e;
 #pragma unroll
-    for (int i = 0; i < HD; ++i) acc[i] += wp * vv[i];
+    for (int x = 0; x < DS; ++x) acc[x] = acc[x] * corr + e * vv[x];
+    m = mn;
   }
-  store_vec<HD>(out + (static_cast<int64_t>(qi) * H + h) * HD, acc);
+  // merge the key groups
+  const float mt = pg_max<NS>(m, ln.hw, ln.pgs);
+  const float cf = m == -INFINITY ? 0.0f : fast_exp2(m - mt);
+  const float lt = pg_sum<NS>(l * cf, ln.hw, ln.pgs);
+#pragma unroll
+  for (int x = 0; x < DS; ++x) acc[x] = pg_sum<NS>(acc[x] * cf, ln.hw, ln.pgs);
+  const float inv = len > 0 ? 1.0f / lt : 0.0f;
+  if (act && pg == 0) {
+    float o[DS];
+#pragma unroll
+    for (int x = 0; x < DS; ++x) o[x] = acc[x] * inv;
+    store_vec<DS>(out + (static_cast<int64_t>(qi) * H + h) * HD + DS * dsub, o);
+  }
+  if (act && dsub == 0)
+    for (int i = 0; i < np; ++i) {
+      const int p = pg + i * ln.pgs;
+      w[p] = fast_exp2(w[p] * kLog2e - mt) * inv;
+    }
 }
 
 // Node-level backward: every packed row belongs to exactly one node, so the
-// thread of (node, head) owns its rows and writes them.
+// lanes of (node, head) own its rows and write them. δ = Σ_p w_p (dO·v_p)
+// in float64 as in the reference (batched_depth_backward.cr:637-651), then
+// dS, dQ (summed over the key groups), and the rows' dK = dS q, dV = w dO.
 template <int HD>
 __global__ __launch_bounds__(256) void varlen_bwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ weights, const float* __restrict__ d_out,
     const int* __restrict__ kv_off, const int* __restrict__ kv_len, float* __restrict__ dq,
     float* __restrict__ dk, float* __restrict__ dv, int n_nodes, int H, int max_len, float scale) {
-  const int item = blockIdx.x * blockDim.x + threadIdx.x;
-  if (item >= n_nodes * H) return;
-  const int i = item / H, h = item - (item / H) * H;
+  using LN = VLanes<HD>;
+  constexpr int NS = LN::NS, DS = LN::DS;
+  const LN ln(H);
+  const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= n_nodes * ln.slots) return;  // uniform per wave
+  const int i = item / ln.slots;
+  const int lane = threadIdx.x & 63;
+  const int dsub = lane % NS, hl = (lane / NS) % ln.hw, pg = lane / (NS * ln.hw);
+  const int h = (item - i * ln.slots) * ln.hw + hl;
+  const bool act = h < H && pg < ln.pgs;
+  const int hh = act ? h : 0;
   int node;
   const int len = visible_len(i, nullptr, nullptr, kv_len, max_len, &node);
   const int64_t off = kv_off[node];
-  float g[HD], qq[HD], dqa[HD];
-  load_vec<HD>(d_out + (static_cast<int64_t>(i) * H + h) * HD, g);
-  load_vec<HD>(q + (static_cast<int64_t>(i) * H + h) * HD, qq);
+  float g[DS], qq[DS], dqa[DS];
+  load_vec<DS>(d_out + (static_cast<int64_t>(i) * H + hh) * HD + DS * dsub, g);
+  load_vec<DS>(q + (static_cast<int64_t>(i) * H + hh) * HD + DS * dsub, qq);
 #pragma unroll
-  for (int j = 0; j < HD; ++j) dqa[j] = 0.0f;
-  const float* w = weights + (static_cast<int64_t>(i) * H + h) * max_len;
+  for (int x = 0; x < DS; ++x) dqa[x] = 0.0f;
+  const float* w = weights + (static_cast<int64_t>(i) * H + hh) * max_len;
+  const int np = act ? (len - pg + ln.pgs - 1) / ln.pgs : 0;
+  const int np_max = (len + ln.pgs - 1) / ln.pgs;  // uniform per wave
+  // dO·v of the lane's first kCache keys stays in registers between the two
+  // passes (the second then reads no V); later keys recompute it.
+  constexpr int kCache = 8;
+  float dwc[kCache];
+  auto dw_of = [&](int p, bool on) {
+    float vv[DS];
+    load_vec<DS>(v + ((off + (on ? p : 0)) * H + hh) * HD + DS * dsub, vv);
+    float dw = 0.0f;
+#pragma unroll
+    for (int x = 0; x < DS; ++x) dw += g[x] * vv[x];
+    return sub_sum<NS>(dw);
+  };
   double dot = 0.0;
-  for (int p = 0; p < len; ++p) {
-    float vv[HD];
-    load_vec<HD>(v + ((off + p) * H + h) * HD, vv);
-    float dw = 0.0f;
 #pragma unroll
-    for (int j = 0; j < HD; ++j) dw += g[j] * vv[j];
-    dot += static_cast<double>(dw * w[p]);
+  for (int t = 0; t < kCache; ++t) {
+    if (t >= np_max) break;
+    const int p = pg + t * ln.pgs;
+    const bool on = t < np;
+    dwc[t] = dw_of(p, on);
+    if (on) dot += static_cast<double>(dwc[t] * w[p]);
   }
-  for (int p = 0; p < len; ++p) {
-    float vv[HD], kk[HD];
-    load_vec<HD>(v + ((off + p) * H + h) * HD, vv);
-    load_vec<HD>(k + ((off + p) * H + h) * HD, kk);
-    float dw = 0.0f;
-#pragma unroll
-    for (int j = 0; j < HD; ++j) dw += g[j] * vv[j];
-    const float wp = w[p];
+  for (int t = kCache; t < np_max; ++t) {
+    const int p = pg + t * ln.pgs;
+    const bool on = t < np;
+    const float dw = dw_of(p, on);
+    if (on) dot += static_cast<double>(dw * w[p]);
+  }
+  dot = pg_sum_d<NS>(dot, ln.hw, ln.pgs);
+  auto emit = [&](int p, bool on, float dw) {
+    const int64_t row = (off + (on ? p : 0)) * H + hh;
+    float kk[DS];
+    load_vec<DS>(k + row * HD + DS * dsub, kk);
+    const float wp = on ? w[p] : 0.0f;
     const float ds = static_cast<float>(static_cast<double>(wp) * (static_cast<double>(dw) - dot) *
                                         static_cast<double>(scale));
-    float rk[HD], rv[HD];
+    float rk[DS], rv[DS];
 #pragma unroll
-    for (int j = 0; j < HD; ++j) {
-      dqa[j] += ds * kk[j];
-      rk[j] = ds * qq[j];
-      rv[j] = wp * g[j];
+    for (int x = 0; x < DS; ++x) {
+      dqa[x] += ds * kk[x];
+      rk[x] = ds * qq[x];
+      rv[x] = wp * g[x];
     }
-    store_vec<HD>(dk + ((off + p) * H + h) * HD, rk);
-    store_vec<HD>(dv + ((off + p) * H + h) * HD, rv);
+    if (on) {
+      store_vec<DS>(dk + row * HD + DS * dsub, rk);
+      store_vec<DS>(dv + row * HD + DS * dsub, rv);
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < kCache; ++t) {
+    if (t >= np_max) break;
+    emit(pg + t * ln.pgs, t < np, dwc[t]);
   }
-  store_vec<HD>(dq + (static_cast<int64_t>(i) * H + h) * HD, dqa);
+  for (int t = kCache; t < np_max; ++t) {
+    const int p = pg + t * ln.pgs;
+    const bool on = t < np;
+    emit(p, on, dw_of(p, on));
+  }
+#pragma unroll
+  for (int x = 0; x < DS; ++x) dqa[x] = pg_sum<NS>(dqa[x], ln.hw, ln.pgs);
+  if (act && pg == 0) store_vec<DS>(dq + (static_cast<int64_t>(i) * H + h) * HD + DS * dsub, dqa);
 }
 
 // L-query backward: one 64-lane workgroup per (radix node, head), launched
@@ -266,10 +386,10 @@ extern "C" int agpt_varlen_attention(const float* q, const float* k, const float
   if (n_nodes == 0) return AGPT_OK;
   if (!q || !k || !v || !kv_offsets || !kv_lengths || !output || !weights_out)
     return vset_error(AGPT_ERR_INVALID_ARG, "varlen: null pointer");
-  const int items = n_nodes * n_heads;
   const int rc = dispatch(head_dim, [&](auto c) {
     constexpr int HD = decltype(c)::value;
-    hipLaunchKernelGGL((varlen_fwd_kernel<HD>), dim3((items + 255) / 256), dim3(256), 0,
+    const int64_t items = static_cast<int64_t>(n_nodes) * VLanes<HD>(n_heads).slots;  // one wave each
+    hipLaunchKernelGGL((varlen_fwd_kernel<HD>), dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), q, k, v, kv_offsets, kv_lengths, nullptr,
                        nullptr, output, weights_out, n_nodes, n_heads, max_len, scale);
   });
@@ -286,10 +406,10 @@ extern "C" int agpt_varlen_attention_backward(const float* q, const float* k, co
   if (n_nodes == 0) return AGPT_OK;
   if (!q || !k || !v || !attn_weights || !d_out || !kv_offsets || !kv_lengths || !dq || !dk_full || !dv_full)
     return vset_error(AGPT_ERR_INVALID_ARG, "varlen: null pointer");
-  const int items = n_nodes * n_heads;
   const int rc = dispatch(head_dim, [&](auto c) {
     constexpr int HD = decltype(c)::value;
-    hipLaunchKernelGGL((varlen_bwd_kernel<HD>), dim3((items + 255) / 256), dim3(256), 0,
+    const int64_t items = static_cast<int64_t>(n_nodes) * VLanes<HD>(n_heads).slots;  // one wave each
+    hipLaunchKernelGGL((varlen_bwd_kernel<HD>), dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), q, k, v, attn_weights, d_out, kv_offsets,
                        kv_lengths, dq, dk_full, dv_full, n_nodes, n_heads, max_len, scale);
   });
@@ -321,10 +441,10 @@ extern "C" int agpt_varlen_attention_L_queries(const float* q, const float* k, c
   if (!q || !k || !v || !query_to_node || !query_offsets || !kv_offsets || !kv_lengths || !output ||
       !weights_out)
     return vset_error(AGPT_ERR_INVALID_ARG, "varlen_L: null pointer");
-  const int items = T_q * n_heads;
   const int rc = dispatch(head_dim, [&](auto c) {
     constexpr int HD = decltype(c)::value;
-    hipLaunchKernelGGL((varlen_fwd_kernel<HD>), dim3((items + 255) / 256), dim3(256), 0,
+    const int64_t items = static_cast<int64_t>(T_q) * VLanes<HD>(n_heads).slots;  // one wave each
+    hipLaunchKernelGGL((varlen_fwd_kernel<HD>), dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), q, k, v, kv_offsets, kv_lengths, query_to_node,
                        query_offsets, output, weights_out, T_q, n_heads, max_kv_len, scale);
   });
