@@ -253,14 +253,18 @@ VARLEN_METRIC = ("packed varlen drop-ins (agpt_varlen_attention + _backward) fwd
                  "(1 GPU, the reference's packed layout)")
 
 
-def pack_paths(parent: np.ndarray, depth: np.ndarray):
+def pack_paths(parent: np.ndarray, depth: np.ndarray, nodes: np.ndarray | None = None):
     """The reference's packed layout (batched_depth_forward.cr:668-742): node
-    n's rows are its root-to-node path, depth[n] of them, nodes in order.
-    Returns (kv_offsets, kv_lengths, rows)."""
-    T = parent.shape[0]
+    n's rows are its root-to-node path, depth[n] of them, nodes in order (all
+    nodes, or the given ones). Returns (kv_offsets, kv_lengths, rows)."""
+    if nodes is None:
+        nodes = np.arange(parent.shape[0], dtype=np.int64)
+    nodes = np.asarray(nodes, np.int64)
+    T = nodes.shape[0]
+    depth = depth[nodes]
     maxd = int(depth.max())
     anc = np.full((T, maxd), -1, np.int64)
-    cur = np.arange(T, dtype=np.int64)
+    cur = nodes.copy()
     pos = depth.astype(np.int64) - 1
     for _ in range(maxd):
         ok = pos >= 0
@@ -292,7 +296,21 @@ def bench_varlen(args, tr) -> int:
     H, hd = cfg["H"], cfg["hd"]
     D = H * hd
     T = tr.n_nodes
-    offs, lens, rows = pack_paths(tr.parent, tr.depth)
+    radix = args.varlen_layout == "radix"
+    if radix:
+        # the chunk packer's layout (agpt_train.cu:4456-4479): the queries of
+        # radix node r are its edge rows; its packed rows are the path to its
+        # last row, shared by its queries
+        heads = np.flatnonzero(tr.radix_head)
+        qoff = np.append(heads, T).astype(np.int32)
+        elen = np.diff(qoff)
+        q2n = np.repeat(np.arange(heads.shape[0], dtype=np.int32), elen)
+        offs, lens, rows = pack_paths(tr.parent, tr.depth, qoff[1:] - 1)
+        # visible keys of query t of node r: len - L + j + 1
+        vis = (lens[q2n] - elen[q2n] + (np.arange(T) - qoff[q2n]) + 1).astype(np.int64)
+    else:
+        offs, lens, rows = pack_paths(tr.parent, tr.depth)
+        vis = lens.astype(np.int64)
     if offs[-1] + lens[-1] >= 2**31:
         print("bench.py: --path varlen: packed rows exceed the int32 offsets of the drop-in API; "
               "use a smaller --scale", file=sys.stderr)
@@ -317,14 +335,26 @@ def bench_varlen(args, tr) -> int:
         f"{torch.cuda.memory_allocated() / 2**30:.1f} GiB")
     stream = torch.cuda.current_stream(dev).cuda_stream
 
+    if radix:
+        q2n_d = torch.from_numpy(q2n).to(dev)
+        qoff_d = torch.from_numpy(qoff).to(dev)
+
     def step(e=None):
         if e is not None:
             hev.record(e[0], stream)
-        A.batched_varlen_attention(q, kp, vp, offs_d, lens_d, out, w, T, H, hd, max_len, scale)
+        if radix:
+            A.batched_varlen_attention_L_queries(q, kp, vp, q2n_d, qoff_d, offs_d, lens_d, out, w, T, H, hd,
+                                                 max_len, scale)
+        else:
+            A.batched_varlen_attention(q, kp, vp, offs_d, lens_d, out, w, T, H, hd, max_len, scale)
         if e is not None:
             hev.record(e[1], stream)
-        A.batched_varlen_attention_backward(q, kp, vp, w, d_o, offs_d, lens_d, dq, dk, dv, T, H, hd,
-                                            max_len, scale)
+        if radix:  # accumulates into dk, dv
+            A.batched_varlen_attention_L_queries_backward(q, kp, vp, w, d_o, q2n_d, qoff_d, offs_d, lens_d,
+                                                          dq, dk, dv, T, H, hd, max_len, scale)
+        else:
+            A.batched_varlen_attention_backward(q, kp, vp, w, d_o, offs_d, lens_d, dq, dk, dv, T, H, hd,
+                                                max_len, scale)
         if e is not None:
             hev.record(e[2], stream)
 
@@ -342,13 +372,14 @@ def bench_varlen(args, tr) -> int:
     b_ms = float(np.mean([hev.ms(e[1], e[2]) for e in evs]))
     for e in evs:
         hev.destroy(e)
-    fwd_bytes = 4 * (2 * T * D + 2 * L * D + L * H)
-    bwd_bytes = 4 * (3 * T * D + 4 * L * D + L * H)
+    W = int(vis.sum())  # weights written by the forward, read by the backward
+    fwd_bytes = 4 * (2 * T * D + 2 * L * D + W * H)
+    bwd_bytes = 4 * (3 * T * D + (6 if radix else 4) * L * D + W * H)  # radix: dK, dV read and added to
     dom, dom_ms, dom_bytes = ("varlen_bwd", b_ms, bwd_bytes) if b_ms >= f_ms else ("varlen_fwd", f_ms, fwd_bytes)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     step_ms = elapsed / args.steps * 1e3
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not radix:
         from oracle import oracle as ORC
         M = min(args.cpu_rows // 8, T)
         Lm = int(offs[M - 1] + lens[M - 1]) if M < T else L
@@ -369,7 +400,9 @@ def bench_varlen(args, tr) -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": step_ms, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded Markov corpus -> radix trie, packed per node; random-init projections)",
-        "config": {"workload": f"{args.workload} packed varlen drop-ins", "node_tokens": T,
+        "config": {"workload": f"{args.workload} packed varlen drop-ins, "
+                               f"{'radix-node queries (L-query API)' if radix else 'one query per node'}",
+                   "node_tokens": T,
                    "packed_rows": L, "max_len": max_len, "d_model": D, "heads": H, "head_dim": hd,
                    "corpus_scale": args.scale},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS,
@@ -628,6 +661,9 @@ def main() -> int:
                          "c3: the 4-layer training step of config C3 (C1 trie); varlen: the packed "
                          "varlen drop-ins a renaming caller gets (fp32 workloads)")
     ap.add_argument("--vocab", type=int, default=65, help="loss path: vocabulary size V")
+    ap.add_argument("--varlen-layout", default="node", choices=["node", "radix"],
+                    help="varlen path: one query per node (agpt_varlen_attention) or the queries of "
+                         "each radix node over its shared prefix (agpt_varlen_attention_L_queries)")
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
                          "one GPU holds)")
