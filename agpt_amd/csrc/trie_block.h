@@ -1241,17 +1241,29 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto pair = [&](const int i, float (&dst)[4]) {
         const int qr = kBlk * i + c;  // query row this lane supplies
         const int q0 = kBlk * i + 4 * g;
-        float qa[KD], ga[KD];
+        // Every LDS read of the pair is issued before its first product and
+        // before the dS^T store (which the reads could not pass), so their
+        // latency hides behind the S products.
+        float qa[KD], ga[KD], gcol[MT][4], qcol[MT][4];
         load_vec<KD>(Qs + qr * WS + hoff + KD * g, qa);
         load_vec<KD>(Gs + qr * WS + hoff + KD * g, ga);
+        const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[hh][q0]);
+        const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[hh][q0]);
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = (q0 + r) * WS + hoff + kBlk * j + c;
+            gcol[j][r] = ld1(Gs + row);
+            qcol[j][r] = ld1(Qs + row);
+          }
+        __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink them past the S products)
         f4 sv = f4{0.0f, 0.0f, 0.0f, 0.0f}, tv = sv;
 #pragma unroll
         for (int j = 0; j < KD; ++j) {
           sv = mfma16(qa[j], kf[j], sv);  // sv[r]: query q0+r against key kslot
           tv = mfma16(ga[j], vf[j], tv);
         }
-        const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[hh][q0]);
-        const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[hh][q0]);
         float p[4], ds[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -1266,9 +1278,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         for (int j = 0; j < MT; ++j)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int row = (q0 + r) * WS + hoff + kBlk * j + c;
-            dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
-            dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+            dv[j] = mfma16(gcol[j][r], p[r], dv[j]);
+            dk[j] = mfma16(qcol[j][r], ds[r], dk[j]);
           }
 #pragma unroll
         for (int r = 0; r < 4; ++r) dst[r] = tr[(4 * g + r) * 20 + c];
