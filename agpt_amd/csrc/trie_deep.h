@@ -109,17 +109,21 @@ __device__ __forceinline__ f4 mfma_a_bf16(agpt_blk::bf16x4_bits a, uint2 wb, f4 
 // The tile's key list and row tables. Keys 0 .. A-1 are the prefix rows
 // (depth 1 .. A), keys A .. A+ntile-1 the tile rows; the list is padded to
 // whole chunks with empty keys that name row s (finite data, never live).
-struct alignas(16) Tables {
+// The query side keeps only the key list (KeyTables, 2.7 KB, so that four
+// forward workgroups fit a CU); the key side adds the row tables.
+struct alignas(16) KeyTables {
   alignas(16) int32_t kint[kKeyCap];  // per key: lo | len << 16, the tile rows [lo, lo + len) that see it
   int32_t krow[kKeyCap];  // per key: its row in the tensors (negative: a context row of a range plan)
   alignas(16) int32_t blo[kKeyCap / kBlk];  // per key block: least lo of its live keys (kTile if none)
   alignas(16) int32_t bhi[kKeyCap / kBlk];  // per key block: greatest lo + len
+  int32_t next[2];       // claims, alternating by unit
+};
+struct alignas(16) Tables : KeyTables {
   int32_t pend[kKeyCap];  // per prefix key: its subtree end (rows of the plan)
   int32_t rdep[kTile];   // depth of the tile rows
   int32_t rend[kTile];   // subtree end of the tile rows
   alignas(16) float l2[kTile];  // lse * log2(e) of the tile rows (key side)
   alignas(16) float dl[kTile];  // δ of the tile rows (key side)
-  int32_t next[2];       // claims, alternating by unit
 };
 
 // The tile of unit t; fills its key list and tables.
@@ -130,9 +134,10 @@ struct Unit {
 // Fills the tables of tile t, whose prefix list is entries poff .. poff+A-1
 // of the plan's; src gives the prefix rows and their subtree ends (entry j
 // of the tile's list) and the tile rows' subtree ends and depths.
-template <typename Src>
-__device__ __forceinline__ Unit fill_tables(Tables& tb, int t, int64_t T, int poff, int A, bool row_tabs,
+template <typename TB, typename Src>
+__device__ __forceinline__ Unit fill_tables(TB& tb, int t, int64_t T, int poff, int A, bool row_tabs,
                                             const Src& src) {
+  constexpr bool kRows = std::is_same<TB, Tables>::value;  // the key side's row tables
   Unit w;
   w.t = t;
   w.s = w.t * kTile;
@@ -148,15 +153,19 @@ __device__ __forceinline__ Unit fill_tables(Tables& tb, int t, int64_t T, int po
       row = src.pre(j);
       const int e = src.pend(j);
       iv = min(e - w.s, w.ntile) << 16;
-      if (row_tabs) tb.pend[j] = e;
+      if constexpr (kRows) {
+        if (row_tabs) tb.pend[j] = e;
+      }
     } else if (j < w.nk) {
       const int r = j - w.A;
       row = w.s + r;
       const int e = src.end(r);
       iv = r | ((min(e - w.s, w.ntile) - r) << 16);
-      if (row_tabs) {
-        tb.rdep[r] = src.dep(r);
-        tb.rend[r] = e;
+      if constexpr (kRows) {
+        if (row_tabs) {
+          tb.rdep[r] = src.dep(r);
+          tb.rend[r] = e;
+        }
       }
     }
     tb.kint[j] = iv;
@@ -191,8 +200,8 @@ struct PlanSrc {
   __device__ __forceinline__ int dep(int r) const { return pl.depth[s + r]; }
 };
 
-template <typename PlanT>
-__device__ __forceinline__ Unit build_tables(const PlanT& pl, Tables& tb, int t, bool row_tabs) {
+template <typename PlanT, typename TB>
+__device__ __forceinline__ Unit build_tables(const PlanT& pl, TB& tb, int t, bool row_tabs) {
   const int poff = pl.pref_off[t];
   const int A = pl.pref_off[t + 1] - poff;
   return fill_tables(tb, t, pl.T, poff, A, row_tabs, PlanSrc<PlanT>{pl, poff, t * kTile});
@@ -254,7 +263,7 @@ __device__ __forceinline__ int tile_of(const PlanT& pl, int i) {
 // 16-byte reads per chunk, and a scalar bit test per block, where a test per
 // block would make two dependent LDS round trips and an exec-mask branch.
 static_assert(kChunk / kBlk == 4, "four key blocks per chunk");
-__device__ __forceinline__ int chunk_live(const Tables& tb, int ch, int i) {
+__device__ __forceinline__ int chunk_live(const KeyTables& tb, int ch, int i) {
   const int4 lo = *reinterpret_cast<const int4*>(tb.blo + 4 * ch);
   const int4 hi = *reinterpret_cast<const int4*>(tb.bhi + 4 * ch);
   const int r0 = kBlk * i, r1 = r0 + kBlk;
@@ -264,7 +273,7 @@ __device__ __forceinline__ int chunk_live(const Tables& tb, int ch, int i) {
 }
 
 // Whether query block i (rows 16i .. 16i+15) has a live pair with key block b.
-__device__ __forceinline__ bool block_live(const Tables& tb, int b, int i) {
+__device__ __forceinline__ bool block_live(const KeyTables& tb, int b, int i) {
   return kBlk * i < uniform(tb.bhi[b]) && kBlk * i + kBlk > uniform(tb.blo[b]);
 }
 
@@ -284,7 +293,7 @@ struct KeyRing {
   u4 r[PER];
   __device__ __forceinline__ Tin* ks(int buf) const { return base + buf * BUF; }
   __device__ __forceinline__ Tin* vs(int buf) const { return base + buf * BUF + kChunk * WS; }
-  __device__ __forceinline__ void load(const Tables& tb, const Tin* K, const Tin* V, int D, int h, int c) {
+  __device__ __forceinline__ void load(const KeyTables& tb, const Tin* K, const Tin* V, int D, int h, int c) {
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int ten = k * kThreads / PER_T;  // a constant once unrolled
@@ -324,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   constexpr int MT = HD / 16;
   using Ring = KeyRing<HD, Tin>;
   constexpr int WS = Ring::WS;
-  __shared__ Tables tb;
+  __shared__ KeyTables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
   Ring ring;
   ring.base = reinterpret_cast<Tin*>(dyn);
@@ -458,7 +467,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   constexpr int NP = kDeltaFromO ? 1 : 2;  // passes over the key chunks per head
   using Ring = KeyRing<HD, Tin>;
   constexpr int WS = Ring::WS;
-  __shared__ Tables tb;
+  __shared__ KeyTables tb;
   extern __shared__ __align__(16) unsigned char dyn[];
   Ring ring;
   ring.base = reinterpret_cast<Tin*>(dyn);
