@@ -342,6 +342,9 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
+  // bf16 scores come unscaled (the fp32 operands are scaled once): the
+  // scale goes into the exponent's multiply-add.
+  const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
   int* ctr = pl.sched + 0;
   if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
   __syncthreads();
@@ -395,11 +398,12 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
         Slice<Tin, KD> kf;
         kf.load(Ks + (kBlk * bl + c) * WS + KD * g);
         f4 sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16b+4g+r against query q
-        if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
         float sc[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) sc[r] = live[r] ? sv[r] : -__builtin_inff();
-        const float lmx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        // The scale (> 0) goes on the maximum, and into the exponent's
+        // multiply-add.
+        const float lmx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * sfac;
         if (__any(lmx > m + kRescaleLog2)) {
           const float mx = group_max(lmx);
           const bool resc = mx > m + kRescaleLog2;
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
         float p[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          p[r] = fast_exp2(sc[r] - m);  // masked: exp2(-inf) = 0
+          p[r] = fast_exp2(__builtin_fmaf(sc[r], sfac, -m));  // masked: exp2(-inf) = 0
           l += p[r];
         }
         if constexpr (sizeof(Tin) == 2) {
@@ -476,6 +480,9 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
+  // bf16 scores come unscaled (the fp32 operands are scaled once): the
+  // scale goes into the exponent's multiply-add.
+  const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
   int* ctr = pl.sched + 1;
   if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
   __syncthreads();
@@ -516,7 +523,6 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       vf.load(Vs + (kBlk * bl + c) * WS + KD * g);
       sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});
       tv = slice_dot(vf, gf, f4{0.0f, 0.0f, 0.0f, 0.0f});
-      if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
     };
     auto mask = [&](int b, bool (&live)[4]) {
       const int4 iv = *reinterpret_cast<const int4*>(tb.kint + kBlk * b + 4 * g);
@@ -568,13 +574,13 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         scores(Ks, Vs, bl, sv, tv);
         if (pass == 0) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc += fast_exp2(live[r] ? sv[r] - l2 : -__builtin_inff()) * tv[r];
+          for (int r = 0; r < 4; ++r) acc += fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2) : -__builtin_inff()) * tv[r];
           continue;
         }
         float ds[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)  // masked: exp2(-inf) = 0, no branch per pair
-          ds[r] = fast_exp2(live[r] ? sv[r] - l2 : -__builtin_inff()) * (tv[r] - dl) * scale;
+          ds[r] = fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2) : -__builtin_inff()) * (tv[r] - dl) * scale;
         if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per output tile
           const uint2 dw = pack_bf16(ds);
 #pragma unroll
@@ -649,6 +655,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   const int g = lane >> 4, c = lane & 15;
   const int D = H * HD;
   const float qscale = scale * kLog2e;
+  // bf16 scores come unscaled (the fp32 operands are scaled once): the
+  // scale goes into the exponent's multiply-add.
+  const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
   int* ctr = pl.sched + 2;
   if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
   __syncthreads();
@@ -735,13 +744,12 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
           ga.load(Gs + qr * WS + KD * g);
           f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // sv[r]: query q0+r against key `key`
           const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
-          if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
           const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
           const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
           float p[4], ds[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
-            p[r] = fast_exp2(live[r] ? sv[r] - l2v[r] : -__builtin_inff());
+            p[r] = fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2v[r]) : -__builtin_inff());
             ds[r] = p[r] * (tv[r] - dlv[r]) * scale;
           }
           if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
@@ -868,6 +876,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
   const int D = H * HD;
   const int P = agpt_blk::prefix_cap(pl.max_depth);
   const float qscale = scale * kLog2e;
+  // bf16 scores come unscaled (the fp32 operands are scaled once): the
+  // scale goes into the exponent's multiply-add.
+  const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
   float* const cs = Cs + static_cast<int64_t>(blockIdx.x) * 2 * P * 2 * HD;
   const int64_t n_units = static_cast<int64_t>(pl.n_chunks) * H;
   int* ctr = pl.sched + 2;
@@ -974,13 +985,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
           ga.load(Gs + qr * WS + KD * g);
           f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});
           const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
-          if constexpr (!Slice<Tin, KD>::kPre) sv *= qscale;
           const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
           const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
           float p[4], ds[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
-            p[r] = fast_exp2(live[r] ? sv[r] - l2v[r] : -__builtin_inff());
+            p[r] = fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2v[r]) : -__builtin_inff());
             ds[r] = p[r] * (tv[r] - dlv[r]) * scale;
           }
           if constexpr (sizeof(Tin) == 2) {
