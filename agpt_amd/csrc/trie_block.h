@@ -685,9 +685,14 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
         for (int j = 0; j < MT; ++j) o[e][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
       }
       // The diagonal block first (it holds every row's own key), then the
-      // prefix blocks and the row blocks above the diagonal.
-      for (int n = 0, b = rb0 + i; n <= i + rb0 - pb0; ++n, b = pb0 + n - 1) {
-        if (kBlk * i >= uniform(tb.bhi[b])) continue;  // no live pair
+      // prefix blocks and the row blocks above the diagonal. Which of them
+      // have a live pair is one wave-uniform mask (lane n tests the n-th
+      // block), not an LDS round trip at the top of every block.
+      const int nb = i + rb0 - pb0 + 1;  // <= (P + kTile) / kBlk <= 20
+      const uint32_t bmask = static_cast<uint32_t>(__ballot(
+          lane < nb && kBlk * i < tb.bhi[lane == 0 ? rb0 + i : pb0 + min(lane, nb) - 1]));
+      for (int n = 0, b = rb0 + i; n < nb; ++n, b = pb0 + n - 1) {
+        if (!((bmask >> n) & 1u)) continue;  // no live pair
         const int k0 = kBlk * b;
         const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
         const bool live[4] = {in_interval(q, iv.x), in_interval(q, iv.y), in_interval(q, iv.z),
