@@ -1197,10 +1197,15 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     if constexpr (!kCarry)
       for (int x = lane; x < kTile * HD / 4; x += 64) reinterpret_cast<f4*>(mydq)[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int load0 = 0, load1 = 0, load2 = 0, load3 = 0;
+    // The units' query-block ends, read once: lane u holds unit u's (nu <=
+    // (P + kTile) / kBlk <= 20), taken out with a lane read per unit instead
+    // of an LDS round trip per unit in every wave.
+    const int bh = tb.bhi[pb0 + min(lane, nu - 1)];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): bh is in before the loop
     for (int u = 0; u < nu; ++u) {
       const int b = pb0 + u;
       const int i0 = b < rb0 ? 0 : b - rb0;
-      const int i1 = uniform((tb.bhi[b] + kBlk - 1) / kBlk);
+      const int i1 = (__builtin_amdgcn_readlane(bh, u) + kBlk - 1) / kBlk;
       // Least loaded wave of the head (lowest index on ties) takes the unit.
       const int cost = i1 - i0;
       int w = 0;
