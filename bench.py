@@ -25,6 +25,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = ("trie-attn fwd+bwd node-tokens/sec (1 GPU, depth 32); % of HBM/MFMA roofline")
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0}  # MI355X dense matrix peaks
 
 
 def log(msg: str) -> None:
@@ -862,7 +863,11 @@ def main() -> int:
         },
         "step_roofline": {"bytes_per_node_token": bpt["step"], "achieved_GBps": step_gbs,
                           "frac": step_gbs / HBM_PEAK_GBS,
-                          "tflops_algorithmic": flops / (ms_step * 1e-3) / 1e12},
+                          "tflops_algorithmic": flops / (ms_step * 1e-3) / 1e12,
+                          # the same useful flops against the dense matrix peak of
+                          # the step's input type (plain causal attention's roofline)
+                          "mfma_peak_tflops": MFMA_PEAK_TFLOPS[cfg["dtype"]],
+                          "mfma_frac": flops / (ms_step * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS[cfg["dtype"]]},
         "kernel_avg_ms": avg,
         "cpu_baseline": cpu,
     }
