@@ -694,7 +694,10 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
       for (int n = 0, b = rb0 + i; n < nb; ++n, b = pb0 + n - 1) {
         if (!((bmask >> n) & 1u)) continue;  // no live pair
         const int k0 = kBlk * b;
+        // The interval read is issued ahead of the first K read and product
+        // (the scheduler would put it after the product and wait for it there).
         const int4 iv = *reinterpret_cast<const int4*>(tb.kint + k0 + 4 * g);
+        __builtin_amdgcn_sched_barrier(0);
         const bool live[4] = {in_interval(q, iv.x), in_interval(q, iv.y), in_interval(q, iv.z),
                               in_interval(q, iv.w)};
 #pragma unroll
