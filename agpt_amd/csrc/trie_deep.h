@@ -987,6 +987,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
           const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
           const f4 l2v = *reinterpret_cast<const f4*>(&tb.l2[q0]);
           const f4 dlv = *reinterpret_cast<const f4*>(&tb.dl[q0]);
+          // bf16: the second products' transposed operands are read here,
+          // in the registers the first products' operands free, so the reads
+          // overlap the softmax instead of one wait per product after it.
+          agpt_blk::bf16x4_bits tgv[sizeof(Tin) == 2 ? MT : 1], tqv[sizeof(Tin) == 2 ? MT : 1];
+          if constexpr (sizeof(Tin) == 2) {
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T blocks: dims 16j .., queries 16i ..
+              tgv[j] = read_tr(Gs, WS, kBlk * i, kBlk * j, lane);
+              tqv[j] = read_tr(Qs, WS, kBlk * i, kBlk * j, lane);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
           float p[4], ds[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
@@ -996,9 +1008,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
           if constexpr (sizeof(Tin) == 2) {
             const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
 #pragma unroll
-            for (int j = 0; j < MT; ++j) {  // dO^T, Q^T blocks: dims 16j .., queries 16i ..
-              dv[j] = mfma_a_bf16(read_tr(Gs, WS, kBlk * i, kBlk * j, lane), pw, dv[j]);
-              dk[j] = mfma_a_bf16(read_tr(Qs, WS, kBlk * i, kBlk * j, lane), dw, dk[j]);
+            for (int j = 0; j < MT; ++j) {
+              dv[j] = mfma_a_bf16(tgv[j], pw, dv[j]);
+              dk[j] = mfma_a_bf16(tqv[j], dw, dk[j]);
             }
           } else {
 #pragma unroll
