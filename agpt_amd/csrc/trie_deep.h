@@ -577,6 +577,14 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           for (int r = 0; r < 4; ++r) acc += fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2) : -__builtin_inff()) * tv[r];
           continue;
         }
+        // bf16: the K^T blocks of the dQ product read before the softmax,
+        // so the reads overlap it.
+        agpt_blk::bf16x4_bits tkv[sizeof(Tin) == 2 ? MT : 1];
+        if constexpr (sizeof(Tin) == 2) {
+#pragma unroll
+          for (int j = 0; j < MT; ++j) tkv[j] = read_tr(Ks, WS, kBlk * bl, kBlk * j, lane);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         float ds[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)  // masked: exp2(-inf) = 0, no branch per pair
@@ -584,8 +592,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         if constexpr (sizeof(Tin) == 2) {  // dS rounded to bf16, one 16-deep step per output tile
           const uint2 dw = pack_bf16(ds);
 #pragma unroll
-          for (int j = 0; j < MT; ++j)
-            dq[j] = mfma_a_bf16(read_tr(Ks, WS, kBlk * bl, kBlk * j, lane), dw, dq[j]);
+          for (int j = 0; j < MT; ++j) dq[j] = mfma_a_bf16(tkv[j], dw, dq[j]);
         } else {
 #pragma unroll
           for (int j = 0; j < MT; ++j)
