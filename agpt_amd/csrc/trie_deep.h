@@ -978,9 +978,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
         kf.scale(qscale);
         const int key = kBlk * b + c;
+        // The key's interval and the block's query range read together (the
+        // compiler would sink the interval read past the range's wait).
         const int iv = tb.kint[key];
-        const int i0 = uniform(tb.blo[b]) / kBlk;
-        const int i1 = (uniform(tb.bhi[b]) + kBlk - 1) / kBlk;
+        const int blo = tb.blo[b], bhi = tb.bhi[b];
+        asm volatile("" ::"v"(iv), "v"(blo), "v"(bhi));
+        const int i0 = uniform(blo) / kBlk;
+        const int i1 = (uniform(bhi) + kBlk - 1) / kBlk;
         for (int i = i0; i < i1; ++i) {
           const int qr = kBlk * i + c;
           const int q0 = kBlk * i + 4 * g;
