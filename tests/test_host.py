@@ -226,3 +226,19 @@ def test_new_entry_points_reject_bad_arguments_without_a_device():
     i = lambda *v: np.array(v, np.int32).ctypes.data_as(C.POINTER(C.c_int32))
     assert lib.agpt_loss_mass_weights(i(0), i(5), i(2), i(0, 2), 1, 2, 9,
                                       mass.ctypes.data_as(C.POINTER(C.c_float))) == _native.AGPT_ERR_INVALID_ARG
+
+
+def test_bench_one_gpu_contract():
+    """bench.py refuses --gpus N > 1 with a message (one GPU per box), and
+    has a dense matrix peak for every input type a workload computes in."""
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       cwd=ROOT, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    assert {c["dtype"] for c in trie.CONFIGS.values()} <= set(bench.MFMA_PEAK_TFLOPS)
