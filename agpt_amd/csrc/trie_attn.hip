@@ -1226,9 +1226,10 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
     int cus = 256;
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
     // The deep key side's units are (chunk, head): ~8 per CU, and chunks up
-    // to 48 tiles (fewer chunk partials: C4 83.0 -> 81.6 ms).
+    // to 96 tiles (fewer chunk partials and carry work: C4 83.0 -> 81.6 ms
+    // at 48, the carry kernel 0.70 -> 0.39 ms at 96).
     const int64_t per_claim = h->deep_carry ? static_cast<int64_t>(n_tiles) * h->cfg.n_heads : n_tiles;
-    const int cap = h->deep_carry ? 48 : 24;
+    const int cap = h->deep_carry ? 96 : 24;
     const int dflt = static_cast<int>(std::min<int64_t>(cap, std::max<int64_t>(1, per_claim / (8 * std::max(cus, 1)))));
     h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", dflt));
     h->n_chunks_sched = std::max<int32_t>(1, n_tiles / h->chunk_tiles);
@@ -1493,14 +1494,19 @@ int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds, int hg = 0) {
 
 // Heads per unit of the deep-prefix kernels: all heads of a tile when the
 // plan has tiles enough for ~16 units per CU (tables built once per tile,
-// heads streamed back to back), else two (units enough to fill the chip,
-// each unit's tables shared by two heads; one for an odd head count).
-// AGPT_ATTN_DHPU overrides (a divisor of the head count).
-int deep_heads_per_unit(const agpt_attn_s* h) {
+// heads streamed back to back; half of them in the forward from 8 heads
+// on), else two (units enough to fill the chip, each unit's tables shared
+// by two heads; one for an odd head count). AGPT_ATTN_DHPU overrides (a
+// divisor of the head count).
+int deep_heads_per_unit(const agpt_attn_s* h, bool fwd = false) {
   const int H = h->cfg.n_heads;
   int cus = 256;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
-  int hpu = env_int("AGPT_ATTN_DHPU", h->n_tiles >= 16 * cus ? H : H % 2 == 0 ? 2 : 1);
+  // The forward's units are lighter (no δ pass): with 8 or more heads it
+  // takes half of them per unit, twice the units for the same tables
+  // (C4: fwd 18.3 -> 17.95 ms; the dQ kernel is faster with all heads).
+  const int big = fwd && H >= 8 && H % 2 == 0 ? H / 2 : H;
+  int hpu = env_int("AGPT_ATTN_DHPU", h->n_tiles >= 16 * cus ? big : H % 2 == 0 ? 2 : 1);
   if (hpu < 1 || hpu > H || H % hpu != 0) hpu = 1;
   return hpu;
 }
@@ -1563,7 +1569,7 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if (h->variant == 6 && h->deep) {
     if constexpr (HD == 64) {
       clear_sched(h, st);
-      const int hpu = deep_heads_per_unit(h);
+      const int hpu = deep_heads_per_unit(h, true);
       auto fn = agpt_deep::fwd_kernel<HD, Tin, PlanDev>;
       set_lds(fn, h->fwd_lds);
       hipLaunchKernelGGL(fn, dim3(stream_grid(h, fn, h->fwd_lds, hpu)), dim3(agpt_deep::kThreads), h->fwd_lds, st,
