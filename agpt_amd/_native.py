@@ -59,6 +59,7 @@ ATTN_SYMBOLS = {
     "agpt_attn_plan_static": (C.c_int, [_vp, _i32p, C.c_int64]),
     "agpt_attn_plan_range": (C.c_int, [_vp, _i32p, C.c_int64, C.c_int64, C.c_int64, C.c_int]),
     "agpt_attn_plan_radix": (C.c_int, [_vp, _i32p, _i32p, C.c_int64]),
+    "agpt_attn_radix_rows": (C.c_int, [_i32p, _i32p, C.c_int64, _i32p, C.c_int64, C.POINTER(C.c_int64)]),
     "agpt_attn_plan_info": (C.c_int, [_vp, _i64p, _i64p, _i64p, _i32p]),
     "agpt_attn_describe": (C.c_char_p, [_vp]),
     "agpt_attn_fwd": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.POINTER(AttnOpts)]),

@@ -236,9 +236,16 @@ class RangedTrieAttention:
 
     def __init__(self, n_heads: int, head_dim: int, parent: np.ndarray, ranges, max_depth: int = 32,
                  dtype: torch.dtype = torch.float32):
-        self.ranges = list(ranges)
+        self.ranges = [(int(a), int(b)) for a, b in ranges]
         self.parts = []
         par = np.ascontiguousarray(parent, dtype=np.int32)
+        # Each range adds its share of dK/dV into the rows of earlier ranges,
+        # and the outputs start uninitialised: the ranges must tile the trie
+        # in ascending order from row 0.
+        if not self.ranges or self.ranges[0][0] != 0 or self.ranges[-1][1] != par.shape[0] or any(
+                b <= a for a, b in self.ranges) or any(
+                self.ranges[i][1] != self.ranges[i + 1][0] for i in range(len(self.ranges) - 1)):
+            raise ValueError("ranges must be non-empty, contiguous, ascending, start at row 0 and end at n_nodes")
         for a, b in self.ranges:
             att = TrieAttention(n_heads, head_dim, max_depth=max_depth, dtype=dtype)
             att.plan_range(par, a, b)

@@ -1350,40 +1350,63 @@ extern "C" int agpt_attn_plan_static(agpt_attn_handle h, const int32_t* parent, 
   int rc = scratch_base(h->device, &ar.base);
   if (rc != AGPT_OK) return rc;
   {
-    // Claim the scratch first: an earlier static plan on this device stops
-    // being valid whatever happens next.
+    // Claim the scratch and upload into it under one lock: an earlier static
+    // plan on this device stops being valid whatever happens next, and two
+    // threads planning static on one device never write the scratch at once
+    // (the later claim's tables are the ones left in it).
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     h->static_gen = ++g_scratch_gen[h->device];
+    rc = plan_impl(h, parent, n, 0, {}, ar);
   }
-  rc = plan_impl(h, parent, n, 0, {}, ar);
   if (rc != AGPT_OK) free_plan(h);
   h->row_off = 0;
   h->n_ctx = 0;
   return rc;
 }
 
-extern "C" int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_parent,
-                                    const int32_t* edge_len, int64_t n_radix) {
-  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
-  if (n_radix < 1 || !radix_parent || !edge_len)
+// The radix tree's node-token rows: node r's edge rows follow each other,
+// the first one's parent being the last row of radix_parent[r]'s edge.
+extern "C" int agpt_attn_radix_rows(const int32_t* radix_parent, const int32_t* edge_len, int64_t n_radix,
+                                    int32_t* parent_out, int64_t cap, int64_t* n_rows) {
+  if (n_radix < 1 || !radix_parent || !edge_len || !n_rows)
     return set_error(AGPT_ERR_INVALID_ARG, "empty radix tree or null table");
-  std::vector<int64_t> last_row(static_cast<size_t>(n_radix));
-  std::vector<int32_t> parent;
+  int64_t rows = 0;
   for (int64_t r = 0; r < n_radix; ++r) {
     const int32_t rp = radix_parent[r];
     if (rp < -1 || rp >= r)
       return set_error(AGPT_ERR_NOT_DFS, "radix_parent[%lld] = %d is not an earlier node or -1",
                        (long long)r, rp);
     if (edge_len[r] < 1) return set_error(AGPT_ERR_INVALID_ARG, "edge_len[%lld] = %d", (long long)r, edge_len[r]);
-    int64_t prev = rp < 0 ? -1 : last_row[rp];
-    for (int j = 0; j < edge_len[r]; ++j) {
-      parent.push_back(static_cast<int32_t>(prev));
-      prev = static_cast<int64_t>(parent.size()) - 1;
-      if (prev >= (int64_t{1} << 31) - kMaxTileRows) return set_error(AGPT_ERR_INVALID_ARG, "too many rows");
+    rows += edge_len[r];
+    if (rows >= (int64_t{1} << 31) - kMaxTileRows)
+      return set_error(AGPT_ERR_INVALID_ARG, "more than 2^31 rows by radix node %lld", (long long)r);
+  }
+  *n_rows = rows;
+  if (!parent_out) return AGPT_OK;
+  if (cap < rows) return set_error(AGPT_ERR_INVALID_ARG, "cap %lld < %lld rows", (long long)cap, (long long)rows);
+  std::vector<int32_t> last_row(static_cast<size_t>(n_radix));
+  int32_t next = 0;
+  for (int64_t r = 0; r < n_radix; ++r) {
+    int32_t prev = radix_parent[r] < 0 ? -1 : last_row[radix_parent[r]];
+    for (int32_t j = 0; j < edge_len[r]; ++j, ++next) {
+      parent_out[next] = prev;
+      prev = next;
     }
     last_row[r] = prev;
   }
-  return agpt_attn_plan(h, parent.data(), static_cast<int64_t>(parent.size()));
+  return AGPT_OK;
+}
+
+extern "C" int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_parent,
+                                    const int32_t* edge_len, int64_t n_radix) {
+  if (!h) return set_error(AGPT_ERR_INVALID_ARG, "null handle");
+  int64_t rows = 0;
+  int rc = agpt_attn_radix_rows(radix_parent, edge_len, n_radix, nullptr, 0, &rows);
+  if (rc != AGPT_OK) return rc;
+  std::vector<int32_t> parent(static_cast<size_t>(rows));
+  if ((rc = agpt_attn_radix_rows(radix_parent, edge_len, n_radix, parent.data(), rows, &rows)) != AGPT_OK)
+    return rc;
+  return agpt_attn_plan(h, parent.data(), rows);
 }
 
 extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {

@@ -143,8 +143,10 @@ int agpt_attn_plan_range(agpt_attn_handle h, const int32_t* parent, int64_t n_to
 #define AGPT_STATIC_SCRATCH_BYTES (64u << 20)
 
 /* No counterpart in the reference: for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). Same contract and results as agpt_attn_plan, but every
+ * memory (tight serving loops, harnesses that forbid hipMalloc, code that
+ * captures fwd/bwd into a HIP graph: plan before the capture, since the
+ * uploads here are synchronous hipMemcpy calls, which a capture does not
+ * allow; fwd/bwd of the plan may then be captured). Same contract and results as agpt_attn_plan, but every
  * device table and workspace of the plan is placed in a static array of the
  * library (AGPT_STATIC_SCRATCH_BYTES = 64 MiB per device, held until the
  * process ends) instead of being allocated: the call makes no hipMalloc or
@@ -165,6 +167,16 @@ int agpt_attn_plan_static(agpt_attn_handle h, const int32_t* parent, int64_t n_n
  * as parent. Row order: radix nodes in order, edge rows in order. */
 int agpt_attn_plan_radix(agpt_attn_handle h, const int32_t* radix_parent,
                          const int32_t* edge_len, int64_t n_radix);
+
+/* Host-only: the node-token rows of a radix tree, as agpt_attn_plan_radix
+ * plans them (the ancestor chains of agpt_train.cu:892-940 expanded into one
+ * parent per row). Writes *n_rows = Σ edge_len and, if parent_out is
+ * non-NULL, the rows' parent table (cap entries at most: a smaller cap
+ * returns AGPT_ERR_INVALID_ARG after setting *n_rows). Errors: AGPT_ERR_NOT_DFS
+ * for a radix_parent that is not an earlier node or -1, AGPT_ERR_INVALID_ARG
+ * for edge_len < 1 or more than 2^31 rows. No device calls. */
+int agpt_attn_radix_rows(const int32_t* radix_parent, const int32_t* edge_len, int64_t n_radix,
+                         int32_t* parent_out, int64_t cap, int64_t* n_rows);
 
 /* Planned batch statistics (host values): node-tokens T, number of tiles,
  * sum of depths (keys attended, Σp), maximum depth. Any pointer may be NULL. */

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 from helpers import (ATOL_BF16, ATOL_F32, RTOL_BF16, RTOL_F32, assert_close, assert_close_or_f64,
-                     f64_key_grads, round_bf16, scale_of, small_trie, tensors)
+                     abs_terms, assert_close_terms, f64_key_grads, round_bf16, run_gpu, run_gpu_ranges, scale_of,
+                     small_trie, tensors)
 from oracle import oracle as ORC
 
 pytestmark = pytest.mark.gpu
@@ -28,8 +29,8 @@ VARIANTS = {
                                    "AGPT_ATTN_FUH": "4", "AGPT_ATTN_CHUNK": "1"},
     "block_fwd_one_head_units": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_FUH": "1"},
     "block_whole_key_set": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_DEEP": "0"},
-    "block_deep_heads_per_unit2": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_DHPU": "2"},
-    "block_deep_carry_rows_only": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_REGCARRY": "0"},
+    "block_deep_heads_per_unit1": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_DHPU": "1"},
+    "block_deep_carry_rows_only": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_REGCARRY": "0", "AGPT_ATTN_CHUNK": "2"},
     "block_deep_claims_in_tile_order": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_LPT": "0"},
     "chain": {"AGPT_ATTN_VARIANT": "5"},
     "chain_hg1_qb1_kb1": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "1", "AGPT_ATTN_QB": "1",
@@ -54,90 +55,6 @@ def variant(request, monkeypatch):
     return request.param
 
 
-def _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=None, acc=None, max_depth=None):
-    import torch
-
-    from agpt_amd.attention import TrieAttention, rope_tables
-
-    dev = torch.device("cuda:0")
-    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-    md = max_depth or max(1, int(ORC.depths(tr_parent).max()))
-    att = TrieAttention(H, hd, max_depth=md, dtype=tdt)
-    att.plan(tr_parent)
-    print("kernel:", att.describe())
-    q, k, v, g = (torch.from_numpy(x).to(dev).to(tdt).contiguous() for x in (Q, K, V, G))
-    o, lse = att.forward(q, k, v)
-    rt = None
-    if rope is not None:
-        rt = tuple(torch.from_numpy(x).to(dev).contiguous() for x in rope)
-    acc_t = [None, None]
-    if acc is not None:
-        acc_t = [torch.from_numpy(x).to(dev).contiguous() for x in acc]
-    dq, dk, dv = att.backward(q, k, v, o, lse, g, acc_dk=acc_t[0], acc_dv=acc_t[1], rope=rt)
-    torch.cuda.synchronize()
-    res = [x.float().cpu().numpy() for x in (o, lse, dq, dk, dv)]
-    att.close()
-    return res
-
-
-def _run_gpu_ranges(tr_parent, Q, K, V, G, H, hd, dtype, ranges, packed, rope=None, acc=None, max_depth=None):
-    """The trie as contiguous row ranges, one plan each, in ascending order.
-    Whole-trie tensors (packed=False), or per range a packed copy [context
-    rows, range rows] whose context dK/dV share is added to the owner rows
-    here, in range order."""
-    import torch
-
-    from agpt_amd.attention import RangedTrieAttention, TrieAttention
-
-    dev = torch.device("cuda:0")
-    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
-    md = max_depth or max(1, int(ORC.depths(tr_parent).max()))
-    T, D = tr_parent.shape[0], H * hd
-    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
-    rt = None if rope is None else tuple(cu(x) for x in rope)
-    if not packed:
-        ratt = RangedTrieAttention(H, hd, tr_parent, ranges, max_depth=md, dtype=tdt)
-        print("kernel:", ratt.parts[-1].describe())
-        q, k, v, g = (cu(x).to(tdt).contiguous() for x in (Q, K, V, G))
-        o, lse = ratt.forward(q, k, v)
-        ak = None if acc is None else cu(acc[0])
-        av = None if acc is None else cu(acc[1])
-        dq, dk, dv = ratt.backward(q, k, v, o, lse, g, acc_dk=ak, acc_dv=av, rope=rt)
-        torch.cuda.synchronize()
-        res = [x.float().cpu().numpy() for x in (o, lse, dq, dk, dv)]
-        ratt.close()
-        return res
-    out = [np.zeros((T, D), np.float32), np.zeros((T, H), np.float32)] + [np.zeros((T, D), np.float64)
-                                                                         for _ in range(3)]
-    for a, b in ranges:
-        ctx = []
-        x = int(tr_parent[a])
-        while x >= 0:
-            ctx.append(x)
-            x = int(tr_parent[x])
-        rows = np.concatenate([np.array(ctx[::-1], np.int64), np.arange(a, b)])
-        nc = len(ctx)
-        att = TrieAttention(H, hd, max_depth=md, dtype=tdt)
-        att.plan_range(tr_parent, a, b, packed=True)
-        assert att.n_ctx == nc
-        q, k, v, g = (cu(x[rows]).to(tdt).contiguous() for x in (Q, K, V, G))
-        g[:nc] = 0  # context rows are not queries: their dO is unused
-        o, lse = att.forward(q, k, v)
-        ak = av = None
-        if acc is not None:  # the owner batch adds a row's seeds, context rows get none
-            ak, av = (cu(np.concatenate([np.zeros((nc, D), np.float32), s[a:b]])) for s in acc)
-        dq, dk, dv = att.backward(q, k, v, o, lse, g, acc_dk=ak, acc_dv=av, rope=rt)
-        torch.cuda.synchronize()
-        o, lse, dq, dk, dv = (x.float().cpu().numpy() for x in (o, lse, dq, dk, dv))
-        out[0][a:b], out[1][a:b], out[2][a:b] = o[nc:], lse[nc:], dq[nc:]
-        out[3][a:b] += dk[nc:]
-        out[4][a:b] += dv[nc:]
-        out[3][rows[:nc]] += dk[:nc]  # the range's share of its context rows, to their owners
-        out[4][rows[:nc]] += dv[:nc]
-        att.close()
-    return out
-
-
 def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0, normwise=False,
            ranges=None, packed=False):
     T = tr_parent.shape[0]
@@ -152,23 +69,32 @@ def _check(tr_parent, H, hd, seed, dtype="f32", rope=False, acc=False, sharp=1.0
         rng = np.random.default_rng(seed + 99)
         accs = [rng.standard_normal((T, D)).astype(np.float32) * np.float32(0.1) for _ in range(2)]
     if ranges is None:
-        o, lse, dq, dk, dv = _run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=rope_t, acc=accs)
+        o, lse, dq, dk, dv = run_gpu(tr_parent, Q, K, V, G, H, hd, dtype, rope=rope_t, acc=accs)
     else:
-        o, lse, dq, dk, dv = _run_gpu_ranges(tr_parent, Q, K, V, G, H, hd, dtype, ranges, packed, rope=rope_t,
+        o, lse, dq, dk, dv = run_gpu_ranges(tr_parent, Q, K, V, G, H, hd, dtype, ranges, packed, rope=rope_t,
                                              acc=accs)
     Oo, W, lse_o = ORC.fwd(tr_parent, Q, K, V, H, hd, scale)
     if dtype == "bf16":
         rtol, atol = RTOL_BF16, ATOL_BF16
     else:
         rtol, atol = RTOL_F32, ATOL_F32
-    # Sharp softmax (large scores) makes dK/dV sums of terms far larger than
-    # the result; there the relative bound is taken normwise per (row, head).
-    rs = hd if (sharp > 1.0 or dtype == "bf16" or normwise) else None
-    assert_close(o, Oo, rtol, atol, "O", row_scale=rs)
-    assert_close(lse, lse_o, rtol, atol, "lse")
     dQ, dK, dV = ORC.bwd(tr_parent, Q, K, V, W, G, H, hd, scale,
                          acc_dk=None if accs is None else accs[0],
                          acc_dv=None if accs is None else accs[1], rope=rope_t)
+    assert_close(lse, lse_o, rtol, atol, "lse")
+    if dtype == "bf16":
+        # elementwise; an element whose terms cancel is held to the bar
+        # relative to the sum of its terms' magnitudes (P and dS are rounded
+        # to bf16 before the second products)
+        terms = lambda kind: (lambda rows: abs_terms(kind, tr_parent, Q, K, V, G, W, H, hd, scale, rows,
+                                                     rope=rope_t, acc=accs))
+        for name, got, want in (("O", o, Oo), ("dQ", dq, dQ), ("dK", dk, dK), ("dV", dv, dV)):
+            assert_close_terms(got, want, terms(name), rtol, atol, name)
+        return
+    # Sharp softmax (large scores) makes dK/dV sums of terms far larger than
+    # the result; there the relative bound is taken normwise per (row, head).
+    rs = hd if (sharp > 1.0 or normwise) else None
+    assert_close(o, Oo, rtol, atol, "O", row_scale=rs)
     assert_close(dq, dQ, rtol, atol, "dQ", row_scale=rs)
     if rs is None:
         # fp32: elementwise against the oracle, or for a key whose subtree

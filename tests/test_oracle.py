@@ -444,3 +444,29 @@ def test_planted_mistakes_are_caught():
     assert fails(run(parent=np.full(T, -1, np.int32)))      # ancestors dropped
     Qh = Q.reshape(T, H, hd)[:, ::-1].reshape(T, D).copy()  # heads swapped
     assert fails(run(q=Qh))
+
+
+def test_abs_terms_bound_the_oracle():
+    """The bf16 bar's term magnitudes (helpers.abs_terms): every oracle
+    element is at most its sum of |terms| (triangle inequality), with
+    equality where all terms are non-negative (V >= 0 for O, dO >= 0 for
+    dV), with RoPE and accumulators."""
+    from helpers import abs_terms, scale_of, small_trie, tensors
+    tr = small_trie(n_tokens=300, depth=9, seed=5)
+    T, H, hd = tr.n_nodes, 2, 8
+    Q, K, V, G = tensors(T, H * hd, 3)
+    acc = tensors(T, H * hd, 4, n=2)
+    scale = scale_of(hd)
+    rope = ORC.rope_table(16, hd)
+    rows = np.arange(T)
+    for pos in (False, True):
+        Vx, Gx = (np.abs(V), np.abs(G)) if pos else (V, G)
+        O, W, _ = ORC.fwd(tr.parent, Q, K, Vx, H, hd, scale)
+        dQ, dK, dV = ORC.bwd(tr.parent, Q, K, Vx, W, Gx, H, hd, scale, acc_dk=acc[0],
+                             acc_dv=np.abs(acc[1]) if pos else acc[1], rope=rope)
+        for kind, x in (("O", O), ("dQ", dQ), ("dK", dK), ("dV", dV)):
+            t = abs_terms(kind, tr.parent, Q, K, Vx, Gx, W, H, hd, scale, rows, rope=rope,
+                          acc=(acc[0], np.abs(acc[1]) if pos else acc[1]))
+            assert (np.abs(x) <= t * (1 + 1e-5) + 1e-6).all(), kind
+            if pos and kind in ("O", "dV"):
+                np.testing.assert_allclose(t, x, rtol=1e-5, atol=1e-6)

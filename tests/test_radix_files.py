@@ -140,3 +140,60 @@ def test_subtree_groups_cover_the_rows_in_order():
         assert all(b - a <= max_rows or len([r for r in roots if a < r < b]) == 0 for a, b in g)
     empty = trie.build_trie(np.zeros(1, np.int32), 4, counts=True)
     assert model.subtree_groups(empty, 10) == []
+
+
+def _radix_rows(rp, el, cap=None):
+    import ctypes as C
+
+    from agpt_amd import _native
+    lib = _native.attn_lib()
+    rp = np.ascontiguousarray(rp, np.int32)
+    el = np.ascontiguousarray(el, np.int32)
+    n = C.c_int64(-1)
+    i32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
+    rc = lib.agpt_attn_radix_rows(i32(rp), i32(el), rp.shape[0], None, 0, C.byref(n))
+    if rc:
+        return rc, None, lib.agpt_last_error().decode()
+    out = np.full(n.value if cap is None else cap, -7, np.int32)
+    rc = lib.agpt_attn_radix_rows(i32(rp), i32(el), rp.shape[0], i32(out), out.shape[0], C.byref(n))
+    return rc, out[:n.value], lib.agpt_last_error().decode()
+
+
+def test_radix_rows_of_written_files_equal_the_trie(tmp_path):
+    """agpt_attn_radix_rows, the row expansion agpt_attn_plan_radix plans
+    from (agpt_train.cu:892-940 chains), turns each subtree file's radix
+    tables into the node-token parent table of the trie the files were
+    written from (an independent vectorised expansion, RadixSubtree.rows,
+    and the builder's own trie)."""
+    from agpt_amd import _native
+
+    tok = trie.markov_corpus(5000, 3, 9, 1.1, seed=21)
+    trie.write_radix_files(tok, 16, str(tmp_path), 9)
+    tr = trie.build_radix_trie(tok, 16)
+    rows, base = [], 0
+    for rc, _, chars, _ in trie.read_radix_manifest(str(tmp_path / "manifest.bin")):
+        st = trie.read_radix_subtree(str(tmp_path / "subtrees" / f"radix_subtree_{rc:06d}.bin"))
+        code, par, _ = _radix_rows(st.radix_parent, st.edge_len)
+        assert code == _native.AGPT_OK and par.shape[0] == chars
+        assert (par == st.rows()[0]).all()
+        rows.append(np.where(par < 0, -1, par + base))
+        base += chars
+    assert (np.concatenate(rows) == tr.parent).all()
+
+
+def test_radix_rows_errors():
+    from agpt_amd import _native
+    ok, par, _ = _radix_rows([-1, 0, 0, -1], [2, 1, 3, 1])
+    assert ok == _native.AGPT_OK and par.tolist() == [-1, 0, 1, 1, 3, 4, -1]
+    code, _, msg = _radix_rows([-1, 1], [1, 1])           # a parent that is not an earlier node
+    assert code == _native.AGPT_ERR_NOT_DFS and "radix_parent[1]" in msg
+    code, _, msg = _radix_rows([-1, -2], [1, 1])
+    assert code == _native.AGPT_ERR_NOT_DFS
+    code, _, msg = _radix_rows([-1, 0], [1, 0])           # an empty edge
+    assert code == _native.AGPT_ERR_INVALID_ARG and "edge_len[1] = 0" in msg
+    code, _, msg = _radix_rows([-1, 0], [3, -2])
+    assert code == _native.AGPT_ERR_INVALID_ARG
+    code, _, msg = _radix_rows([-1, 0], [2, 2], cap=3)   # output too small
+    assert code == _native.AGPT_ERR_INVALID_ARG and "cap" in msg
+    code, _, _ = _radix_rows(np.zeros(0, np.int32), np.zeros(0, np.int32))
+    assert code == _native.AGPT_ERR_INVALID_ARG

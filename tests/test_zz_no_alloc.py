@@ -2,9 +2,10 @@
 and workspace live in the library's static scratch) against agpt_attn_plan,
 through the C ABI: two static plans in a row on one handle, the second with
 a smaller trie, each followed by fwd + bwd, give the same bytes as the
-allocating plan; a later static plan on the device invalidates an earlier
-handle's; a batch past the scratch is refused with its size; a handle with
-an allocated plan is refused."""
+allocating plan, and free device memory (hipMemGetInfo) is the same before
+and after them (inputs and outputs allocated beforehand); a later static
+plan on the device invalidates an earlier handle's; a batch past the scratch
+is refused with its size; a handle with an allocated plan is refused."""
 from __future__ import annotations
 
 import numpy as np
@@ -15,14 +16,24 @@ from helpers import scale_of, tensors
 pytestmark = pytest.mark.gpu
 
 
-def _fwd_bwd(att, T, D, seed, rope):
+def _inputs(T, D, seed):
     import torch
     Q, K, V, G = (torch.from_numpy(x).cuda() for x in tensors(T, D, seed))
     acc = [torch.from_numpy(x).cuda() for x in tensors(T, D, seed + 1, n=2)]
-    o, lse = att.forward(Q, K, V)
-    dq, dk, dv = att.backward(Q, K, V, o, lse, G, acc_dk=acc[0], acc_dv=acc[1], rope=rope)
-    torch.cuda.synchronize()
-    return [x.clone() for x in (o, lse, dq, dk, dv)]
+    return Q, K, V, G, acc
+
+
+def _outputs(T, D, H):
+    import torch
+    return [torch.empty(T, D, device="cuda"), torch.empty(T, H, device="cuda")] + \
+        [torch.empty(T, D, device="cuda") for _ in range(3)]
+
+
+def _fwd_bwd(att, inp, out, rope):
+    Q, K, V, G, acc = inp
+    o, lse, dq, dk, dv = out
+    att.forward(Q, K, V, out=o, lse=lse)
+    att.backward(Q, K, V, o, lse, G, acc_dk=acc[0], acc_dv=acc[1], rope=rope, out=(dq, dk, dv))
 
 
 @pytest.mark.parametrize("H,hd", [(8, 16), (2, 64)])
@@ -37,16 +48,28 @@ def test_plan_static_matches_plan(gpu, H, hd):
     big = trie.config_trie("C2", scale=0.0015)     # ~40K node-tokens, depth 32
     small = trie.config_trie("C1", scale=0.002)    # a few thousand
     assert small.n_nodes < big.n_nodes
+    cases = [(tr, _inputs(tr.n_nodes, D, seed), _outputs(tr.n_nodes, D, H)) for tr, seed in ((big, 1), (small, 2))]
     st = TrieAttention(H, hd, max_depth=32)
-    for tr, seed in ((big, 1), (small, 2)):
+    # a first static plan and run loads the code objects and looks the
+    # scratch up; what follows must not change free device memory
+    st.plan_static(small.parent)
+    _fwd_bwd(st, cases[1][1], cases[1][2], rope)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for tr, inp, out in cases:  # two calls in a row, the second smaller
         st.plan_static(tr.parent)
-        got = _fwd_bwd(st, tr.n_nodes, D, seed, rope)
+        _fwd_bwd(st, inp, out, rope)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0, f"device memory allocated (T={tr.n_nodes})"
+    for tr, inp, g in cases:
         ref = TrieAttention(H, hd, max_depth=32)
         ref.plan(tr.parent)
-        want = _fwd_bwd(ref, tr.n_nodes, D, seed, rope)
+        want = _outputs(tr.n_nodes, D, H)
+        _fwd_bwd(ref, inp, want, rope)
+        torch.cuda.synchronize()
         ref.close()
-        for name, g, w in zip(("O", "lse", "dQ", "dK", "dV"), got, want):
-            assert torch.equal(g, w), f"{name} differs (T={tr.n_nodes})"
+        for name, a, b in zip(("O", "lse", "dQ", "dK", "dV"), g, want):
+            assert torch.equal(a, b), f"{name} differs (T={tr.n_nodes})"
     st.close()
 
 
