@@ -29,6 +29,7 @@ using namespace agpt;
 namespace {
 
 constexpr int kMaxPackedLen = 4096;  // LDS bound of the L-query backward
+typedef float f4 __attribute__((ext_vector_type(4)));
 
 int vset_error(int code, const char* msg) { return agpt_internal_set_error(code, msg); }
 
@@ -356,6 +357,344 @@ __global__ __launch_bounds__(64) void varlen_L_bwd_kernel(
   }
 }
 
+// L-query kernels over radix nodes, on 16x16 fp32 matrix instructions. A
+// wave owns the radix nodes whose first query lies in its block of 64
+// queries (one ballot finds them; a node's queries may run past the block),
+// so no launch slot is spent on a query that is not a node's first, and
+// takes each node one head at a time in 16x16 blocks of (query, packed row).
+// Query j of a node with L queries and len packed rows sees rows
+// p <= len - L + j (agpt_train.cu:3106-3117).
+//
+// v_mfma_f32_16x16x4f32: D[16][16] += A[16][4] B[4][16]; lane l = 16g + c
+// supplies A[c][g], B[g][c] and holds D[4g + r][c] in register r. For a
+// contraction over head dims, step j pairs lane group g with dim KD g + j
+// (KD = HD / 4: each lane reads one contiguous slice of a row); over the 16
+// rows or queries of a block, step j pairs group g with index 4g + j, which
+// is the D layout, so a product's registers feed the next one directly.
+constexpr int kLqMaxDelta = 1024;  // queries per node in the backward's per-wave δ table (LDS)
+
+// Bit mask of the lanes whose query t = base + lane is its radix node's first.
+__device__ __forceinline__ uint64_t node_starts(const int* __restrict__ q2n, const int* __restrict__ qoff,
+                                                int64_t base, int T_q) {
+  const int64_t t = base + (threadIdx.x & 63);
+  bool first = false;
+  if (t < T_q) first = qoff[q2n[t]] == t;
+  return __ballot(first);
+}
+
+__device__ __forceinline__ f4 lq_mfma(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// Max / sum over the four lane groups (lanes c, c+16, c+32, c+48).
+__device__ __forceinline__ float lq_gmax(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float lq_gsum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+__device__ __forceinline__ double lq_gsum_d(double x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+// S^T = X_b Y_i^T of one 16x16 block: X rows (packed rows) are the A side,
+// Y rows (queries) the B side; this lane supplies KD dims (from KD g) of its
+// X row at xrow and holds its Y row's slice y. s[r]: packed row 4g + r
+// against query c.
+template <int HD>
+__device__ __forceinline__ f4 lq_rows_dot(const float* __restrict__ xrow, const float (&y)[HD / 4], int g) {
+  constexpr int KD = HD / 4;
+  float x[KD];
+  load_vec<KD>(xrow + KD * g, x);
+  f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < KD; ++j) acc = lq_mfma(x[j], y[j], acc);
+  return acc;
+}
+// Weights of rows p0 .. p0+3 of one query's row (entries from vis on read
+// as 0): one 16-byte load when the rows are 16-byte aligned (max_len a
+// multiple of 4, p0 a multiple of 4), else one load per visible entry.
+__device__ __forceinline__ void lq_weights4(const float* __restrict__ wrow, int p0, bool vec, int vis,
+                                            float (&w)[4]) {
+  if (vec && p0 + 4 <= vis) {
+    const f4 x = *reinterpret_cast<const f4*>(wrow + p0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) w[r] = x[r];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) w[r] = p0 + r < vis ? wrow[p0 + r] : 0.0f;
+  }
+}
+
+// Score blocks a first pass keeps in registers for the second (rows beyond
+// 16 * kLqCache are recomputed).
+constexpr int kLqCache = 4;
+
+// Forward. A wave takes one head of the nodes that start in its query
+// block. Per (node, query block i): a first pass over the visible packed-row
+// blocks takes each query's maximum and sum (S^T blocks: query c in lane
+// column c, rows in registers), a second recomputes S^T, writes the
+// normalized weights (visible entries only) and adds O^T += V^T P^T.
+template <int HD>
+__global__ __launch_bounds__(256) void varlen_Lq_fwd_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const int* __restrict__ q2n, const int* __restrict__ qoff, const int* __restrict__ kv_off,
+    const int* __restrict__ kv_len, float* __restrict__ out, float* __restrict__ weights, int T_q, int H,
+    int max_len, float scale) {
+  constexpr int MT = HD / 16;
+  // wave = (block of 64 queries, head)
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t base = wid / H * 64;
+  const int h = static_cast<int>(wid - wid / H * H);
+  if (base >= T_q) return;  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  uint64_t starts = node_starts(q2n, qoff, base, T_q);
+  const float qs = scale * kLog2e;
+  const int RS = H * HD;         // row stride of q / k / v / out
+  const int WS = H * max_len;    // query stride of the weights
+  const bool wvec = (max_len & 3) == 0;  // weight rows 16-byte aligned
+  while (starts) {
+    const int64_t t0 = base + __builtin_ctzll(starts);
+    starts &= starts - 1;
+    const int node = q2n[t0];
+    const int L = qoff[node + 1] - static_cast<int>(t0);
+    const int len = min(kv_len[node], max_len);
+    if (L < 1 || L > max_len || len < 1) continue;  // inconsistent tables
+    const int64_t off = kv_off[node];
+    const float* qh = q + (t0 * H + h) * HD;  // query j of the node at qh + j RS
+    float* oh = out + (t0 * H + h) * HD;
+    float* wh = weights + (t0 * H + h) * max_len;
+    const float* kh = k + (off * H + h) * HD;  // packed row p at kh + p RS
+    const float* vh = v + (off * H + h) * HD;
+    const int shift = len - L;  // query j sees rows p <= shift + j
+    for (int i = 0; i < L; i += 16) {
+      const int jq = i + c;  // this lane's query (column)
+      const bool qok = jq < L;
+      float qy[HD / 4];
+      load_vec<HD / 4>(qh + (qok ? jq : 0) * RS + (HD / 4) * g, qy);
+      const int pend = min(len, shift + i + 16);  // rows any query of the block sees
+      float m = -INFINITY, l = 0.0f;
+      f4 sc[kLqCache];
+#pragma unroll
+      for (int x = 0; x < kLqCache; ++x) sc[x] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int b = 0; b < pend; b += 16) {
+        const f4 sv0 = lq_rows_dot<HD>(kh + min(b + c, len - 1) * RS, qy, g);
+#pragma unroll
+        for (int x = 0; x < kLqCache; ++x)
+          if (b == 16 * x) sc[x] = sv0;
+        float sv[4], bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int p = b + 4 * g + r;
+          sv[r] = (qok && p < len && p <= shift + jq) ? sv0[r] * qs : -INFINITY;
+          bm = fmaxf(bm, sv[r]);
+        }
+        const float mn = fmaxf(m, lq_gmax(bm));
+        float e = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e += sv[r] == -INFINITY ? 0.0f : fast_exp2(sv[r] - mn);
+        l = (m == -INFINITY ? 0.0f : l * fast_exp2(m - mn)) + lq_gsum(e);
+        m = mn;
+      }
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      f4 o[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      float* wrow = wh + static_cast<int64_t>(qok ? jq : 0) * WS;
+      for (int b = 0; b < pend; b += 16) {
+        // V^T operand first: lane (g, c) supplies V[row b + 4g + j][dim 16t + c]
+        float vt[MT][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) vt[t][j] = vh[min(b + 4 * g + j, len - 1) * RS + 16 * t + c];
+        f4 sv = sc[0];
+#pragma unroll
+        for (int x = 1; x < kLqCache; ++x)
+          if (b == 16 * x) sv = sc[x];
+        if (b >= 16 * kLqCache) sv = lq_rows_dot<HD>(kh + min(b + c, len - 1) * RS, qy, g);
+        float pw[4];
+        const int vis = qok ? min(len, shift + jq + 1) : 0;  // this query's visible rows
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pw[r] = b + 4 * g + r < vis ? fast_exp2(sv[r] * qs - m) * inv : 0.0f;
+        if (wvec && b + 4 * g + 4 <= vis) {
+          *reinterpret_cast<f4*>(wrow + b + 4 * g) = f4{pw[0], pw[1], pw[2], pw[3]};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (b + 4 * g + r < vis) wrow[b + 4 * g + r] = pw[r];
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[t] = lq_mfma(vt[t][j], pw[j], o[t]);
+      }
+      // O^T[dim 16t + 4g + r][query c]
+      if (qok)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) *reinterpret_cast<f4*>(oh + jq * RS + 16 * t + 4 * g) = o[t];
+    }
+  }
+}
+
+// Backward from the saved weights; a wave takes one head of the nodes that
+// start in its query block. Query side, per query block: dW^T = V dO^T
+// blocks and the weights give δ_j = Σ_p w_jp dW_jp, accumulated in float64
+// (batched_depth_backward.cr:637-651) and kept in the wave's LDS table; a
+// second pass forms dS^T = w (dW - δ) scale (float64, rounded once) and
+// dQ^T += K^T dS^T. Key side, per packed-row block: dW blocks in the other
+// orientation (row c in lane column c), dS with the table's δ, dV^T +=
+// dO^T P and dK^T += Q^T dS over the node's query blocks in order, added
+// into dk_full / dv_full — each row of a node has one owner lane, so there
+// are no atomics.
+template <int HD>
+__global__ __launch_bounds__(256) void varlen_Lq_bwd_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ weights, const float* __restrict__ d_out, const int* __restrict__ q2n,
+    const int* __restrict__ qoff, const int* __restrict__ kv_off, const int* __restrict__ kv_len,
+    float* __restrict__ dq, float* __restrict__ dk, float* __restrict__ dv, int T_q, int H, int max_len,
+    float scale) {
+  constexpr int MT = HD / 16;
+  extern __shared__ double lq_delta[];
+  double* delta = lq_delta + (threadIdx.x >> 6) * max_len;
+  // wave = (block of 64 queries, head)
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t base = wid / H * 64;
+  const int h = static_cast<int>(wid - wid / H * H);
+  if (base >= T_q) return;  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  uint64_t starts = node_starts(q2n, qoff, base, T_q);
+  const double dscale = static_cast<double>(scale);
+  const int RS = H * HD;       // row stride of q / k / v / d_out / dq / dk / dv
+  const int WS = H * max_len;  // query stride of the weights
+  const bool wvec = (max_len & 3) == 0;  // weight rows 16-byte aligned
+  while (starts) {
+    const int64_t t0 = base + __builtin_ctzll(starts);
+    starts &= starts - 1;
+    const int node = q2n[t0];
+    const int L = qoff[node + 1] - static_cast<int>(t0);
+    const int len = min(kv_len[node], max_len);
+    if (L < 1 || L > max_len || len < 1) continue;  // inconsistent tables: δ holds max_len queries
+    const int64_t off = kv_off[node];
+    const float* qh = q + (t0 * H + h) * HD;  // query j of the node at + j RS
+    const float* gh = d_out + (t0 * H + h) * HD;
+    float* dqh = dq + (t0 * H + h) * HD;
+    const float* wh = weights + (t0 * H + h) * max_len;
+    const float* kh = k + (off * H + h) * HD;  // packed row p at + p RS
+    const float* vh = v + (off * H + h) * HD;
+    float* dkh = dk + (off * H + h) * HD;
+    float* dvh = dv + (off * H + h) * HD;
+    const int shift = len - L;
+    // ---- query side: δ and dQ
+    for (int i = 0; i < L; i += 16) {
+      const int jq = i + c;
+      const bool qok = jq < L;
+      float gy[HD / 4];
+      load_vec<HD / 4>(gh + (qok ? jq : 0) * RS + (HD / 4) * g, gy);
+      const float* wrow = wh + static_cast<int64_t>(qok ? jq : 0) * WS;
+      const int pend = min(len, shift + i + 16);
+      double dot = 0.0;
+      for (int b = 0; b < pend; b += 16) {
+        const f4 dw = lq_rows_dot<HD>(vh + min(b + c, len - 1) * RS, gy, g);
+        float wp[4];
+        lq_weights4(wrow, b + 4 * g, wvec, qok ? min(len, shift + jq + 1) : 0, wp);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (qok && b + 4 * g + r < len && b + 4 * g + r <= shift + jq) dot += static_cast<double>(dw[r] * wp[r]);
+      }
+      dot = lq_gsum_d(dot);
+      if (qok && g == 0) delta[jq] = dot;
+      f4 dqa[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) dqa[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int b = 0; b < pend; b += 16) {
+        // K^T operand: lane (g, c) supplies K[row b + 4g + j][dim 16t + c]
+        float kt[MT][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) kt[t][j] = kh[min(b + 4 * g + j, len - 1) * RS + 16 * t + c];
+        const f4 dw = lq_rows_dot<HD>(vh + min(b + c, len - 1) * RS, gy, g);
+        float wp[4], ds[4];
+        lq_weights4(wrow, b + 4 * g, wvec, qok ? min(len, shift + jq + 1) : 0, wp);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ds[r] = static_cast<float>(static_cast<double>(wp[r]) * (static_cast<double>(dw[r]) - dot) * dscale);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dqa[t] = lq_mfma(kt[t][j], ds[j], dqa[t]);
+      }
+      if (qok)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) *reinterpret_cast<f4*>(dqh + jq * RS + 16 * t + 4 * g) = dqa[t];
+    }
+    // the δ table is read across lanes below
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- key side: dK, dV of the node's packed rows
+    for (int b = 0; b < len; b += 16) {
+      const int p = b + c;  // this lane's packed row (column)
+      const bool pok = p < len;
+      float vy[HD / 4];
+      load_vec<HD / 4>(vh + (pok ? p : 0) * RS + (HD / 4) * g, vy);
+      f4 dka[MT], dva[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        dka[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        dva[t] = dka[t];
+      }
+      // the block's rows are seen from query max(0, b - shift) on
+      for (int i = max(0, b - shift) / 16 * 16; i < L; i += 16) {
+        // dO^T, Q^T operands: lane (g, c) supplies row i + 4g + j at dim 16t + c
+        float gt[MT][4], qt[MT][4], wv[4];
+        double dl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int jj = i + 4 * g + j;
+          const int jc = min(jj, L - 1);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            gt[t][j] = gh[jc * RS + 16 * t + c];
+            qt[t][j] = qh[jc * RS + 16 * t + c];
+          }
+          const bool live = pok && jj < L && p <= shift + jj;
+          wv[j] = live ? wh[static_cast<int64_t>(jc) * WS + p] : 0.0f;
+          dl[j] = live ? delta[jc] : 0.0;
+        }
+        const f4 dw = lq_rows_dot<HD>(gh + min(i + c, L - 1) * RS, vy, g);
+        float ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ds[r] = static_cast<float>(static_cast<double>(wv[r]) * (static_cast<double>(dw[r]) - dl[r]) * dscale);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            dva[t] = lq_mfma(gt[t][j], wv[j], dva[t]);
+            dka[t] = lq_mfma(qt[t][j], ds[j], dka[t]);
+          }
+      }
+      // dK^T[dim 16t + 4g + r][row c]: add into the caller's rows
+      if (pok)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          f4* pk = reinterpret_cast<f4*>(dkh + p * RS + 16 * t + 4 * g);
+          f4* pv = reinterpret_cast<f4*>(dvh + p * RS + 16 * t + 4 * g);
+          *pk = *pk + dka[t];
+          *pv = *pv + dva[t];
+        }
+    }
+    // the next node's query side rewrites the δ table
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 template <typename Fn>
 int dispatch(int hd, Fn&& fn) {
   switch (hd) {
@@ -443,10 +782,17 @@ extern "C" int agpt_varlen_attention_L_queries(const float* q, const float* k, c
     return vset_error(AGPT_ERR_INVALID_ARG, "varlen_L: null pointer");
   const int rc = dispatch(head_dim, [&](auto c) {
     constexpr int HD = decltype(c)::value;
-    const int64_t items = static_cast<int64_t>(T_q) * VLanes<HD>(n_heads).slots;  // one wave each
-    hipLaunchKernelGGL((varlen_fwd_kernel<HD>), dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), q, k, v, kv_offsets, kv_lengths, query_to_node,
-                       query_offsets, output, weights_out, T_q, n_heads, max_kv_len, scale);
+    if constexpr (HD % 16 == 0) {
+      const int64_t waves = (static_cast<int64_t>(T_q) + 63) / 64 * n_heads;  // (block of 64 queries, head)
+      hipLaunchKernelGGL((varlen_Lq_fwd_kernel<HD>), dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), q, k, v, query_to_node, query_offsets, kv_offsets,
+                         kv_lengths, output, weights_out, T_q, n_heads, max_kv_len, scale);
+    } else {  // head dims 4 and 8: a wave per (query, head group)
+      const int64_t items = static_cast<int64_t>(T_q) * VLanes<HD>(n_heads).slots;
+      hipLaunchKernelGGL((varlen_fwd_kernel<HD>), dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), q, k, v, kv_offsets, kv_lengths, query_to_node,
+                         query_offsets, output, weights_out, T_q, n_heads, max_kv_len, scale);
+    }
   });
   return rc != AGPT_OK ? rc : finish_launch();
 }
@@ -465,10 +811,18 @@ extern "C" int agpt_varlen_attention_L_queries_backward(
     return vset_error(AGPT_ERR_INVALID_ARG, "varlen_L: null pointer");
   const int rc = dispatch(head_dim, [&](auto c) {
     constexpr int HD = decltype(c)::value;
-    hipLaunchKernelGGL((varlen_L_bwd_kernel<HD>), dim3(T_q, n_heads), dim3(64),
-                       sizeof(double) * max_kv_len, static_cast<hipStream_t>(stream), q, k, v,
-                       attn_weights, d_out, query_to_node, query_offsets, kv_offsets, kv_lengths, dq,
-                       dk_full, dv_full, n_heads, max_kv_len, scale);
+    if (HD % 16 == 0 && max_kv_len <= kLqMaxDelta) {
+      const int64_t waves = (static_cast<int64_t>(T_q) + 63) / 64 * n_heads;  // (block of 64 queries, head)
+      hipLaunchKernelGGL((varlen_Lq_bwd_kernel<HD % 16 == 0 ? HD : 16>), dim3(static_cast<unsigned>((waves + 3) / 4)),
+                         dim3(256), sizeof(double) * 4 * max_kv_len, static_cast<hipStream_t>(stream), q, k, v,
+                         attn_weights, d_out, query_to_node, query_offsets, kv_offsets, kv_lengths, dq, dk_full,
+                         dv_full, T_q, n_heads, max_kv_len, scale);
+    } else {  // head dims 4 and 8, or a δ table past the wave's LDS share: a workgroup per (radix node, head)
+      hipLaunchKernelGGL((varlen_L_bwd_kernel<HD>), dim3(T_q, n_heads), dim3(64),
+                         sizeof(double) * max_kv_len, static_cast<hipStream_t>(stream), q, k, v,
+                         attn_weights, d_out, query_to_node, query_offsets, kv_offsets, kv_lengths, dq,
+                         dk_full, dv_full, n_heads, max_kv_len, scale);
+    }
   });
   return rc != AGPT_OK ? rc : finish_launch();
 }

@@ -73,12 +73,26 @@ def test_varlen_matches_trie(gpu, H, hd):
     assert_close(dv.cpu().numpy(), dv_r, what="varlen dV")
 
 
-@pytest.mark.parametrize("H,hd", [(2, 16), (3, 8), (8, 32), (4, 64)])
-def test_varlen_L_queries(gpu, H, hd):
+@pytest.mark.parametrize("H,hd,kind", [(2, 16, "small"), (3, 8, "small"), (8, 32, "small"), (4, 64, "small"),
+                                       (8, 16, "c2"), (2, 16, "chains"), (32, 4, "deep")])
+def test_varlen_L_queries(gpu, H, hd, kind):
+    """small: a depth-12 trie; c2: a C2-shaped sample (depth 32, 8 x 16);
+    chains: radix nodes of 1..300 queries (blocks of 64 queries cut inside
+    a node, more (query, head) pairs than lanes); deep: max_len x H past the
+    radix-node kernel's δ table (the per-(node, head) fallback)."""
     import torch
 
     from agpt_amd import attention as A
-    tr = small_trie(n_tokens=500, depth=12, seed=41)
+    from agpt_amd import trie as T_
+    if kind == "small":
+        tr = small_trie(n_tokens=500, depth=12, seed=41)
+    elif kind == "c2":
+        tr = T_.config_trie("C2", scale=0.001)
+    elif kind == "chains":
+        tok = np.concatenate([T_.uniform_tokens(300, 5, 1), T_.uniform_tokens(40, 5, 2)]).astype(np.int32)
+        tr = T_.build_radix_trie(tok, 300)
+    else:
+        tr = small_trie(n_tokens=400, depth=40, seed=43)
     rpar, elen = tr.radix()
     R = rpar.shape[0]
     D = H * hd
@@ -116,6 +130,12 @@ def test_varlen_L_queries(gpu, H, hd):
     O_trie, _, _ = ORC.fwd(tr.parent, Q, K, V, H, hd, scale)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), o_ref, what="L O")
+    # the saved weights: every visible entry (query t of node r sees
+    # kv_len[r] - L_r + j + 1 rows)
+    vis = kv_len[q2n] - elen[q2n] + (np.arange(T) - qoff[q2n]) + 1
+    mask = (np.arange(max_kv)[None, None, :] < vis[:, None, None]) & np.ones((T, H, 1), bool)
+    wg = w.cpu().numpy().reshape(T, H, max_kv)
+    assert_close(wg[mask], w_ref.reshape(T, H, max_kv)[mask], what="L weights")
     assert_close(o_ref.reshape(T, D), O_trie, what="L oracle vs trie oracle")
     dq = torch.zeros(T * D, device="cuda")
     seed_k = np.random.default_rng(3).standard_normal(kv_rows.size * D).astype(np.float32)
