@@ -40,7 +40,7 @@ class AttnConfig(C.Structure):
 class AttnOpts(C.Structure):
     _fields_ = [("scale", C.c_float), ("rope_cos", _vp), ("rope_sin", _vp),
                 ("rope_seq_len", C.c_int), ("stream", _vp),
-                ("prof_events", C.POINTER(_vp)), ("n_prof_events", C.c_int)]
+                ("prof_events", C.POINTER(_vp)), ("n_prof_events", C.c_int), ("ctx_wait", _vp)]
 
 
 class AgptError(RuntimeError):

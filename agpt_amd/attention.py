@@ -179,7 +179,9 @@ class TrieAttention:
         return o, l
 
     def backward(self, q, k, v, o, lse, d_o, *, acc_dk=None, acc_dv=None, rope=None,
-                 scale=None, stream=None, out=None, events=None):
+                 scale=None, stream=None, out=None, events=None, ctx_wait=None):
+        """ctx_wait: a torch.cuda.Event (recorded) that a range plan's
+        context-row reduction waits for (agpt_attn_opts.ctx_wait)."""
         self._check_rows(q, k, v, o, lse, d_o, acc_dk, acc_dv)
         if out is None:
             out = tuple(torch.empty(self.n_nodes, self.d_model, device=q.device,
@@ -190,6 +192,8 @@ class TrieAttention:
                 raise ValueError("out must be three contiguous float32 CUDA [n_nodes, d_model] tensors")
         dq, dk, dv = out
         opts = self._opts(scale, rope, stream, events)
+        if ctx_wait is not None:
+            opts.ctx_wait = ctx_wait.cuda_event
         N.check(self._lib.agpt_attn_bwd(self._h, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                         o.data_ptr(), lse.data_ptr(), d_o.data_ptr(),
                                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
@@ -267,6 +271,46 @@ class RangedTrieAttention:
             att.backward(q, k, v, o, lse, d_o, acc_dk=acc_dk, acc_dv=acc_dv, rope=rope, scale=scale,
                          stream=stream, out=out)
         return out
+
+    def fwd_bwd(self, q, k, v, d_o, *, out=None, lse=None, grads=None, acc_dk=None, acc_dv=None, rope=None,
+                scale=None, n_streams=2, events=None):
+        """Per range: forward, then backward (a per-subtree trainer's order),
+        the ranges dealt round robin over n_streams streams of default
+        priority so that one range's launch tails overlap the next range's
+        kernels. Each backward's context-row reduction (additions into rows
+        an earlier range wrote) waits for the previous range's backward, so
+        the results are the bytes of the one-stream order. events: per range
+        a pair of prof_events lists (forward, backward) or None. Returns
+        (o, lse, (dq, dk, dv)); the caller's current stream waits for all."""
+        dev = q.device
+        cur = torch.cuda.current_stream(dev)
+        o = out if out is not None else torch.empty_like(q)
+        lse = lse if lse is not None else torch.empty(self.n_nodes, self.n_heads, device=dev, dtype=torch.float32)
+        if grads is None:
+            grads = tuple(torch.empty(self.n_nodes, self.d_model, device=dev, dtype=torch.float32)
+                          for _ in range(3))
+        streams = self._streams(dev, n_streams)
+        ready = torch.cuda.Event()
+        ready.record(cur)
+        for s in streams:
+            s.wait_event(ready)
+        prev = None
+        for j, att in enumerate(self.parts):
+            s = streams[j % len(streams)]
+            ev = events[j] if events is not None else (None, None)
+            att.forward(q, k, v, scale=scale, stream=s, out=o, lse=lse, events=ev[0])
+            att.backward(q, k, v, o, lse, d_o, acc_dk=acc_dk, acc_dv=acc_dv, rope=rope, scale=scale, stream=s,
+                         out=grads, events=ev[1], ctx_wait=prev)
+            prev = torch.cuda.Event()
+            prev.record(s)
+        for s in streams:
+            cur.wait_stream(s)
+        return o, lse, grads
+
+    def _streams(self, dev, n):
+        if getattr(self, "_stream_pool", None) is None or len(self._stream_pool) != n:
+            self._stream_pool = [torch.cuda.Stream(dev) for _ in range(max(1, n))]
+        return self._stream_pool
 
     def close(self) -> None:
         for att in self.parts:

@@ -1228,7 +1228,9 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
     // The deep key side's units are (chunk, head): ~8 per CU, and chunks up
     // to 96 tiles (fewer chunk partials and carry work: C4 83.0 -> 81.6 ms
     // at 48, the carry kernel 0.70 -> 0.39 ms at 96).
-    const int64_t per_claim = h->deep_carry ? static_cast<int64_t>(n_tiles) * h->cfg.n_heads : n_tiles;
+    // Claims are (chunk, head group) pairs (heads one by one on the deep key side).
+    const int64_t per_claim = static_cast<int64_t>(n_tiles) *
+                              (h->deep_carry ? h->cfg.n_heads : std::max(1, h->cfg.n_heads / std::max(1, h->hg)));
     const int cap = h->deep_carry ? 96 : 24;
     const int dflt = static_cast<int>(std::min<int64_t>(cap, std::max<int64_t>(1, per_claim / (8 * std::max(cus, 1)))));
     h->chunk_tiles = std::max(1, env_int("AGPT_ATTN_CHUNK", dflt));
@@ -1636,8 +1638,9 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
 
 // Finishes the context rows' share of dK/dV (range plans; see trie_ctx_kernel).
 template <int HD>
-void launch_ctx(const agpt_attn_s* h, float* dk, float* dv, RopeArgs rope, hipStream_t st) {
+void launch_ctx(const agpt_attn_s* h, float* dk, float* dv, RopeArgs rope, hipStream_t st, hipEvent_t wait) {
   if (h->n_ctx <= 0) return;
+  if (wait) (void)hipStreamWaitEvent(st, wait, 0);
   const int D = h->cfg.n_heads * HD;
   const bool chunks = h->variant == 6 && ((h->fused && h->carry) || h->deep_carry);
   const int P = agpt_blk::prefix_cap(h->max_depth);
@@ -1652,7 +1655,7 @@ template <int HD, typename Tin>
 void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* v, const void* o,
                 const float* lse, const void* dO, float* dq, float* dk, float* dv,
                 const float* acc_dk, const float* acc_dv, RopeArgs rope, float scale,
-                hipStream_t st, const ProfMarks& pm) {
+                hipStream_t st, const ProfMarks& pm, hipEvent_t ctx_wait) {
   const int D = h->cfg.n_heads * HD;
   pm.mark(0);
   bool fused_done = false;
@@ -1690,7 +1693,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
           hipLaunchKernelGGL((agpt_blk::bwd_carry_kernel<HD, PlanDev, RopeArgs>), dim3(h->n_chunks_sched - 1),
                              dim3(256), 0, st, plan_dev(h), h->d_E, h->d_F, dk, dv, acc_dk, acc_dv, rope,
                              h->cfg.n_heads);
-        launch_ctx<HD>(h, dk, dv, rope, st);
+        launch_ctx<HD>(h, dk, dv, rope, st, ctx_wait);
         pm.mark(4);
         return;
       }
@@ -1731,7 +1734,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
           hipLaunchKernelGGL((agpt_blk::bwd_carry_kernel<HD, PlanDev, RopeArgs>), dim3(h->n_chunks_sched - 1),
                              dim3(256), 0, st, plan_dev(h), h->d_E, h->d_F, dk, dv, acc_dk, acc_dv, rope,
                              h->cfg.n_heads);
-        launch_ctx<HD>(h, dk, dv, rope, st);
+        launch_ctx<HD>(h, dk, dv, rope, st, ctx_wait);
         pm.mark(4);
         return;
       }
@@ -1807,7 +1810,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   } else {
     pm.mark(3);
   }
-  launch_ctx<HD>(h, dk, dv, rope, st);
+  launch_ctx<HD>(h, dk, dv, rope, st, ctx_wait);
   pm.mark(4);
 }
 
@@ -1972,12 +1975,13 @@ extern "C" int agpt_attn_bwd(agpt_attn_handle h, const void* q, const void* k, c
   if (opts && opts->rope_cos) rope = RopeArgs{opts->rope_cos, opts->rope_sin, opts->rope_seq_len};
   ProfMarks pm;
   if (opts) pm = ProfMarks{opts->prof_events, opts->n_prof_events, st};
+  const hipEvent_t ctx_wait = opts ? static_cast<hipEvent_t>(opts->ctx_wait) : nullptr;
   rc = dispatch_hd(h->cfg.head_dim, [&](auto hdc) {
     constexpr int HD = decltype(hdc)::value;
     if (h->cfg.dtype == AGPT_DTYPE_F32)
-      launch_bwd<HD, float>(h, q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv, rope, scale, st, pm);
+      launch_bwd<HD, float>(h, q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv, rope, scale, st, pm, ctx_wait);
     else
-      launch_bwd<HD, bf16_t>(h, q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv, rope, scale, st, pm);
+      launch_bwd<HD, bf16_t>(h, q, k, v, o, lse, d_o, dq, dk, dv, acc_dk, acc_dv, rope, scale, st, pm, ctx_wait);
   });
   if (rc != AGPT_OK) return rc;
   HIP_TRY(hipGetLastError());

@@ -675,6 +675,8 @@ def main() -> int:
     ap.add_argument("--scale", type=float, default=None,
                     help="corpus scale (1 = BASELINE size; default: 1, or the largest share "
                          "one GPU holds)")
+    ap.add_argument("--batch-streams", type=int, default=3,
+                    help="with --batch-rows: streams the batches are dealt over (1 = one after another)")
     ap.add_argument("--batch-rows", type=int, default=None,
                     help="attn path: batches of whole bigram partitions of at most this many rows, "
                          "one plan each, run in row order (default 0: every partition in one plan)")
@@ -707,7 +709,7 @@ def main() -> int:
 
     import torch
     from agpt_amd import trie as trie_mod
-    from agpt_amd.attention import TrieAttention, partition_starts, range_batches
+    from agpt_amd.attention import RangedTrieAttention, TrieAttention, partition_starts, range_batches
 
     if args.path == "c3":
         if args.scale is None:
@@ -745,19 +747,19 @@ def main() -> int:
     batch_rows = args.batch_rows if args.batch_rows is not None else 0
     starts = partition_starts(tr.radix_head, tr.depth)
     ranges = range_batches(T, batch_rows, starts) if batch_rows > 0 else [(0, T)]
-    parts = []
-    for a, b in ranges:
+    ratt = None
+    if len(ranges) == 1:
         att = TrieAttention(H, hd, max_depth=max(tr.max_depth, 1), dtype=dtype)
-        if len(ranges) == 1:
-            att.plan(tr.parent)
-        else:
-            att.plan_range(tr.parent, a, b)
-        parts.append(att)
+        att.plan(tr.parent)
+        parts = [att]
+    else:
+        ratt = RangedTrieAttention(H, hd, tr.parent, ranges, max_depth=max(tr.max_depth, 1), dtype=dtype)
+        parts = ratt.parts
     infos = [p.plan_info() for p in parts]
     info = {"n_nodes": T, "n_tiles": sum(i["n_tiles"] for i in infos), "batches": len(parts)}
     batching = (f"one batch: all {starts.shape[0]} bigram partitions in one plan" if len(parts) == 1 else
                 f"{len(parts)} batches of whole bigram partitions ({starts.shape[0]} partitions), "
-                f"<= {batch_rows} rows each")
+                f"<= {batch_rows} rows each, dealt over {args.batch_streams} stream(s)")
     log(f"plan: {info}; {batching}; kernel: {parts[0].describe()}")
     q, k, v, d_o = make_inputs(tr, D, H, hd, dtype, seed=1234, dev=dev)
     o = torch.empty(T, D, device=dev, dtype=dtype)
@@ -767,7 +769,11 @@ def main() -> int:
     log(f"inputs resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
 
     def step(evs=None):
-        # per batch: forward, then backward (the per-subtree trainer's order)
+        # per batch: forward, then backward (the per-subtree trainer's order);
+        # batches dealt over --batch-streams streams
+        if ratt is not None:
+            ratt.fwd_bwd(q, k, v, d_o, out=o, lse=lse, grads=grads, n_streams=args.batch_streams, events=evs)
+            return
         for j, att in enumerate(parts):
             att.forward(q, k, v, out=o, lse=lse, events=None if evs is None else evs[j][0])
             att.backward(q, k, v, o, lse, d_o, out=grads, events=None if evs is None else evs[j][1])
@@ -778,14 +784,23 @@ def main() -> int:
         log(f"warmup step {i + 1}/{args.warmup} done")
 
     hev = HipEvents()
-    evs = [[(hev.create(2), hev.create(5)) for _ in parts] for _ in range(args.steps)]
+    # One batch: the per-kernel events ride along in the timed steps. Many
+    # batches: the timed steps run without them (7 event records per batch
+    # are host work of their own) and the per-kernel times come from as many
+    # steps again with the events, outside the timed region.
+    ev_steps = args.steps
+    evs = [[(hev.create(2), hev.create(5)) for _ in parts] for _ in range(ev_steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(evs[i])
+        step(evs[i] if len(parts) == 1 else None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
+    if len(parts) > 1:
+        for i in range(ev_steps):
+            step(evs[i])
+        torch.cuda.synchronize()
     desc = parts[0].describe()
     split = "split backward" in desc
     carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce

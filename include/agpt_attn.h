@@ -76,6 +76,14 @@ typedef struct {
      * The events (hipEvent_t) are created and owned by the caller. */
     void** prof_events;
     int n_prof_events;
+    /* Backward of a range plan (agpt_attn_plan_range) only: an event
+     * (hipEvent_t, or NULL) that the reduction of the context rows' dK/dV
+     * waits for on the stream before it starts. The batches of one trie may
+     * then run on several streams: each batch passes the event its caller
+     * recorded after the previous batch's backward, so the context rows
+     * (rows that an earlier batch wrote) get their additions in batch order
+     * while the batches' other kernels overlap. */
+    void* ctx_wait;
 } agpt_attn_opts;
 
 /* Message describing the last failure on this thread ("" if none). */

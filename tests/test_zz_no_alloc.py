@@ -92,7 +92,7 @@ def test_plan_static_errors(gpu):
     o, lse = b.forward(q, q, q)
     torch.cuda.synchronize()
     # too large for the scratch: refused, with the bytes it needs
-    big = trie.config_trie("C2", scale=0.01)
+    big = trie.config_trie("C2", scale=0.05)
     with pytest.raises(N.AgptError) as e:
         b.plan_static(big.parent)
     assert e.value.code == N.AGPT_ERR_INVALID_ARG and "bytes" in str(e.value)
