@@ -380,6 +380,30 @@ def bench_varlen(args, tr) -> int:
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     step_ms = elapsed / args.steps * 1e3
     cpu = None
+    if not args.no_cpu and radix:
+        from oracle import oracle as ORC
+        R = int(np.searchsorted(qoff, min(args.cpu_rows // 8, T), side="right")) - 1  # whole radix nodes
+        R = max(R, 1)
+        Tm = int(qoff[R])
+        Lm = int(offs[R - 1] + lens[R - 1])
+        qm, gm = q[:Tm].cpu().numpy(), d_o[:Tm].cpu().numpy()
+        km, vm = kp[:Lm].cpu().numpy(), vp[:Lm].cpu().numpy()
+        om = offs[:R].astype(np.int32)
+        reps = 0
+        t0c = time.perf_counter()
+        while True:  # repeat the bounded sample to about 10 s of CPU work
+            o_r, w_r = ORC.varlen_L_fwd(qm, km, vm, q2n[:Tm], qoff[:R + 1], om, lens[:R], Tm, H, hd, max_len, scale)
+            ORC.varlen_L_bwd(qm, km, vm, w_r, gm, q2n[:Tm], qoff[:R + 1], om, lens[:R], Tm, H, hd, max_len, scale,
+                             Lm)
+            reps += 1
+            dt = time.perf_counter() - t0c
+            if dt >= 10.0:
+                break
+        cpu = {"value": Tm * reps / dt, "unit": "node-tokens/s", "cores": 1, "kind": "port",
+               "sample": f"first {R} radix nodes ({Tm} queries, {Lm} packed rows) of the same layout, oracle "
+                         f"L-query forward + backward (C restatement of the packed path), {reps} passes, "
+                         f"1 thread, {dt:.1f} s",
+               "cpu_model": cpu_model()}
     if not args.no_cpu and not radix:
         from oracle import oracle as ORC
         M = min(args.cpu_rows // 8, T)
