@@ -1712,11 +1712,15 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                          static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, hpu, scale);
       pm.mark(1);
       if (h->deep_carry) {
-        // Key slots of a tile: prefix_cap + 64. With all of them in 4 NI
-        // blocks of 16 every sum stays in registers; deeper plans keep the
-        // first 4 kRegItersDeep blocks there.
+        // Key slots of a tile: prefix_cap + 64. The first 4 kRegItersDeep
+        // blocks of 16 keep their sums in registers, the rest in the carry
+        // rows. AGPT_ATTN_REGITERS=3 keeps every slot of a plan to depth 128
+        // in 4 kRegIters blocks instead; at 256 VGPRs that spills 256 bytes
+        // per lane inside the key-block loop, and C4's key side ran 0.75 ms
+        // slower (28.5 vs 27.8 ms).
         const bool regs = env_int("AGPT_ATTN_REGCARRY", 1) != 0;
-        const bool all_regs = agpt_blk::prefix_cap(h->max_depth) + agpt_deep::kTile <= 64 * agpt_deep::kRegIters;
+        const bool all_regs = agpt_blk::prefix_cap(h->max_depth) + agpt_deep::kTile <= 64 * agpt_deep::kRegIters &&
+                              env_int("AGPT_ATTN_REGITERS", agpt_deep::kRegItersDeep) == agpt_deep::kRegIters;
         auto fc = !regs      ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, 0, PlanDev, RopeArgs>
                   : all_regs ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegIters, PlanDev, RopeArgs>
                              : agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegItersDeep, PlanDev, RopeArgs>;

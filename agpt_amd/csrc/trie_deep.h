@@ -60,9 +60,10 @@ constexpr int kThreads = 256;
 constexpr int kChunk = 64;  // keys per streamed chunk: one 16-key block per wave-sized step
 constexpr int kKeyCap = (kMaxDepth - 1 + kTile + kChunk - 1) / kChunk * kChunk;
 // Key blocks per wave of the carry key side with its sums in registers:
-// every key slot of a tile of a plan to depth kRegDepth (prefix_cap + 64
-// keys in 4 kRegIters blocks of 16); deeper plans keep kRegItersDeep
-// blocks per wave (key slots 0 .. 16 * 4 * kRegItersDeep - 1) in registers.
+// kRegItersDeep blocks per wave (key slots 0 .. 16 * 4 * kRegItersDeep - 1),
+// the default; or, on request, every key slot of a tile of a plan to depth
+// kRegDepth (prefix_cap + 64 keys in 4 kRegIters blocks of 16), which at
+// the register limit spills inside the key-block loop.
 constexpr int kRegIters = 3;
 constexpr int kRegDepth = 4 * kRegIters * 16 - kTile;  // 128
 constexpr int kRegItersDeep = 2;
@@ -840,8 +841,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 // chains). With NI > 0 the wave that owns a key block keeps the block's
 // sums in registers, as the accumulators of its matrix products, from one
 // tile to the next: a key that stays in its slot never leaves them. NI ==
-// kRegIters (plans to depth kRegDepth) covers every key slot of a tile;
-// NI == kRegItersDeep covers the first 16 * 4 NI slots of deeper plans.
+// kRegItersDeep covers the first 16 * 4 NI slots of a tile; NI == kRegIters
+// (plans to depth kRegDepth) covers every key slot.
 // The other sums go through this workgroup's carry rows Cs
 // [parity][depth][dK, dV][HD] (global memory, read and written only by this
 // workgroup; a tile reads the rows of its parity and writes the next
