@@ -683,6 +683,7 @@ struct agpt_attn_s {
   bool carry = false;           // one-pass backward carries path sums (E, F replace Pk, Pv)
   bool deep = false;            // block kernels at head_dim 64: streamed key set (trie_deep.h)
   bool deep_carry = false;      // deep key side carries path sums (E, F replace Pk, Pv)
+  bool dq_one_pass = true;      // deep bf16 dQ kernel: δ and dQ in one pass over the keys
   float* d_Cs = nullptr;        // deep carry: per-workgroup carry rows [slot][2][P][2][head_dim]
   int cs_slots = 0;             // workgroups the carry rows are sized for
   float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
@@ -980,6 +981,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     // bf16 row segment already fills whole lines), its key set streamed
     // through a ring (trie_deep.h) instead of held whole in LDS.
     h->deep = hd == 64 && hg == 1 && env_int("AGPT_ATTN_DEEP", 1) != 0;
+    h->dq_one_pass = env_int("AGPT_ATTN_DQ1", 1) != 0;
     h->deep_carry = h->deep && env_int("AGPT_ATTN_CARRY", 1) != 0;
     if (h->deep) {
       h->fwd_lds = agpt_deep::ring_lds_bytes(hd, elem);
@@ -1704,12 +1706,20 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
     if constexpr (HD == 64) {
       clear_sched(h, st);
       const int hpu = deep_heads_per_unit(h);
-      auto fq = agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs>;
-      set_lds(fq, h->bq_lds);
-      hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds, hpu)), dim3(agpt_deep::kThreads), h->bq_lds, st,
-                         plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
-                         static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
-                         static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, hpu, scale);
+      auto launch_q = [&](auto fq) {
+        set_lds(fq, h->bq_lds);
+        hipLaunchKernelGGL(fq, dim3(stream_grid(h, fq, h->bq_lds, hpu)), dim3(agpt_deep::kThreads), h->bq_lds, st,
+                           plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), static_cast<const Tin*>(o), lse,
+                           static_cast<const Tin*>(dO), dq, h->d_Dl, rope, h->cfg.n_heads, hpu, scale);
+      };
+      // bf16: δ and dQ in one pass over the key chunks (AGPT_ATTN_DQ1=0: a δ pass, then dQ)
+      if constexpr (sizeof(Tin) == 2) {
+        if (h->dq_one_pass) launch_q(agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs, true>);
+        else launch_q(agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs, false>);
+      } else {
+        launch_q(agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs, false>);
+      }
       pm.mark(1);
       if (h->deep_carry) {
         // Key slots of a tile: prefix_cap + 64. The first 4 kRegItersDeep

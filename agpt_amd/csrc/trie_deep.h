@@ -461,15 +461,22 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
 // the key chunks for δ, then one for dQ. δ goes to Dl [T, H] for the key
 // side; dQ gets the inverse rotation at the query's depth.
 // ---------------------------------------------------------------------------
-template <int HD, typename Tin, typename PlanT, typename RopeT>
+template <int HD, typename Tin, typename PlanT, typename RopeT, bool kOnePass = false>
 __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
     float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, int hpu, float scale) {
+  // kOnePass (bf16): one pass over the key chunks. With a_j = w_j dw_j,
+  // dQ = scale (Σ_j a_j k_j − δ Σ_j w_j k_j) and δ = Σ_j a_j, so the pass
+  // accumulates δ and both sums and combines them at the end. The two sums
+  // nearly cancel where the dw_j are close to δ, so their bf16 operands
+  // a_j and w_j each go in as a high and a low bf16 part (two products per
+  // output tile, 2^-17 relative per operand) instead of dS rounded once.
+  static_assert(!kOnePass || sizeof(Tin) == 2, "the fp32 inputs take δ = dO·O in one pass already");
   constexpr int KD = HD / 4;
   constexpr int MT = HD / 16;
   constexpr bool kDeltaFromO = sizeof(Tin) == sizeof(float);
-  constexpr int NP = kDeltaFromO ? 1 : 2;  // passes over the key chunks per head
+  constexpr int NP = kDeltaFromO || kOnePass ? 1 : 2;  // passes over the key chunks per head
   using Ring = KeyRing<HD, Tin>;
   constexpr int WS = Ring::WS;
   __shared__ KeyTables tb;
@@ -532,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       live[2] = in_interval(q, iv.z);
       live[3] = in_interval(q, iv.w);
     };
-    f4 dq[MT];
+    f4 dq[MT], dqw[kOnePass ? MT : 1];  // kOnePass: Σ a_j k_j and Σ w_j k_j
     float acc = 0.0f;
     const int per = NP * w.nch;  // steps per head
     const int nsteps = hpu * per;
@@ -547,7 +554,10 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
         qf.scale(qscale);
         acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MT; ++j) dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < MT; ++j) {
+          dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+          if constexpr (kOnePass) dqw[j] = dq[j];
+        }
         if constexpr (kDeltaFromO) {
           float x = 0.0f;
 #pragma unroll
@@ -586,6 +596,29 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           for (int j = 0; j < MT; ++j) tkv[j] = read_tr(Ks, WS, kBlk * bl, kBlk * j, lane);
           __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (kOnePass) {
+          float pw[4], aw[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0
+            pw[r] = fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2) : -__builtin_inff());
+            aw[r] = pw[r] * tv[r];
+            acc += aw[r];
+          }
+          const uint2 ph = pack_bf16(pw), ah = pack_bf16(aw);
+          const float plo[4] = {pw[0] - __uint_as_float(ph.x << 16), pw[1] - __uint_as_float(ph.x & 0xffff0000u),
+                                pw[2] - __uint_as_float(ph.y << 16), pw[3] - __uint_as_float(ph.y & 0xffff0000u)};
+          const float alo[4] = {aw[0] - __uint_as_float(ah.x << 16), aw[1] - __uint_as_float(ah.x & 0xffff0000u),
+                                aw[2] - __uint_as_float(ah.y << 16), aw[3] - __uint_as_float(ah.y & 0xffff0000u)};
+          const uint2 pl2 = pack_bf16(plo), al2 = pack_bf16(alo);
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            dq[j] = mfma_a_bf16(tkv[j], ah, dq[j]);
+            dq[j] = mfma_a_bf16(tkv[j], al2, dq[j]);
+            dqw[j] = mfma_a_bf16(tkv[j], ph, dqw[j]);
+            dqw[j] = mfma_a_bf16(tkv[j], pl2, dqw[j]);
+          }
+          continue;
+        }
         float ds[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)  // masked: exp2(-inf) = 0, no branch per pair
@@ -605,6 +638,11 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       if (pass == 0 && ch + 1 == w.nch) dl = group_sum(acc);
       if (more) ring.store((st + 1) & 1);
       if (last) {
+        if constexpr (kOnePass) {
+          dl = group_sum(acc);
+#pragma unroll
+          for (int j = 0; j < MT; ++j) dq[j] = (dq[j] - dl * dqw[j]) * scale;
+        }
         if (q < w.ntile) {
           const int64_t row = static_cast<int64_t>(w.s) + q;
           const int pos = rope.cos_t ? rope_pos(qdep, rope.seq_len) : 0;

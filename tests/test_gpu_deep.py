@@ -35,9 +35,10 @@ DEEP_SHAPES = {
     "chunk2_one_head_units": {"AGPT_ATTN_CHUNK": "2", "AGPT_ATTN_DHPU": "1"},
     "whole_key_set": {"AGPT_ATTN_DEEP": "0"},
     "carry_all_slots_in_registers_chunk96": {"AGPT_ATTN_REGITERS": "3", "AGPT_ATTN_CHUNK": "96"},
+    "dq_delta_pass_then_dq": {"AGPT_ATTN_DQ1": "0"},
 }
 _KNOBS = ("AGPT_ATTN_VARIANT", "AGPT_ATTN_DHPU", "AGPT_ATTN_CHUNK", "AGPT_ATTN_LPT", "AGPT_ATTN_REGCARRY",
-          "AGPT_ATTN_DEEP", "AGPT_ATTN_CARRY", "AGPT_ATTN_HG", "AGPT_ATTN_REGITERS")
+          "AGPT_ATTN_DEEP", "AGPT_ATTN_CARRY", "AGPT_ATTN_HG", "AGPT_ATTN_REGITERS", "AGPT_ATTN_DQ1")
 
 _CASES: dict = {}
 

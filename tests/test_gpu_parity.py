@@ -48,7 +48,7 @@ def variant(request, monkeypatch):
               "AGPT_ATTN_QB", "AGPT_ATTN_KB", "AGPT_ATTN_SPLIT", "AGPT_ATTN_QSLOTS",
               "AGPT_ATTN_KSLOTS", "AGPT_ATTN_UH", "AGPT_ATTN_CHUNK", "AGPT_ATTN_FUSED",
               "AGPT_ATTN_FHG", "AGPT_ATTN_CARRY", "AGPT_ATTN_FUH", "AGPT_ATTN_DEEP", "AGPT_ATTN_DHPU",
-              "AGPT_ATTN_REGCARRY", "AGPT_ATTN_LPT", "AGPT_ATTN_REGITERS"):
+              "AGPT_ATTN_REGCARRY", "AGPT_ATTN_LPT", "AGPT_ATTN_REGITERS", "AGPT_ATTN_DQ1"):
         monkeypatch.delenv(k, raising=False)
     for k, v in VARIANTS[request.param].items():
         monkeypatch.setenv(k, v)
