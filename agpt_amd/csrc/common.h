@@ -90,10 +90,26 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&x
     *reinterpret_cast<float4*>(p + i) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
 }
 
+// Two floats rounded to nearest-even bf16 by one v_cvt_pk_bf16_f32 (NaN
+// stays NaN), the first in the low half.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
+}
+
+// bf16 stores: groups of four as one 8-byte store (p 8-byte aligned when
+// HD % 4 == 0, as every caller's row and head offsets are).
 template <int HD>
 __device__ __forceinline__ void store_vec(bf16_t* __restrict__ p, const float (&x)[HD]) {
+  if constexpr (HD % 4 == 0) {
 #pragma unroll
-  for (int i = 0; i < HD; ++i) from_f32(x[i], p + i);
+    for (int i = 0; i < HD; i += 4)
+      *reinterpret_cast<uint2*>(p + i) = uint2{pack2_bf16(x[i], x[i + 1]), pack2_bf16(x[i + 2], x[i + 3])};
+  } else {
+#pragma unroll
+    for (int i = 0; i < HD; ++i) from_f32(x[i], p + i);
+  }
 }
 
 // Inverse RoPE on one head slice (batched_depth_backward.cr:738-748): the

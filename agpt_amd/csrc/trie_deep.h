@@ -361,34 +361,33 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
     Slice<Tin, KD> qf, qn;
     qf.load(Q + qbase + h0 * HD);
     ring.load(tb, K, V, D, h0, 0);
+    // The live key blocks of every chunk for this wave's query block, 4 bits
+    // per chunk (nch <= 5), once per unit.
+    uint32_t lm_all = 0;
+    for (int ch = 0; ch < w.nch; ++ch) lm_all |= static_cast<uint32_t>(chunk_live(tb, ch, wave)) << (4 * ch);
     wait_loads();
     ring.store(0);
     __syncthreads();
+    qf.scale(qscale);
     float m = kNoMax, l = 0.0f;
     f4 o[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int nsteps = hpu * w.nch;
     __builtin_assume(nsteps > 0);  // no guard block for the slice loads to sink into
+    // Step st is chunk ch of head h0 + hl; the counters advance at its end.
+    int hl = 0, ch = 0;
     for (int st = 0; st < nsteps; ++st) {
-      const int hl = st / w.nch;
       const int h = h0 + hl;
-      const int ch = st - hl * w.nch;
-      if (ch == 0) {
-        qf.scale(qscale);
-        m = kNoMax;
-        l = 0.0f;
-#pragma unroll
-        for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-      const bool more = st + 1 < nsteps;
-      if (more) {
-        const int h2 = (st + 1) / w.nch;
-        ring.load(tb, K, V, D, h0 + h2, st + 1 - h2 * w.nch);
-      }
       const bool last = ch + 1 == w.nch;
+      const int nxc = last ? 0 : ch + 1;
+      const int nxh = last ? hl + 1 : hl;
+      const bool more = st + 1 < nsteps;
+      if (more) ring.load(tb, K, V, D, h0 + nxh, nxc);
       if (last && hl + 1 < hpu) qn.load(Q + qbase + (h + 1) * HD);
       const Tin* Ks = ring.ks(st & 1);
       const Tin* Vs = ring.vs(st & 1);
-      const int lmask = chunk_live(tb, ch, wave);
+      const int lmask = (lm_all >> (4 * ch)) & 15;
 #pragma unroll
       for (int bl = 0; bl < kChunk / kBlk; ++bl) {
         const int b = ch * (kChunk / kBlk) + bl;
@@ -445,8 +444,17 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
           }
           if (g == 0) lse[row * H + h] = (m + fast_log2(le)) * kLn2;
         }
-        qf = qn;
+        if (hl + 1 < hpu) {  // the next head starts from zero
+          qf = qn;
+          qf.scale(qscale);
+          m = kNoMax;
+          l = 0.0f;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
       }
+      hl = nxh;
+      ch = nxc;
       __syncthreads();
     }
     u = uniform(tb.next[par]);
@@ -519,6 +527,10 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
     fetch(h0, qf, gf, l2, ov);
     const int qdep = pl.depth[qrow];
     ring.load(tb, K, V, D, h0, 0);
+    // The live key blocks of every chunk for this wave's query block, 4 bits
+    // per chunk (nch <= 5), once per unit.
+    uint32_t lm_all = 0;
+    for (int ch = 0; ch < w.nch; ++ch) lm_all |= static_cast<uint32_t>(chunk_live(tb, ch, wave)) << (4 * ch);
     wait_loads();
     l2 *= kLog2e;
     ring.store(0);
@@ -540,41 +552,42 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
       live[3] = in_interval(q, iv.w);
     };
     f4 dq[MT], dqw[kOnePass ? MT : 1];  // kOnePass: Σ a_j k_j and Σ w_j k_j
-    float acc = 0.0f;
-    const int per = NP * w.nch;  // steps per head
-    const int nsteps = hpu * per;
+    float acc;
+    // A head's state at its first step.
+    auto start_head = [&]() {
+      qf.scale(qscale);
+      acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (kOnePass) dqw[j] = dq[j];
+      }
+      if constexpr (kDeltaFromO) {
+        float x = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KD; ++j) x += gf.v[j] * ov[j];
+        dl = group_sum(x);
+      }
+    };
+    start_head();
+    const int nsteps = hpu * NP * w.nch;
     __builtin_assume(nsteps > 0);
+    // Step st is chunk ch of pass `pass` (0: δ, bf16 two-pass only; 1: dQ)
+    // of head h0 + hl; the counters advance at its end.
+    int hl = 0, pass = NP == 2 ? 0 : 1, ch = 0;
     for (int st = 0; st < nsteps; ++st) {
-      const int hl = st / per;
       const int h = h0 + hl;
-      const int r0 = st - hl * per;
-      const int pass = NP == 2 ? r0 / w.nch : 1;  // 0: δ (bf16 only), 1: dQ
-      const int ch = r0 % w.nch;
-      if (r0 == 0) {
-        qf.scale(qscale);
-        acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-          if constexpr (kOnePass) dqw[j] = dq[j];
-        }
-        if constexpr (kDeltaFromO) {
-          float x = 0.0f;
-#pragma unroll
-          for (int j = 0; j < KD; ++j) x += gf.v[j] * ov[j];
-          dl = group_sum(x);
-        }
-      }
+      const bool pend = ch + 1 == w.nch;  // the pass's last chunk
+      const bool last = pend && pass == 1;  // the head's last step
+      const int nxc = pend ? 0 : ch + 1;
+      const int nxp = pend ? (last ? (NP == 2 ? 0 : 1) : 1) : pass;
+      const int nxh = last ? hl + 1 : hl;
       const bool more = st + 1 < nsteps;
-      if (more) {
-        const int h2 = (st + 1) / per;
-        ring.load(tb, K, V, D, h0 + h2, (st + 1 - h2 * per) % w.nch);
-      }
-      const bool last = r0 + 1 == per;
+      if (more) ring.load(tb, K, V, D, h0 + nxh, nxc);
       if (last && hl + 1 < hpu) fetch(h + 1, qn, gn, l2n, on);
       const Tin* Ks = ring.ks(st & 1);
       const Tin* Vs = ring.vs(st & 1);
-      const int lmask = chunk_live(tb, ch, wave);
+      const int lmask = (lm_all >> (4 * ch)) & 15;
 #pragma unroll
       for (int bl = 0; bl < kChunk / kBlk; ++bl) {
         const int b = ch * (kChunk / kBlk) + bl;
@@ -654,14 +667,20 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           }
           if (g == 0) Dl[row * H + h] = dl;
         }
-        qf = qn;
-        gf = gn;
-        l2 = l2n * kLog2e;
-        if constexpr (kDeltaFromO) {
+        if (hl + 1 < hpu) {  // the next head's operands, its state from zero
+          qf = qn;
+          gf = gn;
+          l2 = l2n * kLog2e;
+          if constexpr (kDeltaFromO) {
 #pragma unroll
-          for (int j = 0; j < KD; ++j) ov[j] = on[j];
+            for (int j = 0; j < KD; ++j) ov[j] = on[j];
+          }
+          start_head();
         }
       }
+      hl = nxh;
+      pass = nxp;
+      ch = nxc;
       __syncthreads();
     }
     u = uniform(tb.next[par]);
@@ -1176,7 +1195,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
       } else if constexpr (NI > 0) {
         // Deeper plans: the wave's first NI blocks in registers (selected by
         // the block's turn i, a uniform value), the blocks after them through
-        // the carry rows.
+        // the carry rows. (One call per block, unrolled, spills 192 bytes per
+        // lane and ran slower than these selects.)
         for (int b = wave, i = 0; b < nkb; b += 4, ++i) {
           f4 dk[MT], dv[MT];
 #pragma unroll
