@@ -60,7 +60,12 @@ int set_error(int code, const char* fmt, ...) {
       return set_error(AGPT_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(_e));   \
   } while (0)
 
-constexpr size_t kSchedBytes = 3 * kMaxHeads * sizeof(int32_t);
+// Claim counters: [3][kMaxHeads] of the block kernels, then the deep query
+// side's per-XCD counters (forward, dQ kernel: agpt_deep::kXcdCtr.. +16).
+// Deep key side by subtree range: the longest query range (tiles) a plan
+// may have for it.
+constexpr int kRangeTiles = 8;
+constexpr size_t kSchedBytes = (3 * kMaxHeads + 2 * 8) * sizeof(int32_t);
 
 struct PlanDev {
   const int32_t* parent;
@@ -87,6 +92,13 @@ struct PlanDev {
   // Deep query side: the tile of claim i is tile_order[i] (tiles of more key
   // chunks first, DFS order within), or tile i when null.
   const int32_t* tile_order;
+  // Deep query side without tile_order: each XCD claims from its own
+  // contiguous range of units first (neighbouring tiles share prefix rows
+  // in that XCD's L2), then from the other XCDs' ranges.
+  int32_t xcd_claims;
+  // Deep key side by subtree range (agpt_deep::bwd_kv_range_kernel).
+  const int32_t* range_bend;
+  const int32_t* range_order;
 };
 
 // ---------------------------------------------------------------------------
@@ -671,6 +683,8 @@ struct agpt_attn_s {
   int32_t* d_q_item_off = nullptr;
   int32_t* d_k_item_off = nullptr;
   int32_t* d_tile_order = nullptr;  // deep query side: claim order of the tiles (null: tile order)
+  int32_t* d_range_bend = nullptr;  // deep key side by subtree range: [n_tiles][4] block range ends
+  int32_t* d_range_order = nullptr; // and the tiles by descending range
   // kernel family chosen at plan time: 0 = global-memory walk (any shape),
   // 5 = streaming chain-group walk (trie_fast.h), 6 = streaming block-sparse
   // 16x16 matrix tiles (trie_block.h)
@@ -684,6 +698,8 @@ struct agpt_attn_s {
   bool deep = false;            // block kernels at head_dim 64: streamed key set (trie_deep.h)
   bool deep_carry = false;      // deep key side carries path sums (E, F replace Pk, Pv)
   bool dq_one_pass = true;      // deep bf16 dQ kernel: δ and dQ in one pass over the keys
+  bool xcd_claims = true;       // deep query side in tile order: claims by XCD ranges
+  bool deep_range = false;      // deep key side over each tile's subtree range (short subtrees)
   float* d_Cs = nullptr;        // deep carry: per-workgroup carry rows [slot][2][P][2][head_dim]
   int cs_slots = 0;             // workgroups the carry rows are sized for
   float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
@@ -691,7 +707,7 @@ struct agpt_attn_s {
   size_t fb_lds = 0;
   bool split = true;  // cut long work items into parts (see agpt_fast::kCutSteps)
   int q_slots = 0, k_slots = 0;  // scratch slots of cut query / key items per tile
-  size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0;
+  size_t fwd_lds = 0, bq_lds = 0, kv_lds = 0, kv_range_lds = 0;
   int max_lds = 65536;
   std::string desc;
   // plan placed in the library's static scratch (agpt_attn_plan_static):
@@ -708,7 +724,7 @@ void free_plan(agpt_attn_s* h) {
   const bool own = !h->static_plan;
   int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
                     &h->d_prefix,   &h->d_pref_end,    &h->d_q_item_off,  &h->d_k_item_off,
-                    &h->d_tile_order};
+                    &h->d_tile_order, &h->d_range_bend, &h->d_range_order};
   for (auto p : ip)
     if (*p) {
       if (own) (void)hipFree(*p);
@@ -805,6 +821,9 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.n_chunks = h->n_chunks_sched;
   p.n_prefix = static_cast<int32_t>(h->n_prefix_rows);
   p.tile_order = h->d_tile_order;
+  p.xcd_claims = h->xcd_claims && !h->d_tile_order ? 1 : 0;
+  p.range_bend = h->d_range_bend;
+  p.range_order = h->d_range_order;
   return p;
 }
 
@@ -982,6 +1001,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
     // through a ring (trie_deep.h) instead of held whole in LDS.
     h->deep = hd == 64 && hg == 1 && env_int("AGPT_ATTN_DEEP", 1) != 0;
     h->dq_one_pass = env_int("AGPT_ATTN_DQ1", 1) != 0;
+    h->xcd_claims = env_int("AGPT_ATTN_XCD", 1) != 0;
     h->deep_carry = h->deep && env_int("AGPT_ATTN_CARRY", 1) != 0;
     if (h->deep) {
       h->fwd_lds = agpt_deep::ring_lds_bytes(hd, elem);
@@ -989,6 +1009,7 @@ void choose_variant(agpt_attn_s* h, int& tile) {
       // the key side's staged rows, and the carry kernel's prefetched table
       // inputs of the next tile
       h->kv_lds = agpt_deep::rows_lds_bytes(hd, elem) + agpt_deep::RawTabs::kBytes;
+      h->kv_range_lds = agpt_deep::rows_lds_bytes(hd, elem);  // the staged query rows
     }
     const bool ok = (hd == 16 || hd == 32 || (hd == 64 && hg == 1)) && H % hg == 0 &&
                     (hg == 1 || hg == 2 || hg == 4) &&
@@ -1222,6 +1243,35 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
         if ((rc = upload(ar, &h->d_tile_order, order)) != AGPT_OK) return rc;
       }
     }
+    // Deep key side by subtree range: when every tile's rows have their
+    // subtrees end within kRangeTiles tiles (and the plan has no context
+    // rows, whose shares only the carry path collects), each tile's keys
+    // take their queries from the contiguous rows [s, E) in one unit.
+    h->deep_range = false;
+    if (h->deep && A0 == 0 && tile == agpt_deep::kTile && env_int("AGPT_ATTN_RANGE", 1) != 0) {
+      std::vector<int32_t> bend(static_cast<size_t>(n_tiles) * 4, 0), nq(n_tiles);
+      bool fits = true;
+      for (int32_t t = 0; t < n_tiles && fits; ++t) {
+        const int64_t s = int64_t(t) * tile;
+        const int nt = static_cast<int>(std::min<int64_t>(tile, n - s));
+        int64_t te = s;
+        for (int r = 0; r < nt; ++r) {
+          bend[4 * t + r / agpt_blk::kBlk] = std::max(bend[4 * t + r / agpt_blk::kBlk], end[s + r]);
+          te = std::max<int64_t>(te, end[s + r]);
+        }
+        nq[t] = static_cast<int32_t>((te - s + tile - 1) / tile);
+        fits = nq[t] <= kRangeTiles;
+      }
+      if (fits) {
+        std::vector<int32_t> order(n_tiles);
+        for (int32_t t = 0; t < n_tiles; ++t) order[t] = t;
+        std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return nq[a] > nq[b]; });
+        if ((rc = upload(ar, &h->d_range_bend, bend)) != AGPT_OK) return rc;
+        if ((rc = upload(ar, &h->d_range_order, order)) != AGPT_OK) return rc;
+        h->deep_range = true;
+        h->deep_carry = false;  // nothing to carry: no partials, E, F or carry rows
+      }
+    }
     // Up to 24 tiles per claim (the carry's reach), but at least ~8 chunks
     // per CU: a plan of few tiles (C5: 2048) would otherwise leave most
     // workgroups without a chunk.
@@ -1252,7 +1302,7 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
         (rc = fl(&h->d_Cs, static_cast<size_t>(h->cs_slots) * 2 * agpt_blk::prefix_cap(maxd) * 2 *
                                h->cfg.head_dim * sizeof(float))) != AGPT_OK)
       return rc;
-  } else {
+  } else if (!h->deep_range) {
     const size_t pbytes = std::max<size_t>(1, static_cast<size_t>(h->n_prefix_rows) * D) * sizeof(float);
     if ((rc = fl(&h->d_Pk, pbytes)) != AGPT_OK || (rc = fl(&h->d_Pv, pbytes)) != AGPT_OK) return rc;
     const size_t cbytes = std::max<size_t>(1, static_cast<size_t>(h->n_chunks) * maxd * D) * sizeof(float);
@@ -1421,7 +1471,7 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
     snprintf(buf, sizeof(buf),
              "streamed key ring (deep prefixes) 16x16 mfma, split backward%s: tile_rows=%d tiles=%d "
              "heads_per_wg=1 key_chunk=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
-             h->deep_carry ? " with path-carry" : "", h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds,
+             h->deep_range ? " with the key side by subtree range" : h->deep_carry ? " with path-carry" : "", h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds,
              h->kv_lds, h->max_lds);
   else if (h->variant == 6)
     snprintf(buf, sizeof(buf),
@@ -1721,6 +1771,23 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
         launch_q(agpt_deep::bwd_q_kernel<HD, Tin, PlanDev, RopeArgs, false>);
       }
       pm.mark(1);
+      if (h->deep_range) {
+        auto fr = agpt_deep::bwd_kv_range_kernel<HD, Tin, PlanDev, RopeArgs>;
+        set_lds(fr, h->kv_range_lds);
+        int cus = 256;
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
+        const int64_t units = static_cast<int64_t>(h->n_tiles) * h->cfg.n_heads;
+        const int grid = static_cast<int>(
+            std::max<int64_t>(1, std::min<int64_t>(int64_t(wg_per_cu(fr, h->kv_range_lds, h->max_lds)) * cus, units)));
+        hipLaunchKernelGGL(fr, dim3(grid), dim3(agpt_deep::kThreads), h->kv_range_lds, st, plan_dev(h),
+                           static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v), lse,
+                           h->d_Dl, static_cast<const Tin*>(dO), dk, dv, acc_dk, acc_dv, rope, h->cfg.n_heads,
+                           scale);
+        pm.mark(2);
+        pm.mark(3);
+        pm.mark(4);
+        return;
+      }
       if (h->deep_carry) {
         // Key slots of a tile: prefix_cap + 64. The first 4 kRegItersDeep
         // blocks of 16 keep their sums in registers, the rest in the carry

@@ -259,6 +259,42 @@ __device__ __forceinline__ int tile_of(const PlanT& pl, int i) {
   return pl.tile_order ? pl.tile_order[i] : i;
 }
 
+// Claims of the query-side kernels (thread 0 calls next()). One counter over
+// all units, or, with pl.xcd_claims, kXcds counters at ctr[x]: XCD x (the
+// workgroups b with b % kXcds == x, which the dispatcher deals round robin
+// over the XCDs) takes units [n x / kXcds, n (x + 1) / kXcds) in order, so
+// the tiles in flight on one XCD are neighbours whose prefix rows its L2
+// already holds; a range used up is left for the next XCD's, at most kXcds
+// claims that fail per workgroup. Returns n when every range is used up.
+constexpr int kXcdCtr = 3 * kMaxHeads;  // first per-XCD counter in pl.sched
+struct Claims {
+  int* ctr;
+  int64_t n;
+  int xcd, probe;
+  bool ranged;
+  __device__ int next() {
+    if (!ranged) return atomicAdd(ctr, 1);
+    while (probe < agpt_fast::kXcds) {
+      const int x = (xcd + probe) % agpt_fast::kXcds;
+      const int64_t lo = n * x / agpt_fast::kXcds, hi = n * (x + 1) / agpt_fast::kXcds;
+      const int k = atomicAdd(ctr + x, 1);
+      if (lo + k < hi) return static_cast<int>(lo + k);
+      ++probe;
+    }
+    return static_cast<int>(n);
+  }
+};
+template <typename PlanT>
+__device__ __forceinline__ Claims make_claims(const PlanT& pl, int kernel, int64_t n_units) {
+  Claims q;
+  q.ranged = pl.xcd_claims != 0;
+  q.ctr = pl.sched + (q.ranged ? kXcdCtr + agpt_fast::kXcds * kernel : kernel);
+  q.n = n_units;
+  q.xcd = static_cast<int>(blockIdx.x % agpt_fast::kXcds);
+  q.probe = 0;
+  return q;
+}
+
 // The key blocks of chunk ch with a live pair for query block i (rows 16i ..
 // 16i+15): bit bl for key block 4 ch + bl, a wave-uniform value. One pair of
 // 16-byte reads per chunk, and a scalar bit test per block, where a test per
@@ -346,14 +382,14 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
   // bf16 scores come unscaled (the fp32 operands are scaled once): the
   // scale goes into the exponent's multiply-add.
   const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
-  int* ctr = pl.sched + 0;
-  if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
-  __syncthreads();
-  int u = uniform(tb.next[1]);
   const int ngr = H / hpu;  // head groups: unit u = (tile u / ngr, heads hpu * (u % ngr) ..)
   const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * ngr;
+  Claims claims = make_claims(pl, 0, n_units);
+  if (threadIdx.x == 0) tb.next[1] = claims.next();
+  __syncthreads();
+  int u = uniform(tb.next[1]);
   for (int par = 0; u < n_units; par ^= 1) {
-    if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
+    if (threadIdx.x == 0) tb.next[par] = claims.next();
     const int h0 = (u % ngr) * hpu;
     const Unit w = build_tables(pl, tb, tile_of(pl, u / ngr), false);
     const int q = kBlk * wave + c;  // this lane's query row in the tile
@@ -499,14 +535,14 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
   // bf16 scores come unscaled (the fp32 operands are scaled once): the
   // scale goes into the exponent's multiply-add.
   const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
-  int* ctr = pl.sched + 1;
-  if (threadIdx.x == 0) tb.next[1] = atomicAdd(ctr, 1);
-  __syncthreads();
-  int u = uniform(tb.next[1]);
   const int ngr = H / hpu;  // head groups: unit u = (tile u / ngr, heads hpu * (u % ngr) ..)
   const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * ngr;
+  Claims claims = make_claims(pl, 1, n_units);
+  if (threadIdx.x == 0) tb.next[1] = claims.next();
+  __syncthreads();
+  int u = uniform(tb.next[1]);
   for (int par = 0; u < n_units; par ^= 1) {
-    if (threadIdx.x == 0) tb.next[par] = atomicAdd(ctr, 1);
+    if (threadIdx.x == 0) tb.next[par] = claims.next();
     const int h0 = (u % ngr) * hpu;
     const Unit w = build_tables(pl, tb, tile_of(pl, u / ngr), false);
     const int q = kBlk * wave + c;
@@ -885,6 +921,204 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Key side over each tile's subtree range, for plans whose subtrees end
+// within a few tiles (chains of a few hundred rows, C5). In DFS preorder
+// the rows that see key row k are k .. end[k]-1, so every query of a tile's
+// keys lies in the contiguous rows [s, E), E the greatest subtree end of the
+// tile's rows. A unit is (tile, head): wave w owns the tile's key block w
+// (16 keys, K and V slices in registers) and the rows [s, E) pass through
+// LDS 64 at a time (the head's Q and dO rows, lse, δ; the next 64 in
+// registers while the current ones are worked on). Every key's dK/dV is
+// complete at the unit's end: no partials, no carry, no reduction kernel.
+// pl.range_bend[4 t + w]: the greatest subtree end of key block w of tile t
+// (0 for a block past a short tile); pl.range_order: the tiles by
+// descending query range, claimed in that order.
+// ---------------------------------------------------------------------------
+template <int HD, typename Tin, typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) void bwd_kv_range_kernel(
+    PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
+    const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
+    float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ acc_dk,
+    const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+  constexpr int KD = HD / 4;
+  constexpr int MT = HD / 16;
+  constexpr int EPC = 16 / static_cast<int>(sizeof(Tin));
+  constexpr int WS = row_stride(HD, sizeof(Tin));
+  constexpr int PIECES = HD / EPC;
+  constexpr int ROWJ = kTile * PIECES;  // 16-byte pieces of one staged tensor
+  constexpr int RPER = ROWJ / kThreads;
+  static_assert(ROWJ % kThreads == 0, "whole rounds of the workgroup per staged tensor");
+  __shared__ int32_t next[2];
+  __shared__ alignas(16) float l2s[kTile];  // lse * log2(e) of the staged rows
+  __shared__ alignas(16) float dls[kTile];  // δ of the staged rows
+  extern __shared__ __align__(16) unsigned char dyn[];
+  Tin* Qs = reinterpret_cast<Tin*>(dyn);
+  Tin* Gs = Qs + kTile * WS;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * HD;
+  const float qscale = scale * kLog2e;
+  // bf16 scores come unscaled (the fp32 operands are scaled once): the
+  // scale goes into the exponent's multiply-add.
+  const float sfac = Slice<Tin, HD / 4>::kPre ? 1.0f : qscale;
+  const int64_t n_units = static_cast<int64_t>(pl.n_tiles) * H;
+  int* ctr = pl.sched + 2;
+  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
+    const int t = pl.range_order[u / H];
+    const int h = u % H;
+    const int64_t s = static_cast<int64_t>(t) * kTile;
+    const int ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s));
+    // Rows qs .. qs+63 of head h (rows past the plan repeat its last row).
+    u4 rq[RPER], rg[RPER];
+    float rl = 0.0f, rd = 0.0f;
+    auto fetch_rows = [&](int64_t qs) {
+      const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - qs)) - 1;
+#pragma unroll
+      for (int k = 0; k < RPER; ++k) {
+        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        const int64_t off = (qs + min(j / PIECES, last)) * D + h * HD + (j % PIECES) * EPC;
+        rq[k] = *reinterpret_cast<const u4*>(Q + off);
+        rg[k] = *reinterpret_cast<const u4*>(dO + off);
+      }
+      if (threadIdx.x < kTile) {
+        const int64_t r = qs + min(static_cast<int>(threadIdx.x), last);
+        rl = lse[r * H + h];
+        rd = Dl[r * H + h];
+      }
+    };
+    auto stage_rows = [&]() {
+#pragma unroll
+      for (int k = 0; k < RPER; ++k) {
+        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
+        *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
+      }
+      if (threadIdx.x < kTile) {
+        l2s[threadIdx.x] = rl * kLog2e;
+        dls[threadIdx.x] = rd;
+      }
+    };
+    fetch_rows(s);
+    // This lane's key (block `wave`, column c) and the block's query range.
+    const int key = kBlk * wave + c;
+    const bool kvalid = key < ntile;
+    const int64_t krow = s + min(key, ntile - 1);
+    const int64_t kend = kvalid ? static_cast<int64_t>(pl.end[krow]) : 0;
+    const int bend = uniform(pl.range_bend[4 * t + wave]);
+    int tend = bend;  // the tile's range end: the greatest over its blocks
+#pragma unroll
+    for (int w = 0; w < 4; ++w) tend = max(tend, uniform(pl.range_bend[4 * t + w]));
+    const int nq = static_cast<int>((tend - s + kTile - 1) / kTile);
+    Slice<Tin, KD> kf, vf;
+    kf.load(K + krow * D + h * HD + KD * g);
+    vf.load(V + krow * D + h * HD + KD * g);
+    f4 dk[MT], dv[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      dv[j] = dk[j];
+    }
+    stage_rows();
+    kf.scale(qscale);
+    __syncthreads();
+    for (int qt = 0; qt < nq; ++qt) {
+      const int64_t qs = s + static_cast<int64_t>(qt) * kTile;
+      if (qt + 1 < nq) fetch_rows(qs + kTile);
+      // The key's rows [krow, kend) over the staged rows; query blocks of
+      // the first tile before the key block never see it.
+      const int lo = static_cast<int>(max(krow - qs, static_cast<int64_t>(0)));
+      const int hi = static_cast<int>(max(min(kend - qs, static_cast<int64_t>(kTile)), static_cast<int64_t>(lo)));
+      const int iv = lo | ((hi - lo) << 16);
+      const int i0 = qt == 0 ? wave : 0;
+      const int i1 = static_cast<int>(min(max(static_cast<int64_t>(bend) - qs + kBlk - 1, static_cast<int64_t>(0)) / kBlk,
+                                          static_cast<int64_t>(kTile / kBlk)));
+      for (int i = i0; i < i1; ++i) {
+        const int qr = kBlk * i + c;  // query row this lane supplies
+        const int q0 = kBlk * i + 4 * g;
+        bool live[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) live[r] = in_interval(q0 + r, iv);
+        Slice<Tin, KD> qa, ga;
+        qa.load(Qs + qr * WS + KD * g);
+        ga.load(Gs + qr * WS + KD * g);
+        f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // sv[r]: query q0+r against the key
+        const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f4 l2v = *reinterpret_cast<const f4*>(&l2s[q0]);
+        const f4 dlv = *reinterpret_cast<const f4*>(&dls[q0]);
+        agpt_blk::bf16x4_bits tgv[sizeof(Tin) == 2 ? MT : 1], tqv[sizeof(Tin) == 2 ? MT : 1];
+        if constexpr (sizeof(Tin) == 2) {
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {  // dO^T, Q^T blocks: dims 16j .., queries 16i ..
+            tgv[j] = read_tr(Gs, WS, kBlk * i, kBlk * j, lane);
+            tqv[j] = read_tr(Qs, WS, kBlk * i, kBlk * j, lane);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
+          p[r] = fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2v[r]) : -__builtin_inff());
+          ds[r] = p[r] * (tv[r] - dlv[r]) * scale;
+        }
+        if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
+          const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            dv[j] = mfma_a_bf16(tgv[j], pw, dv[j]);
+            dk[j] = mfma_a_bf16(tqv[j], dw, dk[j]);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = (q0 + r) * WS + kBlk * j + c;
+              dv[j] = mfma16(ld1(Gs + row), p[r], dv[j]);
+              dk[j] = mfma16(ld1(Qs + row), ds[r], dk[j]);
+            }
+        }
+      }
+      __syncthreads();  // the staged rows are no longer read
+      if (qt + 1 < nq) {
+        stage_rows();
+        __syncthreads();
+      }
+    }
+    // dims 16j+4g.. of the key: + seeds, inverse RoPE of dK at its depth.
+    if (kvalid) {
+      const int pos = rope.cos_t ? rope_pos(pl.depth[krow], rope.seq_len) : 0;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const int d0 = kBlk * j + 4 * g;
+        float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+        float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
+        if (acc_dk) {
+          float y[4];
+          load_vec<4>(acc_dk + krow * D + h * HD + d0, y);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) gk[x] += y[x];
+        }
+        if (acc_dv) {
+          float y[4];
+          load_vec<4>(acc_dv + krow * D + h * HD + d0, y);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) gv[x] += y[x];
+        }
+        if (rope.cos_t) agpt_fast::rope_inverse_part<4, HD>(gk, rope.cos_t, rope.sin_t, pos, d0);
+        store_vec<4>(dK + krow * D + h * HD + d0, gk);
+        store_vec<4>(dV + krow * D + h * HD + d0, gv);
+      }
+    }
+    u = uniform(next[par]);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Key side with a path carry. A unit is (chunk of consecutive tiles, head);

@@ -828,8 +828,9 @@ def main() -> int:
     desc = parts[0].describe()
     split = "split backward" in desc
     carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce
+    by_range = "subtree range" in desc  # the key side leaves nothing to reduce
     names = (["trie_fwd", "trie_bwd_q", "trie_bwd_kv"] if split else ["trie_fwd", "trie_bwd"])
-    tail = ["trie_bwd_carry"] if carry else ["trie_bwd_chunk", "trie_bwd_reduce"]
+    tail = [] if by_range else ["trie_bwd_carry"] if carry else ["trie_bwd_chunk", "trie_bwd_reduce"]
     k_ms = {n: [] for n in names + tail}
     for step_evs in evs:
         acc = {n: 0.0 for n in k_ms}  # per step: summed over the batches
@@ -840,7 +841,9 @@ def main() -> int:
                 acc["trie_bwd_kv"] += hev.ms(be[1], be[2])
             else:
                 acc["trie_bwd"] += hev.ms(be[0], be[2])
-            if carry:
+            if by_range:
+                pass
+            elif carry:
                 acc["trie_bwd_carry"] += hev.ms(be[3], be[4])
             else:
                 acc["trie_bwd_chunk"] += hev.ms(be[2], be[3])
