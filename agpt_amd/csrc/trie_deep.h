@@ -937,7 +937,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_kernel(
 // descending query range, claimed in that order.
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT, typename RopeT>
-__global__ __launch_bounds__(kThreads) void bwd_kv_range_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof(Tin) == 2 ? 3 : 2))) void bwd_kv_range_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const float* __restrict__ lse, const float* __restrict__ Dl, const Tin* __restrict__ dO,
     float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ acc_dk,
@@ -968,57 +968,72 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_range_kernel(
   int* ctr = pl.sched + 2;
   if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
   __syncthreads();
+  // The next unit's first query rows, its keys' K and V slices, subtree
+  // ends and block range ends are loaded during the current unit's last
+  // query tile (its claim is known from the unit's first barrier on), so a
+  // unit starts on rows already in registers.
+  u4 rq[RPER], rg[RPER];
+  float rl = 0.0f, rd = 0.0f;
+  // Rows qs .. qs+63 of head hh (rows past the plan repeat its last row).
+  auto fetch_rows = [&](int64_t qs, int hh) {
+    const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - qs)) - 1;
+#pragma unroll
+    for (int k = 0; k < RPER; ++k) {
+      const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+      const int64_t off = (qs + min(j / PIECES, last)) * D + hh * HD + (j % PIECES) * EPC;
+      rq[k] = *reinterpret_cast<const u4*>(Q + off);
+      rg[k] = *reinterpret_cast<const u4*>(dO + off);
+    }
+    if (threadIdx.x < kTile) {
+      const int64_t r = qs + min(static_cast<int>(threadIdx.x), last);
+      rl = lse[r * H + hh];
+      rd = Dl[r * H + hh];
+    }
+  };
+  auto stage_rows = [&]() {
+#pragma unroll
+    for (int k = 0; k < RPER; ++k) {
+      const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+      *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
+      *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
+    }
+    if (threadIdx.x < kTile) {
+      l2s[threadIdx.x] = rl * kLog2e;
+      dls[threadIdx.x] = rd;
+    }
+  };
+  const int key = kBlk * wave + c;  // this lane's key of the tile (block `wave`, column c)
+  Slice<Tin, KD> nkf, nvf;
+  int nkend = 0;
+  int nbend = 0;  // lane l < 4: the greatest subtree end of key block l
+  auto prefetch = [&](int uu, int tt) {
+    const int hh = uu % H;
+    const int64_t s0 = static_cast<int64_t>(tt) * kTile;
+    const int nt = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s0));
+    const int64_t kr = s0 + min(key, nt - 1);
+    fetch_rows(s0, hh);
+    nkf.load(K + kr * D + hh * HD + KD * g);
+    nvf.load(V + kr * D + hh * HD + KD * g);
+    nkend = pl.end[kr];
+    nbend = pl.range_bend[4 * tt + (lane & 3)];
+  };
   int u = uniform(next[1]);
+  int t = u < n_units ? uniform(pl.range_order[u / H]) : 0;
+  if (u < n_units) prefetch(u, t);
   for (int par = 0; u < n_units; par ^= 1) {
     if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
-    const int t = pl.range_order[u / H];
     const int h = u % H;
     const int64_t s = static_cast<int64_t>(t) * kTile;
     const int ntile = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s));
-    // Rows qs .. qs+63 of head h (rows past the plan repeat its last row).
-    u4 rq[RPER], rg[RPER];
-    float rl = 0.0f, rd = 0.0f;
-    auto fetch_rows = [&](int64_t qs) {
-      const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - qs)) - 1;
-#pragma unroll
-      for (int k = 0; k < RPER; ++k) {
-        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
-        const int64_t off = (qs + min(j / PIECES, last)) * D + h * HD + (j % PIECES) * EPC;
-        rq[k] = *reinterpret_cast<const u4*>(Q + off);
-        rg[k] = *reinterpret_cast<const u4*>(dO + off);
-      }
-      if (threadIdx.x < kTile) {
-        const int64_t r = qs + min(static_cast<int>(threadIdx.x), last);
-        rl = lse[r * H + h];
-        rd = Dl[r * H + h];
-      }
-    };
-    auto stage_rows = [&]() {
-#pragma unroll
-      for (int k = 0; k < RPER; ++k) {
-        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
-        *reinterpret_cast<u4*>(Qs + (j / PIECES) * WS + (j % PIECES) * EPC) = rq[k];
-        *reinterpret_cast<u4*>(Gs + (j / PIECES) * WS + (j % PIECES) * EPC) = rg[k];
-      }
-      if (threadIdx.x < kTile) {
-        l2s[threadIdx.x] = rl * kLog2e;
-        dls[threadIdx.x] = rd;
-      }
-    };
-    fetch_rows(s);
-    // This lane's key (block `wave`, column c) and the block's query range.
-    const int key = kBlk * wave + c;
     const bool kvalid = key < ntile;
     const int64_t krow = s + min(key, ntile - 1);
-    const int64_t kend = kvalid ? static_cast<int64_t>(pl.end[krow]) : 0;
-    const int bend = uniform(pl.range_bend[4 * t + wave]);
-    int tend = bend;  // the tile's range end: the greatest over its blocks
-#pragma unroll
-    for (int w = 0; w < 4; ++w) tend = max(tend, uniform(pl.range_bend[4 * t + w]));
+    const int64_t kend = kvalid ? static_cast<int64_t>(nkend) : 0;
+    // The block's query range end, and the tile's: the greatest over its blocks.
+    const int bend = __builtin_amdgcn_readlane(nbend, wave);
+    const int tend = max(max(__builtin_amdgcn_readlane(nbend, 0), __builtin_amdgcn_readlane(nbend, 1)),
+                         max(__builtin_amdgcn_readlane(nbend, 2), __builtin_amdgcn_readlane(nbend, 3)));
     const int nq = static_cast<int>((tend - s + kTile - 1) / kTile);
-    Slice<Tin, KD> kf, vf;
-    kf.load(K + krow * D + h * HD + KD * g);
-    vf.load(V + krow * D + h * HD + KD * g);
+    Slice<Tin, KD> kf = nkf, vf = nvf;
     f4 dk[MT], dv[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
@@ -1028,9 +1043,17 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_range_kernel(
     stage_rows();
     kf.scale(qscale);
     __syncthreads();
+    const int un = uniform(next[par]);  // the next unit (claimed above, published by the barrier)
+    const int tn_raw = un < n_units ? pl.range_order[un / H] : 0;
+    int tn = 0;
     for (int qt = 0; qt < nq; ++qt) {
       const int64_t qs = s + static_cast<int64_t>(qt) * kTile;
-      if (qt + 1 < nq) fetch_rows(qs + kTile);
+      if (qt + 1 < nq) {
+        fetch_rows(qs + kTile, h);
+      } else if (un < n_units) {
+        tn = uniform(tn_raw);
+        prefetch(un, tn);
+      }
       // The key's rows [krow, kend) over the staged rows; query blocks of
       // the first tile before the key block never see it.
       const int lo = static_cast<int>(max(krow - qs, static_cast<int64_t>(0)));
@@ -1116,7 +1139,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kv_range_kernel(
         store_vec<4>(dV + krow * D + h * HD + d0, gv);
       }
     }
-    u = uniform(next[par]);
+    u = un;
+    t = tn;
   }
 }
 
