@@ -213,6 +213,22 @@ def test_range_batches_bf16_hd64(gpu, packed):
            ranges=range_batches(tr.n_nodes, 500), packed=packed)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_chain_forest(gpu, dtype):
+    """Chains of 1..256 rows back to back, so tile boundaries fall anywhere
+    in them and a tile's rows may end one chain and start the next: at
+    head_dim 64 every tile's subtree rows end within 8 tiles, so the key
+    side runs by subtree range (the carry under AGPT_ATTN_RANGE=0)."""
+    rng = np.random.default_rng(31)
+    parts, n = [], 0
+    while n < 2500:
+        L = int(rng.integers(1, 257))
+        parts.append(np.concatenate([[-1], np.arange(n, n + L - 1)]))
+        n += L
+    parent = np.concatenate(parts).astype(np.int32)
+    _check(parent, 2, 64, seed=31, dtype=dtype, rope=True, acc=True)
+
+
 @pytest.mark.parametrize("hd", [8, 16, 64])
 @pytest.mark.parametrize("kind", ["single", "roots", "chain256", "tile_edge", "tile_edge1", "deep48"])
 def test_edge_shapes(gpu, kind, hd):
