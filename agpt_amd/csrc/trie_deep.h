@@ -1059,9 +1059,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof
       const int lo = static_cast<int>(max(krow - qs, static_cast<int64_t>(0)));
       const int hi = static_cast<int>(max(min(kend - qs, static_cast<int64_t>(kTile)), static_cast<int64_t>(lo)));
       const int iv = lo | ((hi - lo) << 16);
-      const int i0 = qt == 0 ? wave : 0;
-      const int i1 = static_cast<int>(min(max(static_cast<int64_t>(bend) - qs + kBlk - 1, static_cast<int64_t>(0)) / kBlk,
-                                          static_cast<int64_t>(kTile / kBlk)));
+      const int i0 = uniform(qt == 0 ? wave : 0);
+      const int i1 = uniform(static_cast<int>(
+          min(max(static_cast<int64_t>(bend) - qs + kBlk - 1, static_cast<int64_t>(0)) / kBlk,
+              static_cast<int64_t>(kTile / kBlk))));
       for (int i = i0; i < i1; ++i) {
         const int qr = kBlk * i + c;  // query row this lane supplies
         const int q0 = kBlk * i + 4 * g;
@@ -1088,7 +1089,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof
 #pragma unroll
         for (int r = 0; r < 4; ++r) {  // masked: exp2(-inf) = 0, no branch per pair
           p[r] = fast_exp2(live[r] ? __builtin_fmaf(sv[r], sfac, -l2v[r]) : -__builtin_inff());
-          ds[r] = p[r] * (tv[r] - dlv[r]) * scale;
+          // times scale once per key when dK is emitted (1/8 at head_dim
+          // 64: a power of two, so the bf16 rounding below is unchanged)
+          ds[r] = p[r] * (tv[r] - dlv[r]);
         }
         if constexpr (sizeof(Tin) == 2) {  // P and dS rounded to bf16, one 16-deep step per tile
           const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
@@ -1120,7 +1123,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
         const int d0 = kBlk * j + 4 * g;
-        float gk[4] = {dk[j][0], dk[j][1], dk[j][2], dk[j][3]};
+        float gk[4] = {dk[j][0] * scale, dk[j][1] * scale, dk[j][2] * scale, dk[j][3] * scale};
         float gv[4] = {dv[j][0], dv[j][1], dv[j][2], dv[j][3]};
         if (acc_dk) {
           float y[4];
