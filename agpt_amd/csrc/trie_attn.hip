@@ -99,6 +99,11 @@ struct PlanDev {
   // Deep key side by subtree range (agpt_deep::bwd_kv_range_kernel).
   const int32_t* range_bend;
   const int32_t* range_order;
+  // Chain-forest plans (agpt_chain): chain k is rows chain_start[k] ..
+  // chain_start[k+1]-1; chain_order lists the chains longest first.
+  const int32_t* chain_start;
+  const int32_t* chain_order;
+  int32_t n_chains;
 };
 
 // ---------------------------------------------------------------------------
@@ -640,6 +645,7 @@ __global__ __launch_bounds__(256) void trie_ctx_kernel(PlanDev pl, const float* 
 #include "trie_fast.h"
 #include "trie_block.h"
 #include "trie_deep.h"
+#include "trie_chain.h"
 
 // ===========================================================================
 // Host side: handle, plan, launches.
@@ -685,6 +691,9 @@ struct agpt_attn_s {
   int32_t* d_tile_order = nullptr;  // deep query side: claim order of the tiles (null: tile order)
   int32_t* d_range_bend = nullptr;  // deep key side by subtree range: [n_tiles][4] block range ends
   int32_t* d_range_order = nullptr; // and the tiles by descending range
+  int32_t* d_chain_start = nullptr; // chain-forest plans: chain row offsets [n_chains + 1]
+  int32_t* d_chain_order = nullptr; // and the chains longest first
+  int32_t n_chains = 0;
   // kernel family chosen at plan time: 0 = global-memory walk (any shape),
   // 5 = streaming chain-group walk (trie_fast.h), 6 = streaming block-sparse
   // 16x16 matrix tiles (trie_block.h)
@@ -700,6 +709,7 @@ struct agpt_attn_s {
   bool dq_one_pass = true;      // deep bf16 dQ kernel: δ and dQ in one pass over the keys
   bool xcd_claims = true;       // deep query side in tile order: claims by XCD ranges
   bool deep_range = false;      // deep key side over each tile's subtree range (short subtrees)
+  bool chain_plan = false;      // bf16 head_dim 64 on a forest of chains: the agpt_chain kernels
   float* d_Cs = nullptr;        // deep carry: per-workgroup carry rows [slot][2][P][2][head_dim]
   int cs_slots = 0;             // workgroups the carry rows are sized for
   float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
@@ -724,7 +734,8 @@ void free_plan(agpt_attn_s* h) {
   const bool own = !h->static_plan;
   int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
                     &h->d_prefix,   &h->d_pref_end,    &h->d_q_item_off,  &h->d_k_item_off,
-                    &h->d_tile_order, &h->d_range_bend, &h->d_range_order};
+                    &h->d_tile_order, &h->d_range_bend, &h->d_range_order, &h->d_chain_start,
+                    &h->d_chain_order};
   for (auto p : ip)
     if (*p) {
       if (own) (void)hipFree(*p);
@@ -824,6 +835,9 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.xcd_claims = h->xcd_claims && !h->d_tile_order ? 1 : 0;
   p.range_bend = h->d_range_bend;
   p.range_order = h->d_range_order;
+  p.chain_start = h->d_chain_start;
+  p.chain_order = h->d_chain_order;
+  p.n_chains = h->n_chains;
   return p;
 }
 
@@ -1272,6 +1286,31 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
         h->deep_carry = false;  // nothing to carry: no partials, E, F or carry rows
       }
     }
+    // A forest of chains (each row's parent the row before it, or none) at
+    // bf16 head_dim 64: plain causal attention per chain (agpt_chain).
+    h->chain_plan = false;
+    h->n_chains = 0;
+    if (h->deep && A0 == 0 && h->cfg.dtype == AGPT_DTYPE_BF16 && env_int("AGPT_ATTN_CHAIN", 1) != 0) {
+      bool chains = true;
+      std::vector<int32_t> starts;
+      for (int64_t r = 0; r < n && chains; ++r) {
+        if (parent[r] < 0) starts.push_back(static_cast<int32_t>(r));
+        else chains = parent[r] == r - 1;
+      }
+      if (chains) {
+        const int32_t nc = static_cast<int32_t>(starts.size());
+        starts.push_back(static_cast<int32_t>(n));
+        std::vector<int32_t> order(nc);
+        for (int32_t k = 0; k < nc; ++k) order[k] = k;
+        std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+          return starts[a + 1] - starts[a] > starts[b + 1] - starts[b];
+        });
+        if ((rc = upload(ar, &h->d_chain_start, starts)) != AGPT_OK) return rc;
+        if ((rc = upload(ar, &h->d_chain_order, order)) != AGPT_OK) return rc;
+        h->n_chains = nc;
+        h->chain_plan = true;
+      }
+    }
     // Up to 24 tiles per claim (the carry's reach), but at least ~8 chunks
     // per CU: a plan of few tiles (C5: 2048) would otherwise leave most
     // workgroups without a chunk.
@@ -1467,11 +1506,19 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (!h) return "null handle";
   if (!h->planned) return "no plan";
   char buf[400];
-  if (h->variant == 6 && h->deep)
+  if (h->variant == 6 && h->deep && h->chain_plan)
+    snprintf(buf, sizeof(buf),
+             "dense-causal chain kernels (a forest of %d chains; unit = chain x head, %d waves, the chain's rows "
+             "in LDS), split backward with the key side by subtree range: lds=%zu lds_limit=%d",
+             h->n_chains, agpt_chain::kWaves, agpt_chain::lds_bytes(), h->max_lds);
+  else if (h->variant == 6 && h->deep)
     snprintf(buf, sizeof(buf),
              "streamed key ring (deep prefixes) 16x16 mfma, split backward%s: tile_rows=%d tiles=%d "
              "heads_per_wg=1 key_chunk=%d fwd_lds=%zu bwd_q_lds=%zu bwd_kv_lds=%zu lds_limit=%d",
-             h->deep_range ? " with the key side by subtree range" : h->deep_carry ? " with path-carry" : "", h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds,
+             h->deep_range ? " with the key side by subtree range"
+             : h->deep_carry ? " with path-carry"
+                             : "",
+             h->tile, h->n_tiles, agpt_deep::kChunk, h->fwd_lds, h->bq_lds,
              h->kv_lds, h->max_lds);
   else if (h->variant == 6)
     snprintf(buf, sizeof(buf),
@@ -1544,13 +1591,13 @@ struct ProfMarks {
 // last workgroups waiting for a whole earlier workgroup to finish). 0 if
 // `fn` cannot launch with `lds`.
 template <typename Fn>
-int wg_per_cu(Fn fn, size_t lds, int lds_per_cu) {
+int wg_per_cu(Fn fn, size_t lds, int lds_per_cu, int threads = agpt_fast::kThreads) {
   hipFuncAttributes fa{};
   if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) != hipSuccess) return 0;
   const size_t total = (fa.sharedSizeBytes + lds + 511) & ~static_cast<size_t>(511);
   if (total > static_cast<size_t>(lds_per_cu)) return 0;
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), agpt_fast::kThreads,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), threads,
                                                    lds) != hipSuccess)
     return 0;
   return std::min(n, static_cast<int>(lds_per_cu / total));
@@ -1567,6 +1614,18 @@ int stream_grid(const agpt_attn_s* h, Fn fn, size_t lds, int hg = 0) {
   g = std::min(g, (units + m - 1) / m * m);
   g = std::max<int64_t>(g / m * m, m);
   return static_cast<int>(g);
+}
+
+// Workgroups of a chain-forest kernel: as many as fit the chip, at most one
+// per (chain, head) unit.
+template <typename Fn>
+int chain_grid(const agpt_attn_s* h, Fn fn) {
+  int cus = 256;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
+  const int64_t units = static_cast<int64_t>(h->n_chains) * h->cfg.n_heads;
+  const int64_t g =
+      static_cast<int64_t>(std::max(wg_per_cu(fn, agpt_chain::lds_bytes(), h->max_lds, agpt_chain::kThreads), 1)) * cus;
+  return static_cast<int>(std::max<int64_t>(1, std::min(g, units)));
 }
 
 // Heads per unit of the deep-prefix kernels: all heads of a tile when the
@@ -1644,6 +1703,18 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
                 float* lse, float scale, hipStream_t st, const ProfMarks& pm) {
   pm.mark(0);
   if (h->variant == 6 && h->deep) {
+    if constexpr (HD == 64 && sizeof(Tin) == 2) {
+      if (h->chain_plan) {
+        clear_sched(h, st);
+        auto fn = agpt_chain::fwd_kernel<PlanDev>;
+        set_lds(fn, agpt_chain::lds_bytes());
+        hipLaunchKernelGGL(fn, dim3(chain_grid(h, fn)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,
+                           plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), static_cast<Tin*>(o), lse, h->cfg.n_heads, scale);
+        pm.mark(1);
+        return;
+      }
+    }
     if constexpr (HD == 64) {
       clear_sched(h, st);
       const int hpu = deep_heads_per_unit(h, true);
@@ -1753,6 +1824,28 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   }
   if (fused_done) {
   } else if (h->variant == 6 && h->deep) {
+    if constexpr (HD == 64 && sizeof(Tin) == 2) {
+      if (h->chain_plan) {
+        clear_sched(h, st);
+        auto fq = agpt_chain::bwd_q_kernel<PlanDev, RopeArgs>;
+        set_lds(fq, agpt_chain::lds_bytes());
+        hipLaunchKernelGGL(fq, dim3(chain_grid(h, fq)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,
+                           plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), lse, static_cast<const Tin*>(dO), dq, h->d_Dl, rope,
+                           h->cfg.n_heads, scale);
+        pm.mark(1);
+        auto fk = agpt_chain::bwd_kv_kernel<PlanDev, RopeArgs>;
+        set_lds(fk, agpt_chain::lds_bytes());
+        hipLaunchKernelGGL(fk, dim3(chain_grid(h, fk)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,
+                           plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), lse, h->d_Dl, static_cast<const Tin*>(dO), dk, dv, acc_dk,
+                           acc_dv, rope, h->cfg.n_heads, scale);
+        pm.mark(2);
+        pm.mark(3);
+        pm.mark(4);
+        return;
+      }
+    }
     if constexpr (HD == 64) {
       clear_sched(h, st);
       const int hpu = deep_heads_per_unit(h);

@@ -1,0 +1,420 @@
+// trie_chain.h — head_dim 64, bf16 kernels for plans whose trie is a forest
+// of chains (every row's parent is the row before it or none: independent
+// sequences, C5). Included by trie_attn.hip after trie_deep.h.
+//
+// On such a plan the trie attention of a chain is plain causal attention
+// over its rows, so the general kernels' per-tile key lists, interval tables
+// and per-pair interval tests are overhead. Here a unit is (chain, head): the
+// chain's K and V rows of the head (query side) or Q and dO rows (key side),
+// at most 256, are loaded into LDS once, and the eight waves of the
+// workgroup take the chain's 16-row blocks, costliest first in snake order.
+// A block pair is masked only on the diagonal (key <= query inside the
+// block) and past the chain's end; rows past the end repeat the chain's last
+// row in LDS, so a masked pair never multiplies stale data. Each key's dK/dV and each
+// query's dQ is complete within its unit: no partials, no reduction.
+//
+// Lane layouts and products are those of trie_deep.h: 16x16 blocks on the
+// bf16 matrix instructions, lane l = 16g + c.
+#pragma once
+
+namespace agpt_chain {
+
+using namespace agpt;
+using agpt_blk::group_max;
+using agpt_blk::group_sum;
+using agpt_blk::kBlk;
+using agpt_blk::kRescaleLog2;
+using agpt_blk::pack_bf16;
+using agpt_blk::Slice;
+using agpt_blk::slice_dot;
+using agpt_deep::kNoMax;
+using agpt_deep::mfma_a_bf16;
+using agpt_deep::read_tr;
+using agpt_fast::f4;
+using agpt_fast::u4;
+using agpt_fast::uniform;
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = kMaxDepth;  // longest chain
+constexpr int kHD = 64;
+constexpr int WS = kHD + 8;       // LDS row stride (bf16 elements): 144 bytes
+constexpr int kPieces = kHD / 8;  // 16-byte pieces per row of a head
+
+// Dynamic LDS: two row tiles [kRows][WS] of bf16 (K and V, or Q and dO).
+__host__ __device__ constexpr size_t lds_bytes() { return 2u * kRows * WS * sizeof(bf16_t); }
+
+// Block k (0, 1, ..) of wave w among nb blocks: positions dealt in snake
+// order (wave 0..7, then 7..0, ..); position p is block nb-1-p on the query
+// side (block i has i+1 key blocks) and block p on the key side (block j
+// has nb-j query blocks), so each wave's blocks are costliest first and
+// the waves' totals are close. -1 past the end.
+__device__ __forceinline__ int snake_block(int k, int w, int nb, bool key_side) {
+  const int pos = kWaves * k + ((k & 1) ? kWaves - 1 - w : w);
+  if (pos >= nb) return -1;
+  return key_side ? pos : nb - 1 - pos;
+}
+
+// The unit's chain and head: unit u is chain order[u / H], head u % H.
+struct ChainUnit {
+  int64_t c0;  // first row
+  int L;       // rows
+  int nb;      // 16-row blocks
+  int h;
+};
+template <typename PlanT>
+__device__ __forceinline__ ChainUnit chain_unit(const PlanT& pl, int u, int H) {
+  ChainUnit x;
+  const int ci = uniform(pl.chain_order[u / H]);
+  x.h = u % H;
+  x.c0 = uniform(pl.chain_start[ci]);
+  x.L = uniform(pl.chain_start[ci + 1]) - static_cast<int>(x.c0);
+  x.nb = (x.L + kBlk - 1) / kBlk;
+  return x;
+}
+
+// Rows 0 .. 16 nb - 1 of the unit's chain, head h, of tensors A and B into
+// the LDS tiles As and Bs. Rows past the chain repeat its last row (finite
+// values that the masks give zero weight), so every load is unconditional
+// and in bounds; all of a thread's pieces are in flight before its first
+// LDS store.
+__device__ __forceinline__ void load_rows(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
+                                          bf16_t* As, bf16_t* Bs, const ChainUnit& x, int D) {
+  constexpr int kPer = 2 * kRows * kPieces / kThreads;  // 8
+  const int per_t = kBlk * x.nb * kPieces;              // pieces of one tensor
+  u4 v[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int p = static_cast<int>(threadIdx.x) + k * kThreads;
+    const int ten = p >= per_t ? 1 : 0;
+    const int q = p - ten * per_t;
+    const int r = min(q / kPieces, x.L - 1);
+    v[k] = *reinterpret_cast<const u4*>((ten ? B : A) + (x.c0 + r) * D + x.h * kHD + (q % kPieces) * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int p = static_cast<int>(threadIdx.x) + k * kThreads;
+    if (p < 2 * per_t) {
+      const int ten = p >= per_t ? 1 : 0;
+      const int q = p - ten * per_t;
+      *reinterpret_cast<u4*>((ten ? Bs : As) + (q / kPieces) * WS + (q % kPieces) * 8) = v[k];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward: O and lse. Query block i of the chain against key blocks 0 .. i:
+// S^T = K Q^T puts query c in lane column c (keys 4g .. 4g+3 in its
+// registers); online softmax with the lazy rescale; O^T += V^T P^T with V^T
+// read transposed from the V rows.
+// ---------------------------------------------------------------------------
+template <typename PlanT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void fwd_kernel(PlanT pl, const bf16_t* __restrict__ Q,
+                                                       const bf16_t* __restrict__ K,
+                                                       const bf16_t* __restrict__ V, bf16_t* __restrict__ O,
+                                                       float* __restrict__ lse, int H, float scale) {
+  constexpr int KD = kHD / 4;
+  constexpr int MT = kHD / 16;
+  __shared__ int32_t next[2];
+  extern __shared__ __align__(16) unsigned char dyn[];
+  bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
+  bf16_t* Vs = Ks + kRows * WS;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * kHD;
+  const float sfac = scale * kLog2e;  // bf16 scores come unscaled
+  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
+  int* ctr = pl.sched + 0;
+  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
+    const ChainUnit x = chain_unit(pl, u, H);
+    load_rows(K, V, Ks, Vs, x, D);
+    __syncthreads();
+    for (int k = 0;; ++k) {
+      const int i = snake_block(k, wave, x.nb, false);
+      if (i < 0) break;
+      const int q = kBlk * i + c;  // this lane's query (chain index)
+      Slice<bf16_t, KD> qf;
+      qf.load(Q + (x.c0 + min(q, x.L - 1)) * D + x.h * kHD + KD * g);
+      float m = kNoMax, l = 0.0f;
+      f4 o[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      // key 16kb + 4g + r is live iff it is <= min(q, L - 1), i.e. r <= t
+      const int tq = min(q, x.L - 1) - 4 * g;
+      for (int kb = 0; kb <= i; ++kb) {
+        Slice<bf16_t, KD> kf;
+        kf.load(Ks + (kBlk * kb + c) * WS + KD * g);
+        const f4 sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16kb+4g+r against query q
+        const int t = tq - kBlk * kb;
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = r <= t ? sv[r] : -__builtin_inff();
+        const float lmx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * sfac;
+        if (__any(lmx > m + kRescaleLog2)) {
+          const float mx = group_max(lmx);
+          const bool resc = mx > m + kRescaleLog2;
+          const float a = resc ? fast_exp2(m - mx) : 1.0f;
+          m = resc ? mx : m;
+          l *= a;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) o[j] *= a;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = fast_exp2(__builtin_fmaf(sc[r], sfac, -m));  // masked: exp2(-inf) = 0
+          l += p[r];
+        }
+        const uint2 pw = pack_bf16(p);
+#pragma unroll
+        for (int j = 0; j < MT; ++j) o[j] = mfma_a_bf16(read_tr(Vs, WS, kBlk * kb, kBlk * j, lane), pw, o[j]);
+      }
+      const float le = group_sum(l);
+      if (q < x.L) {
+        const int64_t row = x.c0 + q;
+        const float inv = __builtin_amdgcn_rcpf(le);
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
+          store_vec<4>(O + row * D + x.h * kHD + kBlk * j + 4 * g, v);
+        }
+        if (g == 0) lse[row * H + x.h] = (m + fast_log2(le)) * kLn2;
+      }
+    }
+    __syncthreads();  // the chain's rows are no longer read
+    u = uniform(next[par]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, query side: δ and dQ in one pass over key blocks 0 .. i, as the
+// deep dQ kernel does (batched_depth_backward.cr:637-646 for δ): with
+// a_j = w_j dw_j, dQ = scale (Σ_j a_j k_j − δ Σ_j w_j k_j), δ = Σ_j a_j; the
+// bf16 operands a_j and w_j enter as high and low bf16 parts. δ goes to Dl
+// [T, H] for the key side; dQ gets the inverse rotation at the query's depth.
+// ---------------------------------------------------------------------------
+template <typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_q_kernel(PlanT pl, const bf16_t* __restrict__ Q,
+                                                         const bf16_t* __restrict__ K,
+                                                         const bf16_t* __restrict__ V,
+                                                         const float* __restrict__ lse,
+                                                         const bf16_t* __restrict__ dO, float* __restrict__ dQ,
+                                                         float* __restrict__ Dl, RopeT rope, int H, float scale) {
+  constexpr int KD = kHD / 4;
+  constexpr int MT = kHD / 16;
+  __shared__ int32_t next[2];
+  extern __shared__ __align__(16) unsigned char dyn[];
+  bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
+  bf16_t* Vs = Ks + kRows * WS;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * kHD;
+  const float sfac = scale * kLog2e;
+  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
+  int* ctr = pl.sched + 1;
+  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
+    const ChainUnit x = chain_unit(pl, u, H);
+    load_rows(K, V, Ks, Vs, x, D);
+    __syncthreads();
+    for (int k = 0;; ++k) {
+      const int i = snake_block(k, wave, x.nb, false);
+      if (i < 0) break;
+      const int q = kBlk * i + c;
+      const int64_t qrow = x.c0 + min(q, x.L - 1);
+      Slice<bf16_t, KD> qf, gf;
+      qf.load(Q + qrow * D + x.h * kHD + KD * g);
+      gf.load(dO + qrow * D + x.h * kHD + KD * g);
+      const float l2 = lse[qrow * H + x.h] * kLog2e;
+      f4 dq[MT], dqw[MT];  // Σ a_j k_j and Σ w_j k_j
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        dq[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        dqw[j] = dq[j];
+      }
+      float acc = 0.0f;
+      const int tq = min(q, x.L - 1) - 4 * g;  // key 16kb + 4g + r is live iff r <= tq - 16kb
+      for (int kb = 0; kb <= i; ++kb) {
+        Slice<bf16_t, KD> kf, vf;
+        kf.load(Ks + (kBlk * kb + c) * WS + KD * g);
+        vf.load(Vs + (kBlk * kb + c) * WS + KD * g);
+        const f4 sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16kb+4g+r against query q
+        const f4 tv = slice_dot(vf, gf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // dO_q . v_key
+        agpt_blk::bf16x4_bits tkv[MT];  // K^T blocks: dims 16j .., keys 16kb ..
+#pragma unroll
+        for (int j = 0; j < MT; ++j) tkv[j] = read_tr(Ks, WS, kBlk * kb, kBlk * j, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        float pw[4], aw[4];
+        const int t = tq - kBlk * kb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pw[r] = fast_exp2(r <= t ? __builtin_fmaf(sv[r], sfac, -l2) : -__builtin_inff());
+          aw[r] = pw[r] * tv[r];
+          acc += aw[r];
+        }
+        const uint2 ph = pack_bf16(pw), ah = pack_bf16(aw);
+        const float plo[4] = {pw[0] - __uint_as_float(ph.x << 16), pw[1] - __uint_as_float(ph.x & 0xffff0000u),
+                              pw[2] - __uint_as_float(ph.y << 16), pw[3] - __uint_as_float(ph.y & 0xffff0000u)};
+        const float alo[4] = {aw[0] - __uint_as_float(ah.x << 16), aw[1] - __uint_as_float(ah.x & 0xffff0000u),
+                              aw[2] - __uint_as_float(ah.y << 16), aw[3] - __uint_as_float(ah.y & 0xffff0000u)};
+        const uint2 pl2 = pack_bf16(plo), al2 = pack_bf16(alo);
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          dq[j] = mfma_a_bf16(tkv[j], ah, dq[j]);
+          dq[j] = mfma_a_bf16(tkv[j], al2, dq[j]);
+          dqw[j] = mfma_a_bf16(tkv[j], ph, dqw[j]);
+          dqw[j] = mfma_a_bf16(tkv[j], pl2, dqw[j]);
+        }
+      }
+      const float dl = group_sum(acc);
+      if (q < x.L) {
+        const int64_t row = x.c0 + q;
+        const int pos = rope.cos_t ? rope_pos(q + 1, rope.seq_len) : 0;  // a chain's row q is at depth q + 1
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = (dq[j][r] - dl * dqw[j][r]) * scale;
+          if (rope.cos_t) agpt_fast::rope_inverse_part<4, kHD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
+          store_vec<4>(dQ + row * D + x.h * kHD + kBlk * j + 4 * g, v);
+        }
+        if (g == 0) Dl[row * H + x.h] = dl;
+      }
+    }
+    __syncthreads();
+    u = uniform(next[par]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, key side: dK, dV of key block j against query blocks j .. nb-1,
+// the chain's Q and dO rows (and lse, δ) in LDS. S = Q_i K^T puts key c in
+// lane column c (queries 4g .. 4g+3 in its registers); dV^T += dO^T P,
+// dK^T += Q^T dS with the transposed operands read from the row tiles. dS
+// leaves out the softmax scale, applied once per key (a power of two at
+// head_dim 64, so the bf16 rounding is unchanged).
+// ---------------------------------------------------------------------------
+template <typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kv_kernel(
+    PlanT pl, const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
+    const float* __restrict__ lse, const float* __restrict__ Dl, const bf16_t* __restrict__ dO,
+    float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ acc_dk,
+    const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+  constexpr int KD = kHD / 4;
+  constexpr int MT = kHD / 16;
+  __shared__ int32_t next[2];
+  __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (0 past the end)
+  __shared__ alignas(16) float dls[kRows];  // δ of the chain's rows
+  extern __shared__ __align__(16) unsigned char dyn[];
+  bf16_t* Qs = reinterpret_cast<bf16_t*>(dyn);
+  bf16_t* Gs = Qs + kRows * WS;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int g = lane >> 4, c = lane & 15;
+  const int D = H * kHD;
+  const float sfac = scale * kLog2e;
+  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
+  int* ctr = pl.sched + 2;
+  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
+    const ChainUnit x = chain_unit(pl, u, H);
+    for (int r = threadIdx.x; r < kBlk * x.nb; r += kThreads) {
+      const bool in = r < x.L;
+      const int64_t row = x.c0 + (in ? r : 0);
+      l2s[r] = in ? lse[row * H + x.h] * kLog2e : 0.0f;
+      dls[r] = in ? Dl[row * H + x.h] : 0.0f;
+    }
+    load_rows(Q, dO, Qs, Gs, x, D);
+    __syncthreads();
+    for (int k = 0;; ++k) {
+      const int j = snake_block(k, wave, x.nb, true);
+      if (j < 0) break;
+      const int key = kBlk * j + c;  // this lane's key (chain index)
+      const int64_t krow = x.c0 + min(key, x.L - 1);
+      Slice<bf16_t, KD> kf, vf;
+      kf.load(K + krow * D + x.h * kHD + KD * g);
+      vf.load(V + krow * D + x.h * kHD + KD * g);
+      f4 dk[MT], dv[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        dk[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        dv[t] = dk[t];
+      }
+      // query q0 + r sees the key iff key <= q0 + r < L: (q0 + r - key) < len
+      // as unsigned, len = L - key (0 for a key past the end)
+      const unsigned len = static_cast<unsigned>(max(x.L - key, 0));
+      for (int i = j; i < x.nb; ++i) {
+        const int qr = kBlk * i + c;  // query row this lane supplies
+        const int q0 = kBlk * i + 4 * g;
+        const int base = q0 - key;
+        Slice<bf16_t, KD> qa, ga;
+        qa.load(Qs + qr * WS + KD * g);
+        ga.load(Gs + qr * WS + KD * g);
+        const f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // query q0+r against the key
+        const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+        const f4 l2v = *reinterpret_cast<const f4*>(&l2s[q0]);
+        const f4 dlv = *reinterpret_cast<const f4*>(&dls[q0]);
+        agpt_blk::bf16x4_bits tgv[MT], tqv[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {  // dO^T, Q^T blocks: dims 16t .., queries 16i ..
+          tgv[t] = read_tr(Gs, WS, kBlk * i, kBlk * t, lane);
+          tqv[t] = read_tr(Qs, WS, kBlk * i, kBlk * t, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float p[4], ds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = fast_exp2(static_cast<unsigned>(base + r) < len ? __builtin_fmaf(sv[r], sfac, -l2v[r])
+                                                                : -__builtin_inff());
+          ds[r] = p[r] * (tv[r] - dlv[r]);
+        }
+        const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          dv[t] = mfma_a_bf16(tgv[t], pw, dv[t]);
+          dk[t] = mfma_a_bf16(tqv[t], dw, dk[t]);
+        }
+      }
+      if (key < x.L) {
+        const int pos = rope.cos_t ? rope_pos(key + 1, rope.seq_len) : 0;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const int d0 = kBlk * t + 4 * g;
+          float gk[4] = {dk[t][0] * scale, dk[t][1] * scale, dk[t][2] * scale, dk[t][3] * scale};
+          float gv[4] = {dv[t][0], dv[t][1], dv[t][2], dv[t][3]};
+          if (acc_dk) {
+            float y[4];
+            load_vec<4>(acc_dk + krow * D + x.h * kHD + d0, y);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gk[e] += y[e];
+          }
+          if (acc_dv) {
+            float y[4];
+            load_vec<4>(acc_dv + krow * D + x.h * kHD + d0, y);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gv[e] += y[e];
+          }
+          if (rope.cos_t) agpt_fast::rope_inverse_part<4, kHD>(gk, rope.cos_t, rope.sin_t, pos, d0);
+          store_vec<4>(dK + krow * D + x.h * kHD + d0, gk);
+          store_vec<4>(dV + krow * D + x.h * kHD + d0, gv);
+        }
+      }
+    }
+    __syncthreads();
+    u = uniform(next[par]);
+  }
+}
+
+}  // namespace agpt_chain

@@ -33,6 +33,7 @@ VARIANTS = {
     "block_deep_carry_rows_only": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_REGCARRY": "0", "AGPT_ATTN_CHUNK": "2"},
     "block_deep_claims_in_tile_order": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_LPT": "0"},
     "block_deep_key_side_carry_only": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_RANGE": "0"},
+    "block_deep_no_chain_kernels": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHAIN": "0"},
     "chain": {"AGPT_ATTN_VARIANT": "5"},
     "chain_hg1_qb1_kb1": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "1", "AGPT_ATTN_QB": "1",
                           "AGPT_ATTN_KB": "1"},
@@ -50,7 +51,7 @@ def variant(request, monkeypatch):
               "AGPT_ATTN_KSLOTS", "AGPT_ATTN_UH", "AGPT_ATTN_CHUNK", "AGPT_ATTN_FUSED",
               "AGPT_ATTN_FHG", "AGPT_ATTN_CARRY", "AGPT_ATTN_FUH", "AGPT_ATTN_DEEP", "AGPT_ATTN_DHPU",
               "AGPT_ATTN_REGCARRY", "AGPT_ATTN_LPT", "AGPT_ATTN_REGITERS", "AGPT_ATTN_DQ1", "AGPT_ATTN_XCD",
-              "AGPT_ATTN_RANGE"):
+              "AGPT_ATTN_RANGE", "AGPT_ATTN_CHAIN"):
         monkeypatch.delenv(k, raising=False)
     for k, v in VARIANTS[request.param].items():
         monkeypatch.setenv(k, v)
@@ -218,7 +219,9 @@ def test_chain_forest(gpu, dtype):
     """Chains of 1..256 rows back to back, so tile boundaries fall anywhere
     in them and a tile's rows may end one chain and start the next: at
     head_dim 64 every tile's subtree rows end within 8 tiles, so the key
-    side runs by subtree range (the carry under AGPT_ATTN_RANGE=0)."""
+    side runs by subtree range (the carry under AGPT_ATTN_RANGE=0); in bf16
+    the dense-causal chain kernels take the plan (the general ones under
+    AGPT_ATTN_CHAIN=0)."""
     rng = np.random.default_rng(31)
     parts, n = [], 0
     while n < 2500:
@@ -227,6 +230,28 @@ def test_chain_forest(gpu, dtype):
         n += L
     parent = np.concatenate(parts).astype(np.int32)
     _check(parent, 2, 64, seed=31, dtype=dtype, rope=True, acc=True)
+
+
+@pytest.mark.parametrize("kind", ["single", "roots", "chain17", "chain256", "chains_1_to_40"])
+def test_chain_edges_bf16(gpu, kind):
+    """Forests of chains in bf16 at head_dim 64 (the dense-causal chain
+    kernels): one row, 130 one-row chains, a chain ending inside a 16-row
+    block, a full 256-row chain, and chains of every length 1..40."""
+    if kind == "single":
+        parent = np.array([-1], np.int32)
+    elif kind == "roots":
+        parent = np.full(130, -1, np.int32)
+    elif kind == "chain17":
+        parent = np.arange(-1, 16, dtype=np.int32)
+    elif kind == "chain256":
+        parent = np.arange(-1, 255, dtype=np.int32)
+    else:
+        parts, n = [], 0
+        for L in range(1, 41):
+            parts.append(np.concatenate([[-1], np.arange(n, n + L - 1)]))
+            n += L
+        parent = np.concatenate(parts).astype(np.int32)
+    _check(parent, 2, 64, seed=len(parent) + 3, dtype="bf16", rope=True, acc=True)
 
 
 @pytest.mark.parametrize("hd", [8, 16, 64])
