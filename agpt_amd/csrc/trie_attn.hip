@@ -99,10 +99,9 @@ struct PlanDev {
   // Deep key side by subtree range (agpt_deep::bwd_kv_range_kernel).
   const int32_t* range_bend;
   const int32_t* range_order;
-  // Chain-forest plans (agpt_chain): chain k is rows chain_start[k] ..
-  // chain_start[k+1]-1; chain_order lists the chains longest first.
-  const int32_t* chain_start;
-  const int32_t* chain_order;
+  // Chain-forest plans (agpt_chain): the chains longest first, chain k of
+  // that order as (first row, rows) at chain_info[2k], [2k+1].
+  const int32_t* chain_info;
   int32_t n_chains;
 };
 
@@ -691,8 +690,7 @@ struct agpt_attn_s {
   int32_t* d_tile_order = nullptr;  // deep query side: claim order of the tiles (null: tile order)
   int32_t* d_range_bend = nullptr;  // deep key side by subtree range: [n_tiles][4] block range ends
   int32_t* d_range_order = nullptr; // and the tiles by descending range
-  int32_t* d_chain_start = nullptr; // chain-forest plans: chain row offsets [n_chains + 1]
-  int32_t* d_chain_order = nullptr; // and the chains longest first
+  int32_t* d_chain_info = nullptr;  // chain-forest plans: (first row, rows) of the chains, longest first
   int32_t n_chains = 0;
   // kernel family chosen at plan time: 0 = global-memory walk (any shape),
   // 5 = streaming chain-group walk (trie_fast.h), 6 = streaming block-sparse
@@ -734,8 +732,7 @@ void free_plan(agpt_attn_s* h) {
   const bool own = !h->static_plan;
   int32_t** ip[] = {&h->d_parent,   &h->d_depth,       &h->d_end,         &h->d_pref_off,
                     &h->d_prefix,   &h->d_pref_end,    &h->d_q_item_off,  &h->d_k_item_off,
-                    &h->d_tile_order, &h->d_range_bend, &h->d_range_order, &h->d_chain_start,
-                    &h->d_chain_order};
+                    &h->d_tile_order, &h->d_range_bend, &h->d_range_order, &h->d_chain_info};
   for (auto p : ip)
     if (*p) {
       if (own) (void)hipFree(*p);
@@ -835,8 +832,7 @@ PlanDev plan_dev(const agpt_attn_s* h) {
   p.xcd_claims = h->xcd_claims && !h->d_tile_order ? 1 : 0;
   p.range_bend = h->d_range_bend;
   p.range_order = h->d_range_order;
-  p.chain_start = h->d_chain_start;
-  p.chain_order = h->d_chain_order;
+  p.chain_info = h->d_chain_info;
   p.n_chains = h->n_chains;
   return p;
 }
@@ -1305,8 +1301,12 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
         std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
           return starts[a + 1] - starts[a] > starts[b + 1] - starts[b];
         });
-        if ((rc = upload(ar, &h->d_chain_start, starts)) != AGPT_OK) return rc;
-        if ((rc = upload(ar, &h->d_chain_order, order)) != AGPT_OK) return rc;
+        std::vector<int32_t> info(2 * static_cast<size_t>(nc));
+        for (int32_t k = 0; k < nc; ++k) {
+          info[2 * k] = starts[order[k]];
+          info[2 * k + 1] = starts[order[k] + 1] - starts[order[k]];
+        }
+        if ((rc = upload(ar, &h->d_chain_info, info)) != AGPT_OK) return rc;
         h->n_chains = nc;
         h->chain_plan = true;
       }

@@ -55,7 +55,8 @@ __device__ __forceinline__ int snake_block(int k, int w, int nb, bool key_side) 
   return key_side ? pos : nb - 1 - pos;
 }
 
-// The unit's chain and head: unit u is chain order[u / H], head u % H.
+// The unit's chain and head: unit u is chain u / H of the plan's order
+// (longest first), head u % H; (first row, rows) in one 8-byte read.
 struct ChainUnit {
   int64_t c0;  // first row
   int L;       // rows
@@ -63,42 +64,93 @@ struct ChainUnit {
   int h;
 };
 template <typename PlanT>
-__device__ __forceinline__ ChainUnit chain_unit(const PlanT& pl, int u, int H) {
+__device__ __forceinline__ int2 load_info(const PlanT& pl, int u, int H, int64_t n_units) {
+  return u < n_units ? *reinterpret_cast<const int2*>(pl.chain_info + 2 * (u / H)) : int2{0, 1};
+}
+__device__ __forceinline__ ChainUnit unit_of(int2 info, int u, int H) {
   ChainUnit x;
-  const int ci = uniform(pl.chain_order[u / H]);
-  x.h = u % H;
-  x.c0 = uniform(pl.chain_start[ci]);
-  x.L = uniform(pl.chain_start[ci + 1]) - static_cast<int>(x.c0);
+  x.c0 = uniform(info.x);
+  x.L = uniform(info.y);
   x.nb = (x.L + kBlk - 1) / kBlk;
+  x.h = u % H;
   return x;
 }
 
-// Rows 0 .. 16 nb - 1 of the unit's chain, head h, of tensors A and B into
-// the LDS tiles As and Bs. Rows past the chain repeat its last row (finite
-// values that the masks give zero weight), so every load is unconditional
-// and in bounds; all of a thread's pieces are in flight before its first
-// LDS store.
-__device__ __forceinline__ void load_rows(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
-                                          bf16_t* As, bf16_t* Bs, const ChainUnit& x, int D) {
-  constexpr int kPer = 2 * kRows * kPieces / kThreads;  // 8
-  const int per_t = kBlk * x.nb * kPieces;              // pieces of one tensor
+// A unit's rows 0 .. 16 nb - 1 (chain rows of head h) of tensors A and B,
+// fetched into registers and then stored into the LDS tiles As and Bs;
+// with kTabs also lse * log2(e) and δ of those rows (key side). Rows past
+// the chain repeat its last row (finite values that the masks give zero
+// weight), so every load is unconditional and in bounds.
+template <bool kTabs>
+struct Rows {
+  static constexpr int kPer = 2 * kRows * kPieces / kThreads;  // 8
   u4 v[kPer];
+  float rl, rd;
+  __device__ __forceinline__ void fetch(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
+                                        const float* __restrict__ lse, const float* __restrict__ Dl,
+                                        const ChainUnit& x, int D, int H) {
+    const int per_t = kBlk * x.nb * kPieces;  // pieces of one tensor
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int p = static_cast<int>(threadIdx.x) + k * kThreads;
-    const int ten = p >= per_t ? 1 : 0;
-    const int q = p - ten * per_t;
-    const int r = min(q / kPieces, x.L - 1);
-    v[k] = *reinterpret_cast<const u4*>((ten ? B : A) + (x.c0 + r) * D + x.h * kHD + (q % kPieces) * 8);
-  }
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int p = static_cast<int>(threadIdx.x) + k * kThreads;
-    if (p < 2 * per_t) {
+    for (int k = 0; k < kPer; ++k) {
+      const int p = static_cast<int>(threadIdx.x) + k * kThreads;
       const int ten = p >= per_t ? 1 : 0;
       const int q = p - ten * per_t;
-      *reinterpret_cast<u4*>((ten ? Bs : As) + (q / kPieces) * WS + (q % kPieces) * 8) = v[k];
+      const int r = min(q / kPieces, x.L - 1);
+      v[k] = *reinterpret_cast<const u4*>((ten ? B : A) + (x.c0 + r) * D + x.h * kHD + (q % kPieces) * 8);
     }
+    if constexpr (kTabs) {
+      const int64_t row = x.c0 + min(static_cast<int>(threadIdx.x), x.L - 1);
+      rl = lse[row * H + x.h];
+      rd = Dl[row * H + x.h];
+    }
+  }
+  __device__ __forceinline__ void store(bf16_t* As, bf16_t* Bs, float* l2s, float* dls, const ChainUnit& x) const {
+    const int per_t = kBlk * x.nb * kPieces;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int p = static_cast<int>(threadIdx.x) + k * kThreads;
+      if (p < 2 * per_t) {
+        const int ten = p >= per_t ? 1 : 0;
+        const int q = p - ten * per_t;
+        *reinterpret_cast<u4*>((ten ? Bs : As) + (q / kPieces) * WS + (q % kPieces) * 8) = v[k];
+      }
+    }
+    if constexpr (kTabs) {
+      if (static_cast<int>(threadIdx.x) < kRows) {
+        l2s[threadIdx.x] = rl * kLog2e;
+        dls[threadIdx.x] = rd;
+      }
+    }
+  }
+};
+
+// The unit loop of a chain kernel: the next unit is claimed while the
+// current one is worked on; body(x) works on unit x with its rows in As, Bs
+// (and l2s, dls). (Claims and row loads a unit ahead were measured: with
+// two workgroups per CU one's compute already covers the other's loads, and
+// the registers they took cost the backward kernels more than they saved.)
+template <bool kTabs, typename PlanT, typename Body>
+__device__ __forceinline__ void unit_loop(const PlanT& pl, int H, int* ctr, int32_t* next,
+                                          const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
+                                          const float* __restrict__ lse, const float* __restrict__ Dl,
+                                          bf16_t* As, bf16_t* Bs, float* l2s, float* dls, Body&& body) {
+  const int D = H * kHD;
+  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
+  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
+  __syncthreads();
+  int u = uniform(next[1]);
+  for (int par = 0; u < n_units; par ^= 1) {
+    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
+    const ChainUnit x = unit_of(load_info(pl, u, H, n_units), u, H);
+    {
+      Rows<kTabs> rows;
+      rows.fetch(A, B, lse, Dl, x, D, H);
+      rows.store(As, Bs, l2s, dls, x);
+    }
+    __syncthreads();
+    body(x);
+    __syncthreads();  // the unit's rows are no longer read
+    u = uniform(next[par]);
   }
 }
 
@@ -124,16 +176,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;  // bf16 scores come unscaled
-  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
-  int* ctr = pl.sched + 0;
-  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
-  __syncthreads();
-  int u = uniform(next[1]);
-  for (int par = 0; u < n_units; par ^= 1) {
-    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
-    const ChainUnit x = chain_unit(pl, u, H);
-    load_rows(K, V, Ks, Vs, x, D);
-    __syncthreads();
+  unit_loop<false>(pl, H, pl.sched + 0, next, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
+                   [&](const ChainUnit& x) {
+    // (Two query blocks of a wave in one pass over the key blocks, sharing
+    // the K and V^T reads, were measured no faster.)
     for (int k = 0;; ++k) {
       const int i = snake_block(k, wave, x.nb, false);
       if (i < 0) break;
@@ -186,9 +232,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (g == 0) lse[row * H + x.h] = (m + fast_log2(le)) * kLn2;
       }
     }
-    __syncthreads();  // the chain's rows are no longer read
-    u = uniform(next[par]);
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -216,16 +260,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;
-  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
-  int* ctr = pl.sched + 1;
-  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
-  __syncthreads();
-  int u = uniform(next[1]);
-  for (int par = 0; u < n_units; par ^= 1) {
-    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
-    const ChainUnit x = chain_unit(pl, u, H);
-    load_rows(K, V, Ks, Vs, x, D);
-    __syncthreads();
+  unit_loop<false>(pl, H, pl.sched + 1, next, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
+                   [&](const ChainUnit& x) {
     for (int k = 0;; ++k) {
       const int i = snake_block(k, wave, x.nb, false);
       if (i < 0) break;
@@ -290,9 +326,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (g == 0) Dl[row * H + x.h] = dl;
       }
     }
-    __syncthreads();
-    u = uniform(next[par]);
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -312,7 +346,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
   __shared__ int32_t next[2];
-  __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (0 past the end)
+  __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (past the end: the last row's)
   __shared__ alignas(16) float dls[kRows];  // δ of the chain's rows
   extern __shared__ __align__(16) unsigned char dyn[];
   bf16_t* Qs = reinterpret_cast<bf16_t*>(dyn);
@@ -322,22 +356,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;
-  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
-  int* ctr = pl.sched + 2;
-  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
-  __syncthreads();
-  int u = uniform(next[1]);
-  for (int par = 0; u < n_units; par ^= 1) {
-    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
-    const ChainUnit x = chain_unit(pl, u, H);
-    for (int r = threadIdx.x; r < kBlk * x.nb; r += kThreads) {
-      const bool in = r < x.L;
-      const int64_t row = x.c0 + (in ? r : 0);
-      l2s[r] = in ? lse[row * H + x.h] * kLog2e : 0.0f;
-      dls[r] = in ? Dl[row * H + x.h] : 0.0f;
-    }
-    load_rows(Q, dO, Qs, Gs, x, D);
-    __syncthreads();
+  unit_loop<true>(pl, H, pl.sched + 2, next, Q, dO, lse, Dl, Qs, Gs, l2s, dls, [&](const ChainUnit& x) {
     for (int k = 0;; ++k) {
       const int j = snake_block(k, wave, x.nb, true);
       if (j < 0) break;
@@ -412,9 +431,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
       }
     }
-    __syncthreads();
-    u = uniform(next[par]);
-  }
+  });
 }
 
 }  // namespace agpt_chain
