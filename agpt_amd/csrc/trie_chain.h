@@ -29,6 +29,7 @@ using agpt_blk::Slice;
 using agpt_blk::slice_dot;
 using agpt_deep::kNoMax;
 using agpt_deep::mfma_a_bf16;
+using agpt_deep::mfma_a2_bf16;
 using agpt_deep::read_tr;
 using agpt_fast::f4;
 using agpt_fast::u4;
@@ -124,11 +125,14 @@ struct Rows {
   }
 };
 
-// The unit loop of a chain kernel: the next unit is claimed while the
-// current one is worked on; body(x) works on unit x with its rows in As, Bs
-// (and l2s, dls). (Claims and row loads a unit ahead were measured: with
-// two workgroups per CU one's compute already covers the other's loads, and
-// the registers they took cost the backward kernels more than they saved.)
+// The unit loop of a chain kernel: body(x) works on unit x with its rows in
+// As, Bs (and l2s, dls). Thread 0 claims the next unit as the current one's
+// rows are requested and reads its chain's (first row, rows) once they have
+// arrived, and hands both over in next[0..2] after the body, so that no
+// wave waits on the claim or the chain table between units. (Row loads a
+// unit ahead were measured: with two workgroups per CU one's compute already
+// covers the other's loads, and the registers they took cost the backward
+// kernels more than they saved.)
 template <bool kTabs, typename PlanT, typename Body>
 __device__ __forceinline__ void unit_loop(const PlanT& pl, int H, int* ctr, int32_t* next,
                                           const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
@@ -136,21 +140,38 @@ __device__ __forceinline__ void unit_loop(const PlanT& pl, int H, int* ctr, int3
                                           bf16_t* As, bf16_t* Bs, float* l2s, float* dls, Body&& body) {
   const int D = H * kHD;
   const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
-  if (threadIdx.x == 0) next[1] = atomicAdd(ctr, 1);
+  if (threadIdx.x == 0) {
+    const int nu = atomicAdd(ctr, 1);
+    const int2 ni = load_info(pl, nu, H, n_units);
+    next[0] = nu;
+    next[1] = ni.x;
+    next[2] = ni.y;
+  }
   __syncthreads();
-  int u = uniform(next[1]);
-  for (int par = 0; u < n_units; par ^= 1) {
-    if (threadIdx.x == 0) next[par] = atomicAdd(ctr, 1);
-    const ChainUnit x = unit_of(load_info(pl, u, H, n_units), u, H);
+  int u = uniform(next[0]);
+  int2 info{uniform(next[1]), uniform(next[2])};
+  while (u < n_units) {
+    int nu = 0;
+    if (threadIdx.x == 0) nu = atomicAdd(ctr, 1);
+    const ChainUnit x = unit_of(info, u, H);
     {
       Rows<kTabs> rows;
       rows.fetch(A, B, lse, Dl, x, D, H);
       rows.store(As, Bs, l2s, dls, x);
     }
+    int2 ni{0, 1};
+    if (threadIdx.x == 0) ni = load_info(pl, nu, H, n_units);  // the claim came back before the rows
     __syncthreads();
     body(x);
+    // next[] was last read before the barrier above
+    if (threadIdx.x == 0) {
+      next[0] = nu;
+      next[1] = ni.x;
+      next[2] = ni.y;
+    }
     __syncthreads();  // the unit's rows are no longer read
-    u = uniform(next[par]);
+    u = uniform(next[0]);
+    info = int2{uniform(next[1]), uniform(next[2])};
   }
 }
 
@@ -167,7 +188,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                                                        float* __restrict__ lse, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ int32_t next[2];
+  __shared__ int32_t next[3];
   extern __shared__ __align__(16) unsigned char dyn[];
   bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
   bf16_t* Vs = Ks + kRows * WS;
@@ -192,15 +213,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       for (int j = 0; j < MT; ++j) o[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
       // key 16kb + 4g + r is live iff it is <= min(q, L - 1), i.e. r <= t
       const int tq = min(q, x.L - 1) - 4 * g;
-      for (int kb = 0; kb <= i; ++kb) {
-        Slice<bf16_t, KD> kf;
-        kf.load(Ks + (kBlk * kb + c) * WS + KD * g);
-        const f4 sv = slice_dot(kf, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16kb+4g+r against query q
-        const int t = tq - kBlk * kb;
-        float sc[4];
+      // Key blocks kb and kb + 1 in one step: one online-softmax update for
+      // both and one 32-deep O^T product per output tile. Only the step
+      // that holds the diagonal block i is masked (blocks below i are whole
+      // chain rows); past block i its second half reads block i again with
+      // every weight masked to 0.
+      auto step = [&](int kb, auto masked) {
+        const int kb1 = min(kb + 1, i);
+        Slice<bf16_t, KD> kf0, kf1;
+        kf0.load(Ks + (kBlk * kb + c) * WS + KD * g);
+        kf1.load(Ks + (kBlk * kb1 + c) * WS + KD * g);
+        const f4 sv0 = slice_dot(kf0, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16kb+4g+r against query q
+        const f4 sv1 = slice_dot(kf1, qf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // key 16(kb+1)+4g+r
+        float sc[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = r <= t ? sv[r] : -__builtin_inff();
-        const float lmx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * sfac;
+        for (int r = 0; r < 4; ++r) {
+          sc[r] = sv0[r];
+          sc[4 + r] = sv1[r];
+        }
+        if constexpr (decltype(masked)::value) {
+          const int t = tq - kBlk * kb;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[r] = r <= t ? sc[r] : -__builtin_inff();
+            sc[4 + r] = r + kBlk <= t ? sc[4 + r] : -__builtin_inff();
+          }
+        }
+        const float lmx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                                fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]))) * sfac;
         if (__any(lmx > m + kRescaleLog2)) {
           const float mx = group_max(lmx);
           const bool resc = mx > m + kRescaleLog2;
@@ -210,16 +250,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
           for (int j = 0; j < MT; ++j) o[j] *= a;
         }
-        float p[4];
+        float p[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 8; ++r) {
           p[r] = fast_exp2(__builtin_fmaf(sc[r], sfac, -m));  // masked: exp2(-inf) = 0
           l += p[r];
         }
-        const uint2 pw = pack_bf16(p);
+        const float p0[4] = {p[0], p[1], p[2], p[3]}, p1[4] = {p[4], p[5], p[6], p[7]};
+        const uint2 pw0 = pack_bf16(p0), pw1 = pack_bf16(p1);
 #pragma unroll
-        for (int j = 0; j < MT; ++j) o[j] = mfma_a_bf16(read_tr(Vs, WS, kBlk * kb, kBlk * j, lane), pw, o[j]);
-      }
+        for (int j = 0; j < MT; ++j)  // V^T blocks: dims 16j .., keys 16kb .. and 16kb1 ..
+          o[j] = mfma_a2_bf16(read_tr(Vs, WS, kBlk * kb, kBlk * j, lane), read_tr(Vs, WS, kBlk * kb1, kBlk * j, lane),
+                              pw0, pw1, o[j]);
+      };
+      int kb = 0;
+      for (; kb + 1 < i; kb += 2) step(kb, std::false_type{});
+      step(kb, std::true_type{});
       const float le = group_sum(l);
       if (q < x.L) {
         const int64_t row = x.c0 + q;
@@ -251,7 +297,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                                                          float* __restrict__ Dl, RopeT rope, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ int32_t next[2];
+  __shared__ int32_t next[3];
   extern __shared__ __align__(16) unsigned char dyn[];
   bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
   bf16_t* Vs = Ks + kRows * WS;
@@ -305,10 +351,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const uint2 pl2 = pack_bf16(plo), al2 = pack_bf16(alo);
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
-          dq[j] = mfma_a_bf16(tkv[j], ah, dq[j]);
-          dq[j] = mfma_a_bf16(tkv[j], al2, dq[j]);
-          dqw[j] = mfma_a_bf16(tkv[j], ph, dqw[j]);
-          dqw[j] = mfma_a_bf16(tkv[j], pl2, dqw[j]);
+          dq[j] = mfma_a2_bf16(tkv[j], tkv[j], ah, al2, dq[j]);  // high and low bf16 parts in one step
+          dqw[j] = mfma_a2_bf16(tkv[j], tkv[j], ph, pl2, dqw[j]);
         }
       }
       const float dl = group_sum(acc);
@@ -345,7 +389,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ int32_t next[2];
+  __shared__ int32_t next[3];
   __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (past the end: the last row's)
   __shared__ alignas(16) float dls[kRows];  // δ of the chain's rows
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -374,36 +418,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       // query q0 + r sees the key iff key <= q0 + r < L: (q0 + r - key) < len
       // as unsigned, len = L - key (0 for a key past the end)
       const unsigned len = static_cast<unsigned>(max(x.L - key, 0));
-      for (int i = j; i < x.nb; ++i) {
-        const int qr = kBlk * i + c;  // query row this lane supplies
-        const int q0 = kBlk * i + 4 * g;
-        const int base = q0 - key;
-        Slice<bf16_t, KD> qa, ga;
-        qa.load(Qs + qr * WS + KD * g);
-        ga.load(Gs + qr * WS + KD * g);
-        const f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // query q0+r against the key
-        const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
-        const f4 l2v = *reinterpret_cast<const f4*>(&l2s[q0]);
-        const f4 dlv = *reinterpret_cast<const f4*>(&dls[q0]);
-        agpt_blk::bf16x4_bits tgv[MT], tqv[MT];
+      // Query blocks in pairs (i, i + 1), their dV and dK products summed by
+      // one 32-deep step per output tile; past the last block the pair's
+      // second half reads block i again, with every weight masked to 0.
+      for (int i = j; i < x.nb; i += 2) {
+        const int ib[2] = {i, min(i + 1, x.nb - 1)};
+        uint2 pw[2], dw[2];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {  // dO^T, Q^T blocks: dims 16t .., queries 16i ..
-          tgv[t] = read_tr(Gs, WS, kBlk * i, kBlk * t, lane);
-          tqv[t] = read_tr(Qs, WS, kBlk * i, kBlk * t, lane);
+        for (int h = 0; h < 2; ++h) {
+          const int qr = kBlk * ib[h] + c;  // query row this lane supplies
+          const int q0 = kBlk * ib[h] + 4 * g;
+          const int base = kBlk * (i + h) + 4 * g - key;
+          Slice<bf16_t, KD> qa, ga;
+          qa.load(Qs + qr * WS + KD * g);
+          ga.load(Gs + qr * WS + KD * g);
+          const f4 sv = slice_dot(qa, kf, f4{0.0f, 0.0f, 0.0f, 0.0f});  // query q0+r against the key
+          const f4 tv = slice_dot(ga, vf, f4{0.0f, 0.0f, 0.0f, 0.0f});
+          const f4 l2v = *reinterpret_cast<const f4*>(&l2s[q0]);
+          const f4 dlv = *reinterpret_cast<const f4*>(&dls[q0]);
+          float p[4], ds[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[r] = fast_exp2(static_cast<unsigned>(base + r) < len ? __builtin_fmaf(sv[r], sfac, -l2v[r])
+                                                                  : -__builtin_inff());
+            ds[r] = p[r] * (tv[r] - dlv[r]);
+          }
+          pw[h] = pack_bf16(p);
+          dw[h] = pack_bf16(ds);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        float p[4], ds[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[r] = fast_exp2(static_cast<unsigned>(base + r) < len ? __builtin_fmaf(sv[r], sfac, -l2v[r])
-                                                                : -__builtin_inff());
-          ds[r] = p[r] * (tv[r] - dlv[r]);
-        }
-        const uint2 pw = pack_bf16(p), dw = pack_bf16(ds);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          dv[t] = mfma_a_bf16(tgv[t], pw, dv[t]);
-          dk[t] = mfma_a_bf16(tqv[t], dw, dk[t]);
+        for (int t = 0; t < MT; ++t) {  // dO^T, Q^T blocks: dims 16t .., queries 16 ib[h] ..
+          dv[t] = mfma_a2_bf16(read_tr(Gs, WS, kBlk * ib[0], kBlk * t, lane), read_tr(Gs, WS, kBlk * ib[1], kBlk * t, lane),
+                               pw[0], pw[1], dv[t]);
+          dk[t] = mfma_a2_bf16(read_tr(Qs, WS, kBlk * ib[0], kBlk * t, lane), read_tr(Qs, WS, kBlk * ib[1], kBlk * t, lane),
+                               dw[0], dw[1], dk[t]);
         }
       }
       if (key < x.L) {

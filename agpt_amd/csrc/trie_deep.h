@@ -106,6 +106,18 @@ __device__ __forceinline__ agpt_blk::bf16x4_bits read_tr(const bf16_t* R, int ws
 __device__ __forceinline__ f4 mfma_a_bf16(agpt_blk::bf16x4_bits a, uint2 wb, f4 acc) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(agpt_blk::bf16x4_bits, wb), acc, 0, 0, 0);
 }
+// acc + a0·b0 + a1·b1 (each as in mfma_a_bf16) in one 32-deep step, which
+// takes the time of one 16-deep step: a lane's eight reduction elements are
+// its four of a0 (b0) then its four of a1 (b1) in both operands, so each
+// element of A meets its own element of B.
+__device__ __forceinline__ f4 mfma_a2_bf16(agpt_blk::bf16x4_bits a0, agpt_blk::bf16x4_bits a1, uint2 b0, uint2 b1,
+                                           f4 acc) {
+  typedef __attribute__((ext_vector_type(8))) __bf16 b8;
+  const uint2 x0 = __builtin_bit_cast(uint2, a0), x1 = __builtin_bit_cast(uint2, a1);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, uint4{x0.x, x0.y, x1.x, x1.y}),
+                                                 __builtin_bit_cast(b8, uint4{b0.x, b0.y, b1.x, b1.y}), acc, 0, 0,
+                                                 0);
+}
 
 // The tile's key list and row tables. Keys 0 .. A-1 are the prefix rows
 // (depth 1 .. A), keys A .. A+ntile-1 the tile rows; the list is padded to
@@ -506,7 +518,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
 // side; dQ gets the inverse rotation at the query's depth.
 // ---------------------------------------------------------------------------
 template <int HD, typename Tin, typename PlanT, typename RopeT, bool kOnePass = false>
-__global__ __launch_bounds__(kThreads) void bwd_q_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kOnePass ? 3 : 2))) void bwd_q_kernel(
     PlanT pl, const Tin* __restrict__ Q, const Tin* __restrict__ K, const Tin* __restrict__ V,
     const Tin* __restrict__ O, const float* __restrict__ lse, const Tin* __restrict__ dO,
     float* __restrict__ dQ, float* __restrict__ Dl, RopeT rope, int H, int hpu, float scale) {
@@ -661,10 +673,8 @@ __global__ __launch_bounds__(kThreads) void bwd_q_kernel(
           const uint2 pl2 = pack_bf16(plo), al2 = pack_bf16(alo);
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
-            dq[j] = mfma_a_bf16(tkv[j], ah, dq[j]);
-            dq[j] = mfma_a_bf16(tkv[j], al2, dq[j]);
-            dqw[j] = mfma_a_bf16(tkv[j], ph, dqw[j]);
-            dqw[j] = mfma_a_bf16(tkv[j], pl2, dqw[j]);
+            dq[j] = mfma_a2_bf16(tkv[j], tkv[j], ah, al2, dq[j]);  // high and low bf16 parts in one step
+            dqw[j] = mfma_a2_bf16(tkv[j], tkv[j], ph, pl2, dqw[j]);
           }
           continue;
         }
