@@ -63,6 +63,11 @@ struct ChainUnit {
   int L;       // rows
   int nb;      // 16-row blocks
   int h;
+  // Element offsets of the unit's first row, head h, in a [T, D] tensor and
+  // in a [T, H] table (uniform; rows within the unit are added as 32-bit
+  // offsets, so that per-lane addresses are a scalar base and one VGPR).
+  __device__ __forceinline__ int64_t at(int D) const { return c0 * D + h * kHD; }
+  __device__ __forceinline__ int64_t tab(int H) const { return c0 * H + h; }
 };
 template <typename PlanT>
 __device__ __forceinline__ int2 load_info(const PlanT& pl, int u, int H, int64_t n_units) {
@@ -84,36 +89,38 @@ __device__ __forceinline__ ChainUnit unit_of(int2 info, int u, int H) {
 // weight), so every load is unconditional and in bounds.
 template <bool kTabs>
 struct Rows {
-  static constexpr int kPer = 2 * kRows * kPieces / kThreads;  // 8
-  u4 v[kPer];
+  static constexpr int kPer = kRows * kPieces / kThreads;  // 4 rows of each tensor per thread
+  u4 a[kPer], b[kPer];
   float rl, rd;
+  // Thread t fetches 16-byte piece t % 8 of rows t / 8 + 64 k.
   __device__ __forceinline__ void fetch(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
                                         const float* __restrict__ lse, const float* __restrict__ Dl,
                                         const ChainUnit& x, int D, int H) {
-    const int per_t = kBlk * x.nb * kPieces;  // pieces of one tensor
+    const int r0 = static_cast<int>(threadIdx.x) / kPieces;
+    const int col = (threadIdx.x % kPieces) * 8;
+    const bf16_t* Au = A + x.at(D);
+    const bf16_t* Bu = B + x.at(D);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int p = static_cast<int>(threadIdx.x) + k * kThreads;
-      const int ten = p >= per_t ? 1 : 0;
-      const int q = p - ten * per_t;
-      const int r = min(q / kPieces, x.L - 1);
-      v[k] = *reinterpret_cast<const u4*>((ten ? B : A) + (x.c0 + r) * D + x.h * kHD + (q % kPieces) * 8);
+      const unsigned o = static_cast<unsigned>(min(r0 + k * (kThreads / kPieces), x.L - 1) * D + col);
+      a[k] = *reinterpret_cast<const u4*>(Au + o);
+      b[k] = *reinterpret_cast<const u4*>(Bu + o);
     }
     if constexpr (kTabs) {
-      const int64_t row = x.c0 + min(static_cast<int>(threadIdx.x), x.L - 1);
-      rl = lse[row * H + x.h];
-      rd = Dl[row * H + x.h];
+      const unsigned o = static_cast<unsigned>(min(static_cast<int>(threadIdx.x), x.L - 1) * H);
+      rl = lse[x.tab(H) + o];
+      rd = Dl[x.tab(H) + o];
     }
   }
   __device__ __forceinline__ void store(bf16_t* As, bf16_t* Bs, float* l2s, float* dls, const ChainUnit& x) const {
-    const int per_t = kBlk * x.nb * kPieces;
+    const int r0 = static_cast<int>(threadIdx.x) / kPieces;
+    const int col = (threadIdx.x % kPieces) * 8;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int p = static_cast<int>(threadIdx.x) + k * kThreads;
-      if (p < 2 * per_t) {
-        const int ten = p >= per_t ? 1 : 0;
-        const int q = p - ten * per_t;
-        *reinterpret_cast<u4*>((ten ? Bs : As) + (q / kPieces) * WS + (q % kPieces) * 8) = v[k];
+      const int r = r0 + k * (kThreads / kPieces);
+      if (r < kBlk * x.nb) {
+        *reinterpret_cast<u4*>(As + r * WS + col) = a[k];
+        *reinterpret_cast<u4*>(Bs + r * WS + col) = b[k];
       }
     }
     if constexpr (kTabs) {
@@ -206,7 +213,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       if (i < 0) break;
       const int q = kBlk * i + c;  // this lane's query (chain index)
       Slice<bf16_t, KD> qf;
-      qf.load(Q + (x.c0 + min(q, x.L - 1)) * D + x.h * kHD + KD * g);
+      qf.load(Q + x.at(D) + static_cast<unsigned>(min(q, x.L - 1) * D + KD * g));
       float m = kNoMax, l = 0.0f;
       f4 o[MT];
 #pragma unroll
@@ -268,14 +275,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       step(kb, std::true_type{});
       const float le = group_sum(l);
       if (q < x.L) {
-        const int64_t row = x.c0 + q;
         const float inv = __builtin_amdgcn_rcpf(le);
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
           float v[4] = {o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv};
-          store_vec<4>(O + row * D + x.h * kHD + kBlk * j + 4 * g, v);
+          store_vec<4>(O + x.at(D) + static_cast<unsigned>(q * D + kBlk * j + 4 * g), v);
         }
-        if (g == 0) lse[row * H + x.h] = (m + fast_log2(le)) * kLn2;
+        if (g == 0) lse[x.tab(H) + static_cast<unsigned>(q * H)] = (m + fast_log2(le)) * kLn2;
       }
     }
   });
@@ -312,11 +318,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       const int i = snake_block(k, wave, x.nb, false);
       if (i < 0) break;
       const int q = kBlk * i + c;
-      const int64_t qrow = x.c0 + min(q, x.L - 1);
+      const int qr = min(q, x.L - 1);
       Slice<bf16_t, KD> qf, gf;
-      qf.load(Q + qrow * D + x.h * kHD + KD * g);
-      gf.load(dO + qrow * D + x.h * kHD + KD * g);
-      const float l2 = lse[qrow * H + x.h] * kLog2e;
+      qf.load(Q + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
+      gf.load(dO + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
+      const float l2 = lse[x.tab(H) + static_cast<unsigned>(qr * H)] * kLog2e;
       f4 dq[MT], dqw[MT];  // Σ a_j k_j and Σ w_j k_j
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
@@ -357,7 +363,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       }
       const float dl = group_sum(acc);
       if (q < x.L) {
-        const int64_t row = x.c0 + q;
         const int pos = rope.cos_t ? rope_pos(q + 1, rope.seq_len) : 0;  // a chain's row q is at depth q + 1
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
@@ -365,9 +370,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] = (dq[j][r] - dl * dqw[j][r]) * scale;
           if (rope.cos_t) agpt_fast::rope_inverse_part<4, kHD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
-          store_vec<4>(dQ + row * D + x.h * kHD + kBlk * j + 4 * g, v);
+          store_vec<4>(dQ + x.at(D) + static_cast<unsigned>(q * D + kBlk * j + 4 * g), v);
         }
-        if (g == 0) Dl[row * H + x.h] = dl;
+        if (g == 0) Dl[x.tab(H) + static_cast<unsigned>(q * H)] = dl;
       }
     }
   });
@@ -405,10 +410,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       const int j = snake_block(k, wave, x.nb, true);
       if (j < 0) break;
       const int key = kBlk * j + c;  // this lane's key (chain index)
-      const int64_t krow = x.c0 + min(key, x.L - 1);
+      const int kr = min(key, x.L - 1);
       Slice<bf16_t, KD> kf, vf;
-      kf.load(K + krow * D + x.h * kHD + KD * g);
-      vf.load(V + krow * D + x.h * kHD + KD * g);
+      kf.load(K + x.at(D) + static_cast<unsigned>(kr * D + KD * g));
+      vf.load(V + x.at(D) + static_cast<unsigned>(kr * D + KD * g));
       f4 dk[MT], dv[MT];
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
@@ -459,23 +464,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           const int d0 = kBlk * t + 4 * g;
+          const unsigned ko = static_cast<unsigned>(kr * D + d0);
           float gk[4] = {dk[t][0] * scale, dk[t][1] * scale, dk[t][2] * scale, dk[t][3] * scale};
           float gv[4] = {dv[t][0], dv[t][1], dv[t][2], dv[t][3]};
           if (acc_dk) {
             float y[4];
-            load_vec<4>(acc_dk + krow * D + x.h * kHD + d0, y);
+            load_vec<4>(acc_dk + x.at(D) + ko, y);
 #pragma unroll
             for (int e = 0; e < 4; ++e) gk[e] += y[e];
           }
           if (acc_dv) {
             float y[4];
-            load_vec<4>(acc_dv + krow * D + x.h * kHD + d0, y);
+            load_vec<4>(acc_dv + x.at(D) + ko, y);
 #pragma unroll
             for (int e = 0; e < 4; ++e) gv[e] += y[e];
           }
           if (rope.cos_t) agpt_fast::rope_inverse_part<4, kHD>(gk, rope.cos_t, rope.sin_t, pos, d0);
-          store_vec<4>(dK + krow * D + x.h * kHD + d0, gk);
-          store_vec<4>(dV + krow * D + x.h * kHD + d0, gv);
+          store_vec<4>(dK + x.at(D) + ko, gk);
+          store_vec<4>(dV + x.at(D) + ko, gv);
         }
       }
     }
