@@ -206,14 +206,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const float sfac = scale * kLog2e;  // bf16 scores come unscaled
   unit_loop<false>(pl, H, pl.sched + 0, next, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
                    [&](const ChainUnit& x) {
-    // (Two query blocks of a wave in one pass over the key blocks, sharing
-    // the K and V^T reads, were measured no faster.)
-    for (int k = 0;; ++k) {
-      const int i = snake_block(k, wave, x.nb, false);
-      if (i < 0) break;
+    // The wave's blocks, costliest first: at most two (nb <= 16, eight
+    // waves). Both blocks' Q slices are requested at once, so the second's
+    // arrive while the first block is worked on. (Both blocks in one pass
+    // over the key blocks, sharing the K and V^T reads, was measured no
+    // faster.)
+    const int iA = snake_block(0, wave, x.nb, false);
+    if (iA < 0) return;
+    const int iB = snake_block(1, wave, x.nb, false);
+    Slice<bf16_t, KD> qs[2];
+    qs[0].load(Q + x.at(D) + static_cast<unsigned>(min(kBlk * iA + c, x.L - 1) * D + KD * g));
+    qs[1].load(Q + x.at(D) + static_cast<unsigned>(min(kBlk * max(iB, 0) + c, x.L - 1) * D + KD * g));
+    auto block = [&](int i, const Slice<bf16_t, KD>& qf) {
       const int q = kBlk * i + c;  // this lane's query (chain index)
-      Slice<bf16_t, KD> qf;
-      qf.load(Q + x.at(D) + static_cast<unsigned>(min(q, x.L - 1) * D + KD * g));
       float m = kNoMax, l = 0.0f;
       f4 o[MT];
 #pragma unroll
@@ -274,6 +279,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       for (; kb + 1 < i; kb += 2) step(kb, std::false_type{});
       step(kb, std::true_type{});
       const float le = group_sum(l);
+      // Every slice has arrived: waiting here, before this block's stores,
+      // the next block starts with no wait (one after the stores would
+      // also wait for them).
+      agpt_deep::wait_loads();
       if (q < x.L) {
         const float inv = __builtin_amdgcn_rcpf(le);
 #pragma unroll
@@ -283,7 +292,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         if (g == 0) lse[x.tab(H) + static_cast<unsigned>(q * H)] = (m + fast_log2(le)) * kLn2;
       }
-    }
+    };
+    block(iA, qs[0]);
+    if (iB >= 0) block(iB, qs[1]);
   });
 }
 
@@ -314,15 +325,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const float sfac = scale * kLog2e;
   unit_loop<false>(pl, H, pl.sched + 1, next, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
                    [&](const ChainUnit& x) {
-    for (int k = 0;; ++k) {
-      const int i = snake_block(k, wave, x.nb, false);
-      if (i < 0) break;
-      const int q = kBlk * i + c;
-      const int qr = min(q, x.L - 1);
+    // The wave's (at most two) blocks, costliest first, with both blocks'
+    // Q and dO slices and lse requested at once.
+    const int iA = snake_block(0, wave, x.nb, false);
+    if (iA < 0) return;
+    const int iB = snake_block(1, wave, x.nb, false);
+    struct QIn {
       Slice<bf16_t, KD> qf, gf;
-      qf.load(Q + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
-      gf.load(dO + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
-      const float l2 = lse[x.tab(H) + static_cast<unsigned>(qr * H)] * kLog2e;
+      float ls;
+    } in[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int qr = min(kBlk * (e ? max(iB, 0) : iA) + c, x.L - 1);
+      in[e].qf.load(Q + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
+      in[e].gf.load(dO + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
+      in[e].ls = lse[x.tab(H) + static_cast<unsigned>(qr * H)];
+    }
+    auto block = [&](int i, const QIn& qin) {
+      const int q = kBlk * i + c;
+      const Slice<bf16_t, KD>& qf = qin.qf;
+      const Slice<bf16_t, KD>& gf = qin.gf;
+      const float l2 = qin.ls * kLog2e;
       f4 dq[MT], dqw[MT];  // Σ a_j k_j and Σ w_j k_j
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
@@ -362,6 +385,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
       }
       const float dl = group_sum(acc);
+      agpt_deep::wait_loads();  // every input has arrived; the next block then starts with no wait
       if (q < x.L) {
         const int pos = rope.cos_t ? rope_pos(q + 1, rope.seq_len) : 0;  // a chain's row q is at depth q + 1
 #pragma unroll
@@ -374,7 +398,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         if (g == 0) Dl[x.tab(H) + static_cast<unsigned>(q * H)] = dl;
       }
-    }
+    };
+    block(iA, in[0]);
+    if (iB >= 0) block(iB, in[1]);
   });
 }
 
