@@ -1704,8 +1704,7 @@ void launch_fwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   pm.mark(0);
   if (h->variant == 6 && h->deep) {
     if constexpr (HD == 64 && sizeof(Tin) == 2) {
-      if (h->chain_plan) {
-        clear_sched(h, st);
+      if (h->chain_plan) {  // units dealt by the grid: no counters to clear
         auto fn = agpt_chain::fwd_kernel<PlanDev>;
         set_lds(fn, agpt_chain::lds_bytes());
         hipLaunchKernelGGL(fn, dim3(chain_grid(h, fn)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,
@@ -1825,8 +1824,7 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if (fused_done) {
   } else if (h->variant == 6 && h->deep) {
     if constexpr (HD == 64 && sizeof(Tin) == 2) {
-      if (h->chain_plan) {
-        clear_sched(h, st);
+      if (h->chain_plan) {  // units dealt by the grid: no counters to clear
         auto fq = agpt_chain::bwd_q_kernel<PlanDev, RopeArgs>;
         set_lds(fq, agpt_chain::lds_bytes());
         hipLaunchKernelGGL(fq, dim3(chain_grid(h, fq)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,

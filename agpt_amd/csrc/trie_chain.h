@@ -132,53 +132,45 @@ struct Rows {
   }
 };
 
+// Unit k of this workgroup: the plan's units (longest chains first) dealt
+// to the G workgroups in snake order (0 .. G-1, then G-1 .. 0, ..), so the
+// workgroups' totals are close. The deal is fixed by the grid: no claim
+// counters, so nothing needs clearing before a launch.
+__device__ __forceinline__ int dealt_unit(int k) {
+  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  return k * G + ((k & 1) ? G - 1 - b : b);
+}
+
 // The unit loop of a chain kernel: body(x) works on unit x with its rows in
-// As, Bs (and l2s, dls). Thread 0 claims the next unit as the current one's
-// rows are requested and reads its chain's (first row, rows) once they have
-// arrived, and hands both over in next[0..2] after the body, so that no
-// wave waits on the claim or the chain table between units. (Row loads a
-// unit ahead were measured: with two workgroups per CU one's compute already
-// covers the other's loads, and the registers they took cost the backward
-// kernels more than they saved.)
+// As, Bs (and l2s, dls). The next unit's chain (first row, rows) is read
+// while the current unit's rows are fetched. (Row loads a unit ahead were
+// measured: with two workgroups per CU one's compute already covers the
+// other's loads, and the registers they took cost the backward kernels
+// more than they saved.)
 template <bool kTabs, typename PlanT, typename Body>
-__device__ __forceinline__ void unit_loop(const PlanT& pl, int H, int* ctr, int32_t* next,
-                                          const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
-                                          const float* __restrict__ lse, const float* __restrict__ Dl,
-                                          bf16_t* As, bf16_t* Bs, float* l2s, float* dls, Body&& body) {
+__device__ __forceinline__ void unit_loop(const PlanT& pl, int H, const bf16_t* __restrict__ A,
+                                          const bf16_t* __restrict__ B, const float* __restrict__ lse,
+                                          const float* __restrict__ Dl, bf16_t* As, bf16_t* Bs, float* l2s,
+                                          float* dls, Body&& body) {
   const int D = H * kHD;
   const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
-  if (threadIdx.x == 0) {
-    const int nu = atomicAdd(ctr, 1);
-    const int2 ni = load_info(pl, nu, H, n_units);
-    next[0] = nu;
-    next[1] = ni.x;
-    next[2] = ni.y;
-  }
-  __syncthreads();
-  int u = uniform(next[0]);
-  int2 info{uniform(next[1]), uniform(next[2])};
+  int k = 0;
+  int u = dealt_unit(0);
+  int2 info = load_info(pl, u, H, n_units);
   while (u < n_units) {
-    int nu = 0;
-    if (threadIdx.x == 0) nu = atomicAdd(ctr, 1);
+    const int nu = dealt_unit(++k);
     const ChainUnit x = unit_of(info, u, H);
     {
       Rows<kTabs> rows;
       rows.fetch(A, B, lse, Dl, x, D, H);
       rows.store(As, Bs, l2s, dls, x);
     }
-    int2 ni{0, 1};
-    if (threadIdx.x == 0) ni = load_info(pl, nu, H, n_units);  // the claim came back before the rows
+    const int2 ni = load_info(pl, nu, H, n_units);
     __syncthreads();
     body(x);
-    // next[] was last read before the barrier above
-    if (threadIdx.x == 0) {
-      next[0] = nu;
-      next[1] = ni.x;
-      next[2] = ni.y;
-    }
     __syncthreads();  // the unit's rows are no longer read
-    u = uniform(next[0]);
-    info = int2{uniform(next[1]), uniform(next[2])};
+    u = nu;
+    info = ni;
   }
 }
 
@@ -195,7 +187,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                                                        float* __restrict__ lse, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ int32_t next[3];
   extern __shared__ __align__(16) unsigned char dyn[];
   bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
   bf16_t* Vs = Ks + kRows * WS;
@@ -204,7 +195,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;  // bf16 scores come unscaled
-  unit_loop<false>(pl, H, pl.sched + 0, next, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
+  unit_loop<false>(pl, H, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
                    [&](const ChainUnit& x) {
     // The wave's blocks, costliest first: at most two (nb <= 16, eight
     // waves). Both blocks' Q slices are requested at once, so the second's
@@ -314,7 +305,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                                                          float* __restrict__ Dl, RopeT rope, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ int32_t next[3];
   extern __shared__ __align__(16) unsigned char dyn[];
   bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
   bf16_t* Vs = Ks + kRows * WS;
@@ -323,7 +313,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;
-  unit_loop<false>(pl, H, pl.sched + 1, next, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
+  unit_loop<false>(pl, H, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
                    [&](const ChainUnit& x) {
     // The wave's (at most two) blocks, costliest first, with both blocks'
     // Q and dO slices and lse requested at once.
@@ -420,7 +410,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ int32_t next[3];
   __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (past the end: the last row's)
   __shared__ alignas(16) float dls[kRows];  // δ of the chain's rows
   extern __shared__ __align__(16) unsigned char dyn[];
@@ -431,7 +420,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;
-  unit_loop<true>(pl, H, pl.sched + 2, next, Q, dO, lse, Dl, Qs, Gs, l2s, dls, [&](const ChainUnit& x) {
+  unit_loop<true>(pl, H, Q, dO, lse, Dl, Qs, Gs, l2s, dls, [&](const ChainUnit& x) {
     for (int k = 0;; ++k) {
       const int j = snake_block(k, wave, x.nb, true);
       if (j < 0) break;

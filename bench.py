@@ -808,23 +808,22 @@ def main() -> int:
         log(f"warmup step {i + 1}/{args.warmup} done")
 
     hev = HipEvents()
-    # One batch: the per-kernel events ride along in the timed steps. Many
-    # batches: the timed steps run without them (7 event records per batch
-    # are host work of their own) and the per-kernel times come from as many
+    # The timed steps run without per-kernel events (7 event records per
+    # batch are work of their own on the stream: ~10 us per step, which a
+    # sub-millisecond C5 step shows); the per-kernel times come from as many
     # steps again with the events, outside the timed region.
     ev_steps = args.steps
     evs = [[(hev.create(2), hev.create(5)) for _ in parts] for _ in range(ev_steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(evs[i] if len(parts) == 1 else None)
+        step(None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
-    if len(parts) > 1:
-        for i in range(ev_steps):
-            step(evs[i])
-        torch.cuda.synchronize()
+    for i in range(ev_steps):
+        step(evs[i])
+    torch.cuda.synchronize()
     desc = parts[0].describe()
     split = "split backward" in desc
     carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce
