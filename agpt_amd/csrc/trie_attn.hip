@@ -708,6 +708,7 @@ struct agpt_attn_s {
   bool xcd_claims = true;       // deep query side in tile order: claims by XCD ranges
   bool deep_range = false;      // deep key side over each tile's subtree range (short subtrees)
   bool chain_plan = false;      // bf16 head_dim 64 on a forest of chains: the agpt_chain kernels
+  bool chain_fused = true;      // chain plans: the backward in one launch (AGPT_ATTN_CHAINFUSE=0: two)
   float* d_Cs = nullptr;        // deep carry: per-workgroup carry rows [slot][2][P][2][head_dim]
   int cs_slots = 0;             // workgroups the carry rows are sized for
   float* d_E = nullptr;         // carry: per-chunk partials [n_chunks][P][2][D]
@@ -1309,6 +1310,7 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
         if ((rc = upload(ar, &h->d_chain_info, info)) != AGPT_OK) return rc;
         h->n_chains = nc;
         h->chain_plan = true;
+        h->chain_fused = env_int("AGPT_ATTN_CHAINFUSE", 1) != 0;
       }
     }
     // Up to 24 tiles per claim (the carry's reach), but at least ~8 chunks
@@ -1509,8 +1511,11 @@ extern "C" const char* agpt_attn_describe(agpt_attn_handle h) {
   if (h->variant == 6 && h->deep && h->chain_plan)
     snprintf(buf, sizeof(buf),
              "dense-causal chain kernels (a forest of %d chains; unit = chain x head, %d waves, the chain's rows "
-             "in LDS), split backward with the key side by subtree range: lds=%zu lds_limit=%d",
-             h->n_chains, agpt_chain::kWaves, agpt_chain::lds_bytes(), h->max_lds);
+             "in LDS), %s: lds=%zu lds_limit=%d",
+             h->n_chains, agpt_chain::kWaves,
+             h->chain_fused ? "one-launch backward (query side, then key side per unit; nothing to reduce)"
+                            : "split backward with the key side by subtree range",
+             agpt_chain::lds_bytes(), h->max_lds);
   else if (h->variant == 6 && h->deep)
     snprintf(buf, sizeof(buf),
              "streamed key ring (deep prefixes) 16x16 mfma, split backward%s: tile_rows=%d tiles=%d "
@@ -1824,7 +1829,20 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
   if (fused_done) {
   } else if (h->variant == 6 && h->deep) {
     if constexpr (HD == 64 && sizeof(Tin) == 2) {
-      if (h->chain_plan) {  // units dealt by the grid: no counters to clear
+      if (h->chain_plan && h->chain_fused) {  // units dealt by the grid: no counters to clear
+        auto fb = agpt_chain::bwd_kernel<PlanDev, RopeArgs>;
+        set_lds(fb, agpt_chain::lds_bytes());
+        hipLaunchKernelGGL(fb, dim3(chain_grid(h, fb)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,
+                           plan_dev(h), static_cast<const Tin*>(q), static_cast<const Tin*>(k),
+                           static_cast<const Tin*>(v), lse, static_cast<const Tin*>(dO), dq, dk, dv, acc_dk,
+                           acc_dv, rope, h->cfg.n_heads, scale);
+        pm.mark(1);
+        pm.mark(2);
+        pm.mark(3);
+        pm.mark(4);
+        return;
+      }
+      if (h->chain_plan) {
         auto fq = agpt_chain::bwd_q_kernel<PlanDev, RopeArgs>;
         set_lds(fq, agpt_chain::lds_bytes());
         hipLaunchKernelGGL(fq, dim3(chain_grid(h, fq)), dim3(agpt_chain::kThreads), agpt_chain::lds_bytes(), st,

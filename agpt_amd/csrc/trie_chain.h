@@ -82,12 +82,25 @@ __device__ __forceinline__ ChainUnit unit_of(int2 info, int u, int H) {
   return x;
 }
 
+// threadIdx.x as a value the compiler cannot see through: lane addresses
+// derived from it are formed where each side of the backward runs, not
+// hoisted out of the one-launch backward's unit loop (where those of every
+// phase would be live at once: up to 128 bytes of spills per lane).
+__device__ __forceinline__ int opaque_tid() {
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"(static_cast<int>(threadIdx.x)));
+  return t;
+}
+
 // A unit's rows 0 .. 16 nb - 1 (chain rows of head h) of tensors A and B,
 // fetched into registers and then stored into the LDS tiles As and Bs;
-// with kTabs also lse * log2(e) and δ of those rows (key side). Rows past
+// with kTabs also lse * log2(e) of those rows (key side), and with
+// kTabs == kLseDelta their δ too (kLseOnly: δ is already in LDS). Rows past
 // the chain repeat its last row (finite values that the masks give zero
 // weight), so every load is unconditional and in bounds.
-template <bool kTabs>
+constexpr int kLseDelta = 1;
+constexpr int kLseOnly = 2;
+template <int kTabs>
 struct Rows {
   static constexpr int kPer = kRows * kPieces / kThreads;  // 4 rows of each tensor per thread
   u4 a[kPer], b[kPer];
@@ -96,8 +109,9 @@ struct Rows {
   __device__ __forceinline__ void fetch(const bf16_t* __restrict__ A, const bf16_t* __restrict__ B,
                                         const float* __restrict__ lse, const float* __restrict__ Dl,
                                         const ChainUnit& x, int D, int H) {
-    const int r0 = static_cast<int>(threadIdx.x) / kPieces;
-    const int col = (threadIdx.x % kPieces) * 8;
+    const int tid = opaque_tid();
+    const int r0 = tid / kPieces;
+    const int col = (tid % kPieces) * 8;
     const bf16_t* Au = A + x.at(D);
     const bf16_t* Bu = B + x.at(D);
 #pragma unroll
@@ -106,15 +120,16 @@ struct Rows {
       a[k] = *reinterpret_cast<const u4*>(Au + o);
       b[k] = *reinterpret_cast<const u4*>(Bu + o);
     }
-    if constexpr (kTabs) {
-      const unsigned o = static_cast<unsigned>(min(static_cast<int>(threadIdx.x), x.L - 1) * H);
+    if constexpr (kTabs != 0) {
+      const unsigned o = static_cast<unsigned>(min(tid, x.L - 1) * H);
       rl = lse[x.tab(H) + o];
-      rd = Dl[x.tab(H) + o];
+      if constexpr (kTabs == kLseDelta) rd = Dl[x.tab(H) + o];
     }
   }
   __device__ __forceinline__ void store(bf16_t* As, bf16_t* Bs, float* l2s, float* dls, const ChainUnit& x) const {
-    const int r0 = static_cast<int>(threadIdx.x) / kPieces;
-    const int col = (threadIdx.x % kPieces) * 8;
+    const int tid = opaque_tid();
+    const int r0 = tid / kPieces;
+    const int col = (tid % kPieces) * 8;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int r = r0 + k * (kThreads / kPieces);
@@ -123,10 +138,10 @@ struct Rows {
         *reinterpret_cast<u4*>(Bs + r * WS + col) = b[k];
       }
     }
-    if constexpr (kTabs) {
-      if (static_cast<int>(threadIdx.x) < kRows) {
-        l2s[threadIdx.x] = rl * kLog2e;
-        dls[threadIdx.x] = rd;
+    if constexpr (kTabs != 0) {
+      if (tid < kRows) {
+        l2s[tid] = rl * kLog2e;
+        if constexpr (kTabs == kLseDelta) dls[tid] = rd;
       }
     }
   }
@@ -147,7 +162,7 @@ __device__ __forceinline__ int dealt_unit(int k) {
 // measured: with two workgroups per CU one's compute already covers the
 // other's loads, and the registers they took cost the backward kernels
 // more than they saved.)
-template <bool kTabs, typename PlanT, typename Body>
+template <int kTabs, typename PlanT, typename Body>
 __device__ __forceinline__ void unit_loop(const PlanT& pl, int H, const bf16_t* __restrict__ A,
                                           const bf16_t* __restrict__ B, const float* __restrict__ lse,
                                           const float* __restrict__ Dl, bf16_t* As, bf16_t* Bs, float* l2s,
@@ -195,7 +210,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;  // bf16 scores come unscaled
-  unit_loop<false>(pl, H, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
+  unit_loop<0>(pl, H, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
                    [&](const ChainUnit& x) {
     // The wave's blocks, costliest first: at most two (nb <= 16, eight
     // waves). Both blocks' Q slices are requested at once, so the second's
@@ -293,44 +308,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 // Backward, query side: δ and dQ in one pass over key blocks 0 .. i, as the
 // deep dQ kernel does (batched_depth_backward.cr:637-646 for δ): with
 // a_j = w_j dw_j, dQ = scale (Σ_j a_j k_j − δ Σ_j w_j k_j), δ = Σ_j a_j; the
-// bf16 operands a_j and w_j enter as high and low bf16 parts. δ goes to Dl
-// [T, H] for the key side; dQ gets the inverse rotation at the query's depth.
+// bf16 operands a_j and w_j enter as high and low bf16 parts. dQ gets the
+// inverse rotation at the query's depth.
 // ---------------------------------------------------------------------------
-template <typename PlanT, typename RopeT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_q_kernel(PlanT pl, const bf16_t* __restrict__ Q,
-                                                         const bf16_t* __restrict__ K,
-                                                         const bf16_t* __restrict__ V,
-                                                         const float* __restrict__ lse,
-                                                         const bf16_t* __restrict__ dO, float* __restrict__ dQ,
-                                                         float* __restrict__ Dl, RopeT rope, int H, float scale) {
+// The query side of unit x (its K, V rows in Ks, Vs): this wave's query
+// blocks. δ, for the key side, goes to Dl [T, H] and/or to the unit's LDS
+// table dls, where non-null.
+template <bool kAhead, typename RopeT>
+__device__ __forceinline__ void q_side(const ChainUnit& x, const bf16_t* Ks, const bf16_t* Vs,
+                                       const bf16_t* __restrict__ Q, const float* __restrict__ lse,
+                                       const bf16_t* __restrict__ dO, float* __restrict__ dQ,
+                                       float* __restrict__ Dl, float* dls, const RopeT& rope, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  extern __shared__ __align__(16) unsigned char dyn[];
-  bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
-  bf16_t* Vs = Ks + kRows * WS;
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int tid = opaque_tid();
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;
-  unit_loop<false>(pl, H, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr,
-                   [&](const ChainUnit& x) {
-    // The wave's (at most two) blocks, costliest first, with both blocks'
-    // Q and dO slices and lse requested at once.
+  {
+    // The wave's (at most two) blocks, costliest first; with kAhead both
+    // blocks' Q and dO slices and lse are requested at once (16 more
+    // registers: the one-launch backward loads the second block's after the
+    // first block instead).
     const int iA = snake_block(0, wave, x.nb, false);
     if (iA < 0) return;
     const int iB = snake_block(1, wave, x.nb, false);
     struct QIn {
       Slice<bf16_t, KD> qf, gf;
       float ls;
-    } in[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int qr = min(kBlk * (e ? max(iB, 0) : iA) + c, x.L - 1);
-      in[e].qf.load(Q + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
-      in[e].gf.load(dO + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
-      in[e].ls = lse[x.tab(H) + static_cast<unsigned>(qr * H)];
-    }
+    } in[kAhead ? 2 : 1];
+    auto load_in = [&](QIn& d, int i) {
+      const int qr = min(kBlk * i + c, x.L - 1);
+      d.qf.load(Q + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
+      d.gf.load(dO + x.at(D) + static_cast<unsigned>(qr * D + KD * g));
+      d.ls = lse[x.tab(H) + static_cast<unsigned>(qr * H)];
+    };
+    load_in(in[0], iA);
+    if constexpr (kAhead) load_in(in[kAhead ? 1 : 0], max(iB, 0));
     auto block = [&](int i, const QIn& qin) {
       const int q = kBlk * i + c;
       const Slice<bf16_t, KD>& qf = qin.qf;
@@ -386,11 +402,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
           if (rope.cos_t) agpt_fast::rope_inverse_part<4, kHD>(v, rope.cos_t, rope.sin_t, pos, kBlk * j + 4 * g);
           store_vec<4>(dQ + x.at(D) + static_cast<unsigned>(q * D + kBlk * j + 4 * g), v);
         }
-        if (g == 0) Dl[x.tab(H) + static_cast<unsigned>(q * H)] = dl;
+        if (g == 0) {
+          if (Dl) Dl[x.tab(H) + static_cast<unsigned>(q * H)] = dl;
+          if (dls) dls[q] = dl;
+        }
       }
     };
     block(iA, in[0]);
-    if (iB >= 0) block(iB, in[1]);
+    if (iB >= 0) {
+      if constexpr (kAhead) {
+        block(iB, in[kAhead ? 1 : 0]);
+      } else {
+        load_in(in[0], iB);
+        block(iB, in[0]);
+      }
+    }
+  }
+}
+
+template <typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_q_kernel(PlanT pl, const bf16_t* __restrict__ Q,
+                                                         const bf16_t* __restrict__ K,
+                                                         const bf16_t* __restrict__ V,
+                                                         const float* __restrict__ lse,
+                                                         const bf16_t* __restrict__ dO, float* __restrict__ dQ,
+                                                         float* __restrict__ Dl, RopeT rope, int H, float scale) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  bf16_t* Ks = reinterpret_cast<bf16_t*>(dyn);
+  bf16_t* Vs = Ks + kRows * WS;
+  unit_loop<0>(pl, H, K, V, nullptr, nullptr, Ks, Vs, nullptr, nullptr, [&](const ChainUnit& x) {
+    q_side<true>(x, Ks, Vs, Q, lse, dO, dQ, Dl, nullptr, rope, H, scale);
   });
 }
 
@@ -402,25 +443,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 // leaves out the softmax scale, applied once per key (a power of two at
 // head_dim 64, so the bf16 rounding is unchanged).
 // ---------------------------------------------------------------------------
-template <typename PlanT, typename RopeT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kv_kernel(
-    PlanT pl, const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
-    const float* __restrict__ lse, const float* __restrict__ Dl, const bf16_t* __restrict__ dO,
-    float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ acc_dk,
-    const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+// The key side of unit x (its Q, dO rows in Qs, Gs, lse * log2(e) and δ
+// of those rows in l2s, dls): this wave's key blocks.
+template <typename RopeT>
+__device__ __forceinline__ void kv_side(const ChainUnit& x, const bf16_t* Qs, const bf16_t* Gs, const float* l2s,
+                                        const float* dls, const bf16_t* __restrict__ K,
+                                        const bf16_t* __restrict__ V, float* __restrict__ dK,
+                                        float* __restrict__ dV, const float* __restrict__ acc_dk,
+                                        const float* __restrict__ acc_dv, const RopeT& rope, int H, float scale) {
   constexpr int KD = kHD / 4;
   constexpr int MT = kHD / 16;
-  __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (past the end: the last row's)
-  __shared__ alignas(16) float dls[kRows];  // δ of the chain's rows
-  extern __shared__ __align__(16) unsigned char dyn[];
-  bf16_t* Qs = reinterpret_cast<bf16_t*>(dyn);
-  bf16_t* Gs = Qs + kRows * WS;
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(static_cast<int>(threadIdx.x >> 6));
+  const int tid = opaque_tid();
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int D = H * kHD;
   const float sfac = scale * kLog2e;
-  unit_loop<true>(pl, H, Q, dO, lse, Dl, Qs, Gs, l2s, dls, [&](const ChainUnit& x) {
+  {
     for (int k = 0;; ++k) {
       const int j = snake_block(k, wave, x.nb, true);
       if (j < 0) break;
@@ -500,7 +539,80 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
       }
     }
+  }
+}
+
+template <typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kv_kernel(
+    PlanT pl, const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
+    const float* __restrict__ lse, const float* __restrict__ Dl, const bf16_t* __restrict__ dO,
+    float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ acc_dk,
+    const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+  __shared__ alignas(16) float l2s[kRows];  // lse * log2(e) of the chain's rows (past the end: the last row's)
+  __shared__ alignas(16) float dls[kRows];  // δ of the chain's rows
+  extern __shared__ __align__(16) unsigned char dyn[];
+  bf16_t* Qs = reinterpret_cast<bf16_t*>(dyn);
+  bf16_t* Gs = Qs + kRows * WS;
+  unit_loop<kLseDelta>(pl, H, Q, dO, lse, Dl, Qs, Gs, l2s, dls, [&](const ChainUnit& x) {
+    kv_side(x, Qs, Gs, l2s, dls, K, V, dK, dV, acc_dk, acc_dv, rope, H, scale);
   });
+}
+
+// ---------------------------------------------------------------------------
+// Backward in one launch: per unit the query side (dQ, δ) over the chain's
+// K, V rows in LDS, then the key side (dK, dV) over its Q, dO rows in the
+// same LDS, with δ handed over in LDS. The key side's rows are fetched as
+// each wave finishes its query blocks, and stored once every wave has.
+// Each key's dK/dV needs the δ of every later row of its chain, which the
+// unit has just computed: no δ table in HBM, no second launch, and no
+// drain between the two halves (the next unit's query side follows the key
+// side's tail on the CU). Results are bitwise those of bwd_q_kernel then
+// bwd_kv_kernel.
+// ---------------------------------------------------------------------------
+template <typename PlanT, typename RopeT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void bwd_kernel(
+    PlanT pl, const bf16_t* __restrict__ Q, const bf16_t* __restrict__ K, const bf16_t* __restrict__ V,
+    const float* __restrict__ lse, const bf16_t* __restrict__ dO, float* __restrict__ dQ,
+    float* __restrict__ dK, float* __restrict__ dV, const float* __restrict__ acc_dk,
+    const float* __restrict__ acc_dv, RopeT rope, int H, float scale) {
+  __shared__ alignas(16) float l2s[kRows];
+  __shared__ alignas(16) float dls[kRows];
+  extern __shared__ __align__(16) unsigned char dyn[];
+  bf16_t* As = reinterpret_cast<bf16_t*>(dyn);  // K then Q rows
+  bf16_t* Bs = As + kRows * WS;                 // V then dO rows
+  const int D = H * kHD;
+  const int64_t n_units = static_cast<int64_t>(pl.n_chains) * H;
+  int k = 0;
+  int u = dealt_unit(0);
+  int2 info = load_info(pl, u, H, n_units);
+  while (u < n_units) {
+    const int nu = dealt_unit(++k);
+    const ChainUnit x = unit_of(info, u, H);
+    {
+      Rows<0> rows;
+      rows.fetch(K, V, nullptr, nullptr, x, D, H);
+      rows.store(As, Bs, nullptr, nullptr, x);
+    }
+    const int2 ni = load_info(pl, nu, H, n_units);
+    __syncthreads();
+    q_side<false>(x, As, Bs, Q, lse, dO, dQ, nullptr, dls, rope, H, scale);
+    // (the scheduler would hoist the key side's row loads into the query
+    // side, whose registers are already full)
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      Rows<kLseOnly> rows;
+      rows.fetch(Q, dO, lse, nullptr, x, D, H);
+      __syncthreads();  // every wave is done with the K, V rows; δ of rows < L is in dls
+      const int t = opaque_tid();
+      if (t >= x.L && t < kRows) dls[t] = 0.0f;  // past the end: finite, and masked to zero weight
+      rows.store(As, Bs, l2s, nullptr, x);
+    }
+    __syncthreads();
+    kv_side(x, As, Bs, l2s, dls, K, V, dK, dV, acc_dk, acc_dv, rope, H, scale);
+    __syncthreads();  // the unit's rows are no longer read
+    u = nu;
+    info = ni;
+  }
 }
 
 }  // namespace agpt_chain

@@ -827,7 +827,7 @@ def main() -> int:
     desc = parts[0].describe()
     split = "split backward" in desc
     carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce
-    by_range = "subtree range" in desc  # the key side leaves nothing to reduce
+    by_range = "subtree range" in desc or "nothing to reduce" in desc  # no reduction kernel
     names = (["trie_fwd", "trie_bwd_q", "trie_bwd_kv"] if split else ["trie_fwd", "trie_bwd"])
     tail = [] if by_range else ["trie_bwd_carry"] if carry else ["trie_bwd_chunk", "trie_bwd_reduce"]
     k_ms = {n: [] for n in names + tail}

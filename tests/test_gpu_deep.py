@@ -11,7 +11,8 @@ with the tuning overrides: 4 heads per forward unit (the C4 forward), 8 per
 dQ unit (the C4 dQ kernel), key-side chunks of 96 tiles with the register
 carry, tile-order claims (by XCD ranges, and from one counter); plus the
 carry rows without registers, short chunks and the whole-key-set kernels.
-C5's chains run on the dense-causal chain kernels; with AGPT_ATTN_CHAIN=0
+C5's chains run on the dense-causal chain kernels (the backward in one
+launch; AGPT_ATTN_CHAINFUSE=0 keeps two); with AGPT_ATTN_CHAIN=0
 they take the general kernels, whose key side runs by subtree range unless
 AGPT_ATTN_RANGE=0 sends it through the carry. The oracle
 runs once per case.
@@ -43,10 +44,11 @@ DEEP_SHAPES = {
     "one_claim_counter_tile_order": {"AGPT_ATTN_XCD": "0", "AGPT_ATTN_LPT": "0", "AGPT_ATTN_DHPU": "4"},
     "key_side_carry_not_subtree_range": {"AGPT_ATTN_RANGE": "0", "AGPT_ATTN_CHAIN": "0"},
     "general_kernels_not_chain_kernels": {"AGPT_ATTN_CHAIN": "0"},
+    "chain_kernels_two_launch_backward": {"AGPT_ATTN_CHAINFUSE": "0"},
 }
 _KNOBS = ("AGPT_ATTN_VARIANT", "AGPT_ATTN_DHPU", "AGPT_ATTN_CHUNK", "AGPT_ATTN_LPT", "AGPT_ATTN_REGCARRY",
           "AGPT_ATTN_DEEP", "AGPT_ATTN_CARRY", "AGPT_ATTN_HG", "AGPT_ATTN_REGITERS", "AGPT_ATTN_DQ1",
-          "AGPT_ATTN_XCD", "AGPT_ATTN_RANGE", "AGPT_ATTN_CHAIN")
+          "AGPT_ATTN_XCD", "AGPT_ATTN_RANGE", "AGPT_ATTN_CHAIN", "AGPT_ATTN_CHAINFUSE")
 
 _CASES: dict = {}
 

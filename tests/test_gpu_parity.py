@@ -34,6 +34,7 @@ VARIANTS = {
     "block_deep_claims_in_tile_order": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_LPT": "0"},
     "block_deep_key_side_carry_only": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_RANGE": "0"},
     "block_deep_no_chain_kernels": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHAIN": "0"},
+    "block_deep_chain_two_launch_backward": {"AGPT_ATTN_VARIANT": "6", "AGPT_ATTN_CHAINFUSE": "0"},
     "chain": {"AGPT_ATTN_VARIANT": "5"},
     "chain_hg1_qb1_kb1": {"AGPT_ATTN_VARIANT": "5", "AGPT_ATTN_HG": "1", "AGPT_ATTN_QB": "1",
                           "AGPT_ATTN_KB": "1"},
@@ -51,7 +52,7 @@ def variant(request, monkeypatch):
               "AGPT_ATTN_KSLOTS", "AGPT_ATTN_UH", "AGPT_ATTN_CHUNK", "AGPT_ATTN_FUSED",
               "AGPT_ATTN_FHG", "AGPT_ATTN_CARRY", "AGPT_ATTN_FUH", "AGPT_ATTN_DEEP", "AGPT_ATTN_DHPU",
               "AGPT_ATTN_REGCARRY", "AGPT_ATTN_LPT", "AGPT_ATTN_REGITERS", "AGPT_ATTN_DQ1", "AGPT_ATTN_XCD",
-              "AGPT_ATTN_RANGE", "AGPT_ATTN_CHAIN"):
+              "AGPT_ATTN_RANGE", "AGPT_ATTN_CHAIN", "AGPT_ATTN_CHAINFUSE"):
         monkeypatch.delenv(k, raising=False)
     for k, v in VARIANTS[request.param].items():
         monkeypatch.setenv(k, v)
