@@ -14,7 +14,9 @@ carry rows without registers, short chunks and the whole-key-set kernels.
 C5's chains run on the dense-causal chain kernels (the backward in one
 launch; AGPT_ATTN_CHAINFUSE=0 keeps two); with AGPT_ATTN_CHAIN=0
 they take the general kernels, whose key side runs by subtree range unless
-AGPT_ATTN_RANGE=0 sends it through the carry. The oracle
+AGPT_ATTN_RANGE=0 sends it through the carry. A forest of 200 chains of
+1..256 rows at 4 heads has more (chain, head) units than the chain kernels'
+grid, so their snake deal gives workgroups a second round. The oracle
 runs once per case.
 
 Bar (bf16 inputs): 2e-2 relative + 2e-3 absolute, elementwise; an element
@@ -22,6 +24,8 @@ outside it must be within the same bar relative to the sum of its terms'
 magnitudes (helpers.assert_close_terms), and such elements are counted.
 """
 from __future__ import annotations
+
+import types
 
 import numpy as np
 import pytest
@@ -71,9 +75,21 @@ def _case(name):
     if name == "C4":
         tr = trie.config_trie("C4", scale=0.00008)  # 400 tokens: 34.6K node-tokens, depth 128
         H, hd, seed = 8, 64, 40
-    else:
+    elif name == "C5":
         tr = trie.config_trie("C5", scale=16 / 512)  # 16 chains of 256
         H, hd, seed = 4, 64, 50
+    else:
+        # 200 chains of 1..256 rows at C5's 4 heads: 800 (chain, head) units,
+        # more than a grid of two chain workgroups per CU holds on 256 CUs,
+        # so workgroups take units in a second round of the snake deal.
+        rng = np.random.default_rng(60)
+        parts, n = [], 0
+        for L in rng.integers(1, 257, size=200):
+            parts.append(np.concatenate([[-1], np.arange(n, n + int(L) - 1)]))
+            n += int(L)
+        parent = np.concatenate(parts).astype(np.int32)
+        tr = types.SimpleNamespace(parent=parent, n_nodes=int(parent.shape[0]))
+        H, hd, seed = 4, 64, 60
     T, D = tr.n_nodes, H * hd
     Q, K, V, G = (round_bf16(x) for x in tensors(T, D, seed))
     rng = np.random.default_rng(seed + 1)
@@ -100,7 +116,7 @@ def _compare(c, got):
         assert_close_terms(x, want, terms(name), RTOL_BF16, ATOL_BF16, name)
 
 
-@pytest.mark.parametrize("name", ["C4", "C5"])
+@pytest.mark.parametrize("name", ["C4", "C5", "chains_two_rounds"])
 def test_deep_config_sample(gpu, shape, name):
     """The whole sample as one plan, at the config's head count."""
     c = _case(name)
