@@ -707,6 +707,10 @@ def main() -> int:
     ap.add_argument("--full", action="store_true",
                     help="attn path: build the trie one root-child subtree at a time and run it batch "
                          "by batch (for a corpus whose trie does not fit one GPU, e.g. C4 at --scale 1)")
+    ap.add_argument("--events-after", action="store_true",
+                    help="attn path: time the steps without the per-kernel HIP events and take the "
+                         "kernel times from as many steps again (default with one batch: the events "
+                         "ride along in the timed steps)")
     ap.add_argument("--cpu-rows", type=int, default=250_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -808,22 +812,26 @@ def main() -> int:
         log(f"warmup step {i + 1}/{args.warmup} done")
 
     hev = HipEvents()
-    # The timed steps run without per-kernel events (7 event records per
-    # batch are work of their own on the stream: ~10 us per step, which a
-    # sub-millisecond C5 step shows); the per-kernel times come from as many
-    # steps again with the events, outside the timed region.
+    # One batch: the per-kernel events ride along in the timed steps, on the
+    # library's stream. Many batches, or --events-after: the timed steps run
+    # without them (7 event records per batch are work of their own on the
+    # stream, ~20 us per step, which a sub-millisecond C5 step shows) and
+    # the per-kernel times come from as many steps again with the events,
+    # outside the timed region.
+    events_in_timed = len(parts) == 1 and not args.events_after
     ev_steps = args.steps
     evs = [[(hev.create(2), hev.create(5)) for _ in parts] for _ in range(ev_steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(None)
+        step(evs[i] if events_in_timed else None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps: {elapsed:.3f}s")
-    for i in range(ev_steps):
-        step(evs[i])
-    torch.cuda.synchronize()
+    if not events_in_timed:
+        for i in range(ev_steps):
+            step(evs[i])
+        torch.cuda.synchronize()
     desc = parts[0].describe()
     split = "split backward" in desc
     carry = "path-carry" in desc  # one reduction kernel (chunk partials) instead of chunk + reduce
@@ -888,6 +896,8 @@ def main() -> int:
             "max_depth": tr.max_depth, "d_model": D, "heads": H, "head_dim": hd,
             "corpus_scale": args.scale, "tiles": info["n_tiles"], "batching": batching,
             "kernel": desc,
+            "kernel_events": ("HIP events around each kernel in the timed steps" if events_in_timed else
+                              "HIP events around each kernel in as many steps after the timed ones"),
         },
         "roofline": {
             "bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS,
