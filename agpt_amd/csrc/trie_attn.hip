@@ -1294,7 +1294,8 @@ int plan_impl(agpt_attn_s* h, const int32_t* ext, int64_t n_ext, int32_t A0,
         if (parent[r] < 0) starts.push_back(static_cast<int32_t>(r));
         else chains = parent[r] == r - 1;
       }
-      if (chains) {
+      // (the chain kernels number their (chain, head) units in 32 bits)
+      if (chains && static_cast<int64_t>(starts.size()) * h->cfg.n_heads < (int64_t{1} << 31) - 2 * 65536) {
         const int32_t nc = static_cast<int32_t>(starts.size());
         starts.push_back(static_cast<int32_t>(n));
         std::vector<int32_t> order(nc);
