@@ -1899,23 +1899,24 @@ void launch_bwd(const agpt_attn_s* h, const void* q, const void* k, const void* 
         return;
       }
       if (h->deep_carry) {
-        // Key slots of a tile: prefix_cap + 64. The first 4 kRegItersDeep
-        // blocks of 16 keep their sums in registers, the rest in the carry
-        // rows. AGPT_ATTN_REGITERS=3 keeps every slot of a plan to depth 128
-        // in 4 kRegIters blocks instead; at 256 VGPRs that spills 256 bytes
-        // per lane inside the key-block loop, and C4's key side ran 0.75 ms
-        // slower (28.5 vs 27.8 ms).
+        // Key slots of a tile: prefix_cap + 64. A plan to depth 128 keeps
+        // every slot's sums in registers (4 kRegIters blocks of 16) and, in
+        // bf16, each slot's K/V slices in an LDS cache tagged by row;
+        // deeper plans (or AGPT_ATTN_REGITERS=2) keep the first 4
+        // kRegItersDeep blocks in registers and the rest in the carry rows.
         const bool regs = env_int("AGPT_ATTN_REGCARRY", 1) != 0;
         const bool all_regs = agpt_blk::prefix_cap(h->max_depth) + agpt_deep::kTile <= 64 * agpt_deep::kRegIters &&
-                              env_int("AGPT_ATTN_REGITERS", agpt_deep::kRegItersDeep) == agpt_deep::kRegIters;
+                              env_int("AGPT_ATTN_REGITERS", agpt_deep::kRegIters) == agpt_deep::kRegIters;
         auto fc = !regs      ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, 0, PlanDev, RopeArgs>
                   : all_regs ? agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegIters, PlanDev, RopeArgs>
                              : agpt_deep::bwd_kv_carry_kernel<HD, Tin, agpt_deep::kRegItersDeep, PlanDev, RopeArgs>;
-        set_lds(fc, h->kv_lds);
+        const size_t lds =
+            h->kv_lds + agpt_deep::kv_cache_bytes(regs && all_regs ? agpt_deep::kRegIters : 0, sizeof(Tin));
+        set_lds(fc, lds);
         int cus = 256;
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, h->device);
-        const int grid = std::max(1, std::min(wg_per_cu(fc, h->kv_lds, h->max_lds) * cus, h->cs_slots));
-        hipLaunchKernelGGL(fc, dim3(grid), dim3(agpt_deep::kThreads), h->kv_lds, st, plan_dev(h),
+        const int grid = std::max(1, std::min(wg_per_cu(fc, lds, h->max_lds) * cus, h->cs_slots));
+        hipLaunchKernelGGL(fc, dim3(grid), dim3(agpt_deep::kThreads), lds, st, plan_dev(h),
                            static_cast<const Tin*>(q), static_cast<const Tin*>(k), static_cast<const Tin*>(v), lse,
                            h->d_Dl, static_cast<const Tin*>(dO), dk, dv, h->d_E, h->d_F, h->d_Cs, acc_dk, acc_dv,
                            rope, h->cfg.n_heads, scale);

@@ -30,6 +30,7 @@ using agpt_blk::slice_dot;
 using agpt_deep::kNoMax;
 using agpt_deep::mfma_a_bf16;
 using agpt_deep::mfma_a2_bf16;
+using agpt_deep::opaque_tid;
 using agpt_deep::read_tr;
 using agpt_fast::f4;
 using agpt_fast::u4;
@@ -80,16 +81,6 @@ __device__ __forceinline__ ChainUnit unit_of(int2 info, int u, int H) {
   x.nb = (x.L + kBlk - 1) / kBlk;
   x.h = u % H;
   return x;
-}
-
-// threadIdx.x as a value the compiler cannot see through: lane addresses
-// derived from it are formed where each side of the backward runs, not
-// hoisted out of the one-launch backward's unit loop (where those of every
-// phase would be live at once: up to 128 bytes of spills per lane).
-__device__ __forceinline__ int opaque_tid() {
-  int t;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"(static_cast<int>(threadIdx.x)));
-  return t;
 }
 
 // A unit's rows 0 .. 16 nb - 1 (chain rows of head h) of tensors A and B,

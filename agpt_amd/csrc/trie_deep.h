@@ -1157,6 +1157,38 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof
   }
 }
 
+// The key side's K/V slice cache (bf16, every key slot in registers: NI ==
+// kRegIters): per wave and register block, four 16-byte pieces per lane.
+__host__ __device__ constexpr size_t kv_cache_bytes(int ni, int elem) {
+  return ni == kRegIters && elem == 2 ? static_cast<size_t>(kThreads / 64) * kRegIters * 4 * 64 * 16 : 0;
+}
+static_assert(rows_lds_bytes(64, 2) % 16 == 0 && RawTabs::kBytes % 16 == 0, "16-byte aligned cache entries");
+// A 16-dim bf16 slice from / to two 16-byte pieces.
+template <typename S>
+__device__ __forceinline__ void slice_set(S& s, u4 lo, u4 hi) {
+  s.w[0] = lo.x;
+  s.w[1] = lo.y;
+  s.w[2] = lo.z;
+  s.w[3] = lo.w;
+  s.w[4] = hi.x;
+  s.w[5] = hi.y;
+  s.w[6] = hi.z;
+  s.w[7] = hi.w;
+}
+template <typename S>
+__device__ __forceinline__ void slice_put(const S& s, u4& lo, u4& hi) {
+  lo = u4{s.w[0], s.w[1], s.w[2], s.w[3]};
+  hi = u4{s.w[4], s.w[5], s.w[6], s.w[7]};
+}
+// threadIdx.x through an opaque move: lane addresses derived from it are
+// formed where they are used, not hoisted out of the loops (where they
+// would hold registers across the whole unit).
+__device__ __forceinline__ int opaque_tid() {
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"(static_cast<int>(threadIdx.x)));
+  return t;
+}
+
 // ---------------------------------------------------------------------------
 // Key side with a path carry. A unit is (chunk of consecutive tiles, head);
 // the workgroup walks the chunk's tiles in order. The keys a tile leaves
@@ -1206,6 +1238,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
   Tin* Qs = reinterpret_cast<Tin*>(dyn);
   Tin* Gs = Qs + kTile * WS;
   const RawTabs raw{reinterpret_cast<int32_t*>(dyn + rows_lds_bytes(HD, sizeof(Tin)))};
+  constexpr bool kCache = kv_cache_bytes(NI, sizeof(Tin)) > 0;
+  u4* const kvc = reinterpret_cast<u4*>(dyn + rows_lds_bytes(HD, sizeof(Tin)) + RawTabs::kBytes) +
+                  (kCache ? (threadIdx.x >> 6) * NI * 4 * 64 : 0);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
@@ -1234,9 +1269,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
     auto fetch_rows = [&](int t) {
       const int64_t s = static_cast<int64_t>(t) * kTile;
       const int last = static_cast<int>(min(static_cast<int64_t>(kTile), pl.T - s)) - 1;
+      const int tid = opaque_tid();
 #pragma unroll
       for (int k = 0; k < RPER; ++k) {
-        const int j = static_cast<int>(threadIdx.x) + k * kThreads;
+        const int j = tid + k * kThreads;
         const int64_t off = (s + min(j / PIECES, last)) * D + h * HD + (j % PIECES) * EPC;
         rq[k] = *reinterpret_cast<const u4*>(Q + off);
         rg[k] = *reinterpret_cast<const u4*>(dO + off);
@@ -1251,6 +1287,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
     // Carry registers: the sums of key block wave + 4i (i < NI), one lane
     // column per key slot; zero in the lanes of keys that do not continue.
     constexpr int NR = NI > 0 ? NI : 1;
+    // With every key slot in registers (bf16), each lane also keeps the K
+    // and V slices of its key in each of its blocks in LDS, tagged with the
+    // key's row: a key that stays in its slot from tile to tile (a prefix
+    // key of consecutive tiles, a chain row) is loaded from HBM once per
+    // chunk instead of once per tile. Entry (wave, turn i): four 16-byte
+    // pieces (K low, K high, V low, V high) of 64 lanes each.
+    // No entry yet: a tag no key takes (a range plan's context rows sit at
+    // negative rows before the range, down to -(its depth)).
+    int crow[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) crow[i] = INT32_MIN;
     f4 ck[NR][MT], cv[NR][MT];
 #pragma unroll
     for (int i = 0; i < NR; ++i)
@@ -1292,6 +1339,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
       const int s = w.s, ntile = w.ntile, A = w.A;
       const int nkb = (A + ntile + kBlk - 1) / kBlk;
       Slice<Tin, KD> kf, vf, nkf, nvf;
+      bool nmiss = false;  // the prefetched block's slices came from HBM (kCache)
       auto fetch = [&](int b, Slice<Tin, KD>& a, Slice<Tin, KD>& v) {
         const int64_t row = tb.krow[kBlk * b + c];
         a.load(K + row * D + h * HD + KD * g);
@@ -1301,10 +1349,42 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
       // registers of the block (the carried sums of its prefix keys, zero in
       // every other lane), which keep the sums that continue into the next
       // tile and are zero again in every other lane at the end.
-      auto key_block = [&](int b, f4 (&dk)[MT], f4 (&dv)[MT], bool reg) {
+      // The slices of key block b (turn i of this wave) through the cache:
+      // lanes whose key is the tagged row read LDS, the others HBM (their
+      // entries are written when the block is taken, kmiss).
+      auto fetch_c = [&](int b, int i, Slice<Tin, KD>& a, Slice<Tin, KD>& v, bool& miss) {
+        if constexpr (kCache) {
+          const int row = tb.krow[kBlk * b + c];
+          miss = row != crow[i];
+          if (miss) {
+            a.load(K + static_cast<int64_t>(row) * D + h * HD + KD * g);
+            v.load(V + static_cast<int64_t>(row) * D + h * HD + KD * g);
+            crow[i] = row;
+          } else {
+            const u4* e = kvc + i * 4 * 64 + lane;
+            const u4 x0 = e[0], x1 = e[64], y0 = e[128], y1 = e[192];
+            slice_set(a, x0, x1);
+            slice_set(v, y0, y1);
+          }
+        }
+      };
+      auto key_block = [&](int b, f4 (&dk)[MT], f4 (&dv)[MT], bool reg, int turn) {
+        int tid;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(static_cast<int>(threadIdx.x)));
+        const int lane = tid & 63;
+        const int g = lane >> 4, c = lane & 15;
         kf = nkf;
         vf = nvf;
-        if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
+        if constexpr (kCache) {
+          if (nmiss) {
+            u4* e = kvc + turn * 4 * 64 + lane;
+            slice_put(kf, e[0], e[64]);
+            slice_put(vf, e[128], e[192]);
+          }
+          if (b + 4 < nkb && turn + 1 < NR) fetch_c(b + 4, turn + 1, nkf, nvf, nmiss);
+        } else {
+          if (b + 4 < nkb) fetch(b + 4, nkf, nvf);
+        }
         kf.scale(qscale);
         const int key = kBlk * b + c;
         // The key's interval and the block's query range read together (the
@@ -1458,11 +1538,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
             }
         }
       };
-      if (wave < nkb) fetch(wave, nkf, nvf);
+      if (wave < nkb) {
+        if constexpr (kCache) fetch_c(wave, 0, nkf, nvf, nmiss);
+        else fetch(wave, nkf, nvf);
+      }
       if constexpr (NI == kRegIters) {  // every key block of the tile in registers
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-          if (wave + 4 * i < nkb) key_block(wave + 4 * i, ck[i], cv[i], true);
+          if (wave + 4 * i < nkb) key_block(wave + 4 * i, ck[i], cv[i], true, i);
       } else if constexpr (NI > 0) {
         // Deeper plans: the wave's first NI blocks in registers (selected by
         // the block's turn i, a uniform value), the blocks after them through
@@ -1480,7 +1563,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
               dv[j] = i == x ? cv[x][j] : dv[j];
             }
           }
-          key_block(b, dk, dv, i < NI);
+          key_block(b, dk, dv, i < NI, 0);
 #pragma unroll
           for (int x = 0; x < NI; ++x)
 #pragma unroll
@@ -1497,7 +1580,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
             dk[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             dv[j] = dk[j];
           }
-          key_block(b, dk, dv, false);
+          key_block(b, dk, dv, false, 0);
         }
       }
       a_prev = A;
