@@ -43,7 +43,7 @@ DEEP_SHAPES = {
     "chunk24_carry_rows_only": {"AGPT_ATTN_CHUNK": "24", "AGPT_ATTN_REGCARRY": "0"},
     "chunk2_one_head_units": {"AGPT_ATTN_CHUNK": "2", "AGPT_ATTN_DHPU": "1"},
     "whole_key_set": {"AGPT_ATTN_DEEP": "0"},
-    "carry_all_slots_in_registers_chunk96": {"AGPT_ATTN_REGITERS": "3", "AGPT_ATTN_CHUNK": "96"},
+    "carry_two_register_blocks_chunk96": {"AGPT_ATTN_REGITERS": "2", "AGPT_ATTN_CHUNK": "96"},
     "dq_delta_pass_then_dq": {"AGPT_ATTN_DQ1": "0"},
     "one_claim_counter_tile_order": {"AGPT_ATTN_XCD": "0", "AGPT_ATTN_LPT": "0", "AGPT_ATTN_DHPU": "4"},
     "key_side_carry_not_subtree_range": {"AGPT_ATTN_RANGE": "0", "AGPT_ATTN_CHAIN": "0"},
