@@ -166,6 +166,10 @@ __device__ __forceinline__ void unit_loop(const PlanT& pl, int H, const bf16_t* 
   while (u < n_units) {
     const int nu = dealt_unit(++k);
     const ChainUnit x = unit_of(info, u, H);
+    // The rows' loads, stores and barrier at a higher wave priority than the
+    // blocks, so they go out ahead of the other workgroup's block steps
+    // (forward 0.077-0.079 -> 0.074 ms).
+    __builtin_amdgcn_s_setprio(3);
     {
       Rows<kTabs> rows;
       rows.fetch(A, B, lse, Dl, x, D, H);
@@ -173,6 +177,7 @@ __device__ __forceinline__ void unit_loop(const PlanT& pl, int H, const bf16_t* 
     }
     const int2 ni = load_info(pl, nu, H, n_units);
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
     body(x);
     __syncthreads();  // the unit's rows are no longer read
     u = nu;
@@ -579,6 +584,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   while (u < n_units) {
     const int nu = dealt_unit(++k);
     const ChainUnit x = unit_of(info, u, H);
+    __builtin_amdgcn_s_setprio(3);  // rows and barriers ahead of block steps, as in unit_loop
     {
       Rows<0> rows;
       rows.fetch(K, V, nullptr, nullptr, x, D, H);
@@ -586,10 +592,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     const int2 ni = load_info(pl, nu, H, n_units);
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
     q_side<false>(x, As, Bs, Q, lse, dO, dQ, nullptr, dls, rope, H, scale);
     // (the scheduler would hoist the key side's row loads into the query
     // side, whose registers are already full)
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(3);
     {
       Rows<kLseOnly> rows;
       rows.fetch(Q, dO, lse, nullptr, x, D, H);
@@ -599,6 +607,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       rows.store(As, Bs, l2s, nullptr, x);
     }
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
     kv_side(x, As, Bs, l2s, dls, K, V, dK, dV, acc_dk, acc_dv, rope, H, scale);
     __syncthreads();  // the unit's rows are no longer read
     u = nu;
