@@ -426,6 +426,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
     // Step st is chunk ch of head h0 + hl; the counters advance at its end.
     int hl = 0, ch = 0;
     for (int st = 0; st < nsteps; ++st) {
+      __builtin_amdgcn_s_setprio(0);
       const int h = h0 + hl;
       const bool last = ch + 1 == w.nch;
       const int nxc = last ? 0 : ch + 1;
@@ -479,6 +480,9 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(PlanT pl, const Tin* __re
               o[j] = mfma16(ld1(Vs + (kBlk * bl + 4 * g + r) * WS + kBlk * j + c), p[r], o[j]);
         }
       }
+      // the next chunk's ring store and the step's barrier ahead of the
+      // other workgroups' products
+      __builtin_amdgcn_s_setprio(3);
       if (more) ring.store((st + 1) & 1);
       if (last) {
         if (q < w.ntile) {
@@ -624,6 +628,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kOnePa
     // of head h0 + hl; the counters advance at its end.
     int hl = 0, pass = NP == 2 ? 0 : 1, ch = 0;
     for (int st = 0; st < nsteps; ++st) {
+      __builtin_amdgcn_s_setprio(0);
       const int h = h0 + hl;
       const bool pend = ch + 1 == w.nch;  // the pass's last chunk
       const bool last = pend && pass == 1;  // the head's last step
@@ -695,6 +700,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kOnePa
         }
       }
       if (pass == 0 && ch + 1 == w.nch) dl = group_sum(acc);
+      // the next chunk's ring store and the step's barrier ahead of the
+      // other workgroups' products
+      __builtin_amdgcn_s_setprio(3);
       if (more) ring.store((st + 1) & 1);
       if (last) {
         if constexpr (kOnePass) {
@@ -1538,6 +1546,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
             }
         }
       };
+      __builtin_amdgcn_s_setprio(0);  // the key blocks at the base priority
       if (wave < nkb) {
         if constexpr (kCache) fetch_c(wave, 0, nkf, nvf, nmiss);
         else fetch(wave, nkf, nvf);
@@ -1584,6 +1593,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NI > 0
         }
       }
       a_prev = A;
+      // the tile's end and the next tile's tables, staging and barriers
+      // ahead of the other workgroup's key blocks
+      __builtin_amdgcn_s_setprio(3);
       wait_loads();     // the next tile's table inputs are in LDS
       __syncthreads();  // the tile's staged rows, tables and carry rows are done with
     }
