@@ -241,6 +241,10 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(
   fetch2(r0);
   for (;;) {
     const int n = static_cast<int>(min(static_cast<int64_t>(RB), T_q - r0));
+    // The run's moves between HBM and LDS and their barriers at a higher
+    // wave priority than the rows' arithmetic, so a workgroup moving its run
+    // gets ahead of the others' rows and waits less at its barriers.
+    __builtin_amdgcn_s_setprio(3);
     if (static_cast<int>(threadIdx.x) < n) {
       tab.tgt[threadIdx.x] = tg;
       tab.mw[threadIdx.x] = mwv;
@@ -252,6 +256,7 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(
     __syncthreads();
     const int64_t next = r0 + step;
     if (next < T_q) fetch(next);
+    __builtin_amdgcn_s_setprio(0);
     for (int r = grp; r < n; r += kGroups) {
       const int64_t q = r0 + r;
       float* row = buf + r * V;
@@ -341,6 +346,7 @@ __global__ __launch_bounds__(kThreads) void loss_kernel(
       if (c == 0) loss_out[q] = loss;
     }
     if (next < T_q) fetch2(next);  // its first level arrived during the rows above
+    __builtin_amdgcn_s_setprio(3);
     __syncthreads();
     store_run(d_logits, buf, r0 * V, (r0 + n) * V);
     if (next >= T_q) break;
