@@ -11,7 +11,10 @@
 // A block pair is masked only on the diagonal (key <= query inside the
 // block) and past the chain's end; rows past the end repeat the chain's last
 // row in LDS, so a masked pair never multiplies stale data. Each key's dK/dV and each
-// query's dQ is complete within its unit: no partials, no reduction.
+// query's dQ is complete within its unit: no partials, no reduction. The
+// backward runs both sides in one launch (bwd_kernel: per unit the query
+// side, then the key side in the same LDS); bwd_q_kernel + bwd_kv_kernel
+// are the two-launch form.
 //
 // Lane layouts and products are those of trie_deep.h: 16x16 blocks on the
 // bf16 matrix instructions, lane l = 16g + c.
